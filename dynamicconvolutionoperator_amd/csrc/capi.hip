@@ -1,0 +1,33 @@
+// Library-level C-ABI helpers: status strings, ABI version, support queries.
+#include "ddpm_common.h"
+
+using namespace ddpm;
+
+extern "C" int ddpm_abi_version(void) { return 1; }
+
+extern "C" const char* ddpm_status_string(int code) {
+  switch (code) {
+    case kOk:
+      return "ok";
+    case kBadArgument:
+      return "invalid argument (shape, kernel size, dilation, dtype or null pointer)";
+    case kUnsupported:
+      return "shape or kernel size not supported by this kernel";
+    case kWorkspaceTooSmall:
+      return "workspace missing or smaller than ddpm_gen_bwd_w_workspace_bytes()";
+    default:
+      return hipGetErrorString((hipError_t)code);
+  }
+}
+
+// 1 when the fused generator kernels (forward and recompute backward) handle
+// this channel count, kernel size and largest dilation, else 0 (the caller
+// then materializes the dynamic kernels and uses the ddpm_filter_* entry
+// points).  The forward's fp32 halo tile of (8+2R) x (32+2R) pixels x 16
+// channels, R = (K/2)*max_dilation, must fit 64 KB of LDS.
+extern "C" int ddpm_gen_supported(int64_t c, int kernel_size, int max_dilation) {
+  if (c < 1 || c > 64 || !(kernel_size == 1 || kernel_size == 3) || max_dilation < 1) return 0;
+  const int64_t r = (int64_t)(kernel_size / 2) * max_dilation;
+  const int64_t lds = (8 + 2 * r) * (32 + 2 * r) * 16 * 4 + 3 * kernel_size * kernel_size * 16 * 4;
+  return lds <= 64 * 1024 ? 1 : 0;
+}

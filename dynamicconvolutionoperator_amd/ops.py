@@ -1,0 +1,256 @@
+"""Operator-level API: ``fused_dynamic_cat`` and ``fused_generator_dynamic_cat``.
+
+Drop-in counterparts of the reference's operators
+(_triton_kernels.py:814-870 and :873-1065): same arguments, same output
+dtype rules and the same autograd outputs, backed by hand-written HIP kernels
+for gfx950 through the C-ABI in ``libddpm_hip.so``.
+
+* ``fused_dynamic_cat(x, kernels, kernel_size, dilations)`` -> ``[N, 4C, H, W]``
+  in ``kernels.dtype``; backward returns ``(dX, dK, None, None)``.
+* ``fused_generator_dynamic_cat(x, y, weight, bias, kernel_size, dilations)``
+  -> ``[N, 4C, H, W]`` in ``x.dtype``; backward recomputes the generator and
+  returns ``(dX, dY, dW, db, None, None)``; only ``x, y, weight, bias`` are
+  saved.
+
+All tensors are allocated by torch (so ``max_memory_allocated`` sees them);
+kernels run asynchronously on the current stream.  Tensors must be on a ROCm
+("cuda") device; nothing here runs on the CPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; expected float32, bfloat16 or float16") from None
+
+
+def _ptr(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _require_device(*tensors: torch.Tensor) -> None:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise ValueError(f"HIP operators need tensors on a ROCm device, got {dev}")
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise ValueError(f"all tensors must be on {dev}, got {t.device}")
+
+
+def _check_dilations(dilations) -> tuple[int, int, int]:
+    d = tuple(int(v) for v in dilations)
+    if len(d) != 3 or min(d) < 1:
+        raise ValueError(f"dilations must be three positive integers, got {dilations}")
+    return d
+
+
+def _check_kernel_size(kernel_size: int) -> int:
+    k = int(kernel_size)
+    if k < 1 or k % 2 == 0:
+        raise ValueError(f"kernel_size must be a positive odd integer, got {kernel_size}")
+    return k
+
+
+# ---------------------------------------------------------------------------
+# Materialized path: kernels given as [N, 3, C, K*K, H, W]
+# ---------------------------------------------------------------------------
+def _check_filter_inputs(x: torch.Tensor, kernels: torch.Tensor, k: int) -> None:
+    if x.ndim != 4:
+        raise ValueError(f"x must be NCHW, got shape {tuple(x.shape)}")
+    n, c, h, w = x.shape
+    if tuple(kernels.shape) != (n, 3, c, k * k, h, w):
+        raise ValueError(
+            f"kernels must have shape {(n, 3, c, k * k, h, w)}, got {tuple(kernels.shape)}"
+        )
+    _require_device(x, kernels)
+    _dt(x)
+    _dt(kernels)
+
+
+def _filter_call(fn_name: str, a, b, out, x_shape, k, dil, x_dtype: int, k_dtype: int):
+    lib = _lib.load()
+    n, c, h, w = x_shape
+    with torch.cuda.device(out.device):
+        code = getattr(lib, fn_name)(
+            _ptr(a), _ptr(b), _ptr(out), n, c, h, w, k, dil[0], dil[1], dil[2], x_dtype, k_dtype,
+            _stream(out),
+        )
+    _lib.check(code, fn_name)
+
+
+class _DynamicCat(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, kernels, kernel_size, dilations):
+        k = _check_kernel_size(kernel_size)
+        dil = _check_dilations(dilations)
+        x = x.contiguous()
+        kernels = kernels.contiguous()
+        _check_filter_inputs(x, kernels, k)
+        n, c, h, w = x.shape
+        out = torch.empty((n, 4 * c, h, w), dtype=kernels.dtype, device=x.device)
+        _filter_call("ddpm_filter_fwd", x, kernels, out, x.shape, k, dil, _dt(x), _dt(kernels))
+        ctx.save_for_backward(x, kernels)
+        ctx.kernel_size = k
+        ctx.dilations = dil
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, kernels = ctx.saved_tensors
+        grad_out = grad_out.to(kernels.dtype).contiguous()
+        grad_x = grad_k = None
+        if ctx.needs_input_grad[0]:
+            grad_x = torch.empty_like(x)
+            _filter_call("ddpm_filter_bwd_x", grad_out, kernels, grad_x, x.shape, ctx.kernel_size,
+                         ctx.dilations, _dt(x), _dt(kernels))
+        if ctx.needs_input_grad[1]:
+            grad_k = torch.empty_like(kernels)
+            _filter_call("ddpm_filter_bwd_k", x, grad_out, grad_k, x.shape, ctx.kernel_size,
+                         ctx.dilations, _dt(x), _dt(kernels))
+        return grad_x, grad_k, None, None
+
+
+def fused_dynamic_cat(x, kernels, kernel_size, dilations):
+    """``[x, d0, d1, d2]`` from materialized dynamic kernels (_triton_kernels.py:869-870)."""
+    return _DynamicCat.apply(x, kernels, kernel_size, dilations)
+
+
+# ---------------------------------------------------------------------------
+# Fused generator path
+# ---------------------------------------------------------------------------
+def generator_supported(channels: int, kernel_size: int, dilations=(1, 3, 5)) -> bool:
+    """Whether the fused generator kernels handle this shape (K in {1,3}, C <= 64,
+    halo tile within 64 KB of LDS)."""
+    return bool(_lib.load().ddpm_gen_supported(int(channels), int(kernel_size), int(max(dilations))))
+
+
+def _check_generator_inputs(x, y, weight, bias, k: int) -> None:
+    if x.ndim != 4 or y.shape != x.shape:
+        raise ValueError(f"x and y must be NCHW tensors of identical shapes, got {x.shape} and {y.shape}")
+    n, c, h, w = x.shape
+    g = 3 * c * k * k
+    if weight.numel() != g * c or weight.shape[0] != g:
+        raise ValueError(f"weight must have shape {(g, c, 1, 1)}, got {tuple(weight.shape)}")
+    if bias is None or tuple(bias.shape) != (g,):
+        raise ValueError(f"bias must have shape {(g,)}")
+    _require_device(x, y, weight, bias)
+    if not (x.dtype == y.dtype == weight.dtype == bias.dtype):
+        raise TypeError("x, y, weight and bias must share one dtype on the fused generator path")
+    _dt(x)
+
+
+def _launch_generator_dynamic_cat(x, y, weight, bias, k, dil):
+    x = x.contiguous()
+    y = y.contiguous()
+    weight = weight.contiguous()
+    bias = bias.contiguous()
+    _check_generator_inputs(x, y, weight, bias, k)
+    n, c, h, w = x.shape
+    out = torch.empty((n, 4 * c, h, w), dtype=x.dtype, device=x.device)
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        code = lib.ddpm_gen_fwd(
+            _ptr(x), _ptr(y), _ptr(weight), _ptr(bias), _ptr(out), n, c, h, w, k, *dil, _dt(x),
+            _stream(x),
+        )
+    _lib.check(code, "ddpm_gen_fwd")
+    return out
+
+
+class _GeneratorDynamicCat(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, y, weight, bias, kernel_size, dilations):
+        k = _check_kernel_size(kernel_size)
+        dil = _check_dilations(dilations)
+        x = x.contiguous()
+        y = y.contiguous()
+        weight = weight.contiguous()
+        bias = bias.contiguous()
+        out = _launch_generator_dynamic_cat(x, y, weight, bias, k, dil)
+        ctx.save_for_backward(x, y, weight, bias)
+        ctx.kernel_size = k
+        ctx.dilations = dil
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, y, weight, bias = ctx.saved_tensors
+        grad_out = grad_out.to(x.dtype).contiguous()
+        k, dil = ctx.kernel_size, ctx.dilations
+        n, c, h, w = x.shape
+        lib = _lib.load()
+        dt = _dt(x)
+        stream = _stream(x)
+        grad_x = grad_y = grad_w = grad_b = None
+        with torch.cuda.device(x.device):
+            if ctx.needs_input_grad[0]:
+                grad_x = torch.empty_like(x)
+                _lib.check(
+                    lib.ddpm_gen_bwd_x(_ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
+                                       _ptr(grad_x), n, c, h, w, k, *dil, dt, stream),
+                    "ddpm_gen_bwd_x",
+                )
+            if ctx.needs_input_grad[1]:
+                grad_y = torch.empty_like(y)
+                _lib.check(
+                    lib.ddpm_gen_bwd_y(_ptr(x), _ptr(weight), _ptr(grad_out), _ptr(grad_y), n, c,
+                                       h, w, k, *dil, dt, stream),
+                    "ddpm_gen_bwd_y",
+                )
+            if ctx.needs_input_grad[2] or ctx.needs_input_grad[3]:
+                grad_w = torch.empty_like(weight)
+                grad_b = torch.empty_like(bias)
+                ws_bytes = int(lib.ddpm_gen_bwd_w_workspace_bytes(n, c, h, w, k))
+                ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+                _lib.check(
+                    lib.ddpm_gen_bwd_w(_ptr(x), _ptr(y), _ptr(grad_out), _ptr(grad_w),
+                                       _ptr(grad_b), _ptr(ws), ws_bytes, n, c, h, w, k, *dil, dt,
+                                       stream),
+                    "ddpm_gen_bwd_w",
+                )
+                if not ctx.needs_input_grad[2]:
+                    grad_w = None
+                if not ctx.needs_input_grad[3]:
+                    grad_b = None
+        return grad_x, grad_y, grad_w, grad_b, None, None
+
+
+def _materialized_generator_dynamic_cat(x, y, weight, bias, k, dil):
+    n, c, h, w = x.shape
+    kernels = torch.nn.functional.conv2d(y, weight, bias).reshape(n, 3, c, k * k, h, w)
+    return fused_dynamic_cat(x, kernels, k, dil)
+
+
+def fused_generator_dynamic_cat(x, y, weight, bias, kernel_size, dilations):
+    """Generator + dynamic filter + concat (_triton_kernels.py:1056-1065).
+
+    Uses the autograd Function when grad is enabled and any input requires
+    grad, else a single forward launch.  Shapes outside the fused kernels'
+    coverage (K > 3 or C > 64) run the generator as a 1x1 convolution and the
+    HIP materialized filter, with the same result and autograd outputs.
+    """
+    k = _check_kernel_size(kernel_size)
+    dil = _check_dilations(dilations)
+    if not generator_supported(x.shape[1], k, dil):
+        return _materialized_generator_dynamic_cat(x, y, weight, bias, k, dil)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (x, y, weight, bias)):
+        return _GeneratorDynamicCat.apply(x, y, weight, bias, k, dil)
+    return _launch_generator_dynamic_cat(x, y, weight, bias, k, dil)
+
+
+__all__ = ["fused_dynamic_cat", "fused_generator_dynamic_cat", "generator_supported"]

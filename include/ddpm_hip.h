@@ -1,0 +1,117 @@
+/*
+ * ddpm_hip.h - C ABI of libddpm_hip.so, the MI355X (gfx950) DDPM hot path.
+ *
+ * Every entry point takes plain device pointers, int64 sizes and a HIP
+ * stream; none allocates, none synchronizes; launches are asynchronous on
+ * `stream`.  Each returns 0 on success, a hipError_t value on a launch
+ * failure, or one of the DDPM_STATUS_* codes below (ddpm_status_string()
+ * turns any code into text).  Tensors are contiguous:
+ *
+ *   x, y, grad_x, grad_y        [N][C][H][W]
+ *   kernels, grad_kernels       [N][3][C][K*K][H][W]   (row o = (b*C+c)*K*K + ki*K + kj)
+ *   weight, grad_weight         [3*C*K*K][C]           (Conv2d [3CK^2, C, 1, 1])
+ *   bias, grad_bias             [3*C*K*K]
+ *   out / grad_out ("cat")      [N][4*C][H][W] = [x, d0, d1, d2]
+ *
+ * dtype codes: 0 = float32, 1 = bfloat16, 2 = float16.
+ * Dilations d0, d1, d2 are the three branch dilations ((1, 3, 5) in DDPM).
+ * The neighbour of (h, w) for tap (ki, kj) at dilation d is
+ * (h + (ki - K/2) d, w + (kj - K/2) d), zero outside the image.
+ */
+#ifndef DDPM_HIP_H
+#define DDPM_HIP_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DDPM_STATUS_OK 0
+#define DDPM_STATUS_BAD_ARGUMENT 10001
+#define DDPM_STATUS_UNSUPPORTED 10002
+#define DDPM_STATUS_WORKSPACE_TOO_SMALL 10003
+
+#define DDPM_DTYPE_F32 0
+#define DDPM_DTYPE_BF16 1
+#define DDPM_DTYPE_F16 2
+
+/* ABI version of this header (1). */
+int ddpm_abi_version(void);
+
+/* Text for any status code returned by this library (static storage). */
+const char* ddpm_status_string(int code);
+
+/* 1 when the fused generator entry points (ddpm_gen_*) accept this channel
+ * count, kernel size and largest dilation (C <= 64, K in {1, 3}, halo tile
+ * within 64 KB of LDS: max_dilation <= 6 for K = 3), else 0.  The reference's
+ * fused path has no such limit; callers route other shapes to the
+ * materialized entry points (ddpm_filter_*), with identical results. */
+int ddpm_gen_supported(int64_t c, int kernel_size, int max_dilation);
+
+/* ---- materialized dynamic filter ------------------------------------- */
+
+/* out = [x, d0, d1, d2] from materialized kernels; out has k_dtype, and the
+ * filter accumulates in fp32.
+ * Replaces _dynamic_cat_fwd + _DynamicCat.forward (_triton_kernels.py:21-101, 814-842). */
+int ddpm_filter_fwd(const void* x, const void* kernels, void* out, int64_t n, int64_t c, int64_t h,
+                    int64_t w, int kernel_size, int d0, int d1, int d2, int x_dtype, int k_dtype,
+                    hipStream_t stream);
+
+/* grad_x[c,q] = grad_out[x-channel c, q]
+ *             + sum_b sum_tap kernels[b,c,tap,q-off] * grad_out[branch b, c, q-off].
+ * grad_out and kernels have k_dtype, grad_x has x_dtype.
+ * Replaces _dynamic_cat_bwd_x (_triton_kernels.py:104-190, launched at :862-863). */
+int ddpm_filter_bwd_x(const void* grad_out, const void* kernels, void* grad_x, int64_t n, int64_t c,
+                      int64_t h, int64_t w, int kernel_size, int d0, int d1, int d2, int x_dtype,
+                      int k_dtype, hipStream_t stream);
+
+/* grad_kernels[b,c,tap,p] = grad_out[branch b, c, p] * x[c, p+off(b,tap)].
+ * Replaces _dynamic_cat_bwd_k (_triton_kernels.py:193-254, launched at :864-865). */
+int ddpm_filter_bwd_k(const void* x, const void* grad_out, void* grad_kernels, int64_t n, int64_t c,
+                      int64_t h, int64_t w, int kernel_size, int d0, int d1, int d2, int x_dtype,
+                      int k_dtype, hipStream_t stream);
+
+/* ---- fused generator (all tensors share `dtype`) ---------------------- */
+
+/* out = [x, d0, d1, d2] with the dynamic taps generated on chip
+ * (gen = weight . y + bias, rounded to `dtype` for bf16/f16).
+ * Replaces _generator_dynamic_cat_fwd + _launch_generator_dynamic_cat
+ * (_triton_kernels.py:268-420, 873-908). */
+int ddpm_gen_fwd(const void* x, const void* y, const void* weight, const void* bias, void* out,
+                 int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size, int d0, int d1,
+                 int d2, int dtype, hipStream_t stream);
+
+/* grad_x of the fused op, recomputing the generator at the gathered pixels.
+ * Replaces _generator_dynamic_cat_bwd_x (_triton_kernels.py:430-531, launched at :944-961). */
+int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bias, const void* grad_out,
+                   void* grad_x, int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size,
+                   int d0, int d1, int d2, int dtype, hipStream_t stream);
+
+/* grad_y = weight^T . dK with dK = grad_out[branch] * shifted x formed on chip.
+ * Replaces _generator_dynamic_cat_bwd_y (_triton_kernels.py:534-623, launched at :963-971). */
+int ddpm_gen_bwd_y(const void* x, const void* weight, const void* grad_out, void* grad_y, int64_t n,
+                   int64_t c, int64_t h, int64_t w, int kernel_size, int d0, int d1, int d2,
+                   int dtype, hipStream_t stream);
+
+/* Bytes of fp32 workspace ddpm_gen_bwd_w needs for its split partials
+ * (0 when it writes grad_weight / grad_bias directly).
+ * Replaces the partial-buffer sizing of _GeneratorDynamicCat.backward (_triton_kernels.py:1001-1017). */
+int64_t ddpm_gen_bwd_w_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size);
+
+/* grad_weight[o,i] = sum_p dK[o,p] y[i,p], grad_bias[o] = sum_p dK[o,p]; split
+ * over <= 16 token ranges into fp32 partials in `workspace`, then summed in
+ * a fixed order (deterministic).
+ * Replaces _generator_dynamic_cat_bwd_weight_partial + _bwd_weight_reduce
+ * (_triton_kernels.py:626-811, launched at :973-1053). */
+int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out, void* grad_weight,
+                   void* grad_bias, void* workspace, int64_t workspace_bytes, int64_t n, int64_t c,
+                   int64_t h, int64_t w, int kernel_size, int d0, int d1, int d2, int dtype,
+                   hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DDPM_HIP_H */

@@ -1,0 +1,172 @@
+"""Operator-level parity of the HIP kernels with the oracle (GPU).
+
+Every entry point of libddpm_hip.so is called through the drop-in operators
+(fused_dynamic_cat, fused_generator_dynamic_cat) on seeded inputs and compared
+with the CPU float64 oracle computed from the same (dtype-rounded) inputs.
+"""
+
+import pytest
+import torch
+
+from dynamicconvolutionoperator_amd import ops
+from oracle import unfold_ref as ref
+from tests.gpu_helpers import DEV, DIL, TOL, assert_close, default_generator_params, randn, say
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [
+    (2, 24, 15, 17),  # non-aligned channels and width (scalar path)
+    (1, 16, 16, 32),  # W % 4 == 0 (vector path), C = 16
+    (1, 64, 20, 64),  # C = 64, several tiles
+]
+
+
+def t(case, key, dtype=torch.float32):
+    return torch.tensor(case[key], dtype=torch.float64).to(dtype)
+
+
+# ---------------------------------------------------------------- known answers (exact)
+def test_kat_filter_exact(kat_cases):
+    for case in (c for c in kat_cases if c["kind"] == "filter"):
+        K = case["K"]
+        say(f"kat filter K={K} shape=({case['N']},{case['C']},{case['H']},{case['W']})")
+        x = t(case, "x").to(DEV).requires_grad_()
+        k = t(case, "kernels").to(DEV).requires_grad_()
+        out = ops.fused_dynamic_cat(x, k, K, DIL)
+        assert torch.equal(out.cpu().double(), t(case, "out", torch.float64))
+        out.backward(t(case, "grad_out").to(DEV))
+        assert torch.equal(x.grad.cpu().double(), t(case, "grad_x", torch.float64))
+        assert torch.equal(k.grad.cpu().double(), t(case, "grad_kernels", torch.float64))
+
+
+def test_kat_generator_exact(kat_cases):
+    for case in (c for c in kat_cases if c["kind"] == "generator"):
+        K, C = case["K"], case["C"]
+        say(f"kat generator K={K} shape=({case['N']},{C},{case['H']},{case['W']})")
+        x = t(case, "x").to(DEV).requires_grad_()
+        y = t(case, "y").to(DEV).requires_grad_()
+        w = t(case, "weight").reshape(3 * C * K * K, C, 1, 1).to(DEV).requires_grad_()
+        b = t(case, "bias").to(DEV).requires_grad_()
+        out = ops.fused_generator_dynamic_cat(x, y, w, b, K, DIL)
+        assert torch.equal(out.detach().cpu().double(), t(case, "out", torch.float64))
+        out.backward(t(case, "grad_out").to(DEV))
+        assert torch.equal(x.grad.cpu().double(), t(case, "grad_x", torch.float64))
+        assert torch.equal(y.grad.cpu().double(), t(case, "grad_y", torch.float64))
+        assert torch.equal(w.grad.reshape(-1, C).cpu().double(), t(case, "grad_weight", torch.float64))
+        assert torch.equal(b.grad.cpu().double(), t(case, "grad_bias", torch.float64))
+
+
+# ---------------------------------------------------------------- materialized filter
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("K", [1, 3, 5])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_filter_matches_oracle(shape, K, dtype):
+    n, c, h, w = shape
+    say(f"filter shape={shape} K={K} dtype={dtype}")
+    x = randn(shape, 10, dtype)
+    k = randn((n, 3, c, K * K, h, w), 11, dtype)
+    g = randn((n, 4 * c, h, w), 12, dtype)
+    xd = x.to(DEV).requires_grad_()
+    kd = k.to(DEV).requires_grad_()
+    out = ops.fused_dynamic_cat(xd, kd, K, DIL)
+    assert out.dtype == dtype
+    out.backward(g.to(DEV))
+    atol, rtol = TOL["filter"][dtype]
+    x64, k64, g64 = x.double(), k.double(), g.double()
+    assert_close(out, ref.dynamic_cat(x64, k64, K), atol, rtol, "filter out")
+    dx, dk = ref.dynamic_cat_backward(x64, k64, g64, K)
+    assert_close(xd.grad, dx, atol, rtol, "filter dx")
+    assert_close(kd.grad, dk, atol, rtol, "filter dk")
+
+
+def test_filter_mixed_dtypes_autocast_layout():
+    """x fp32 with bf16 kernels (the autocast case): out and dK in bf16, dX in fp32."""
+    n, c, h, w, K = 1, 8, 12, 20, 3
+    x = randn((n, c, h, w), 20, torch.float32)
+    k = randn((n, 3, c, K * K, h, w), 21, torch.bfloat16)
+    g = randn((n, 4 * c, h, w), 22, torch.bfloat16)
+    xd = x.to(DEV).requires_grad_()
+    kd = k.to(DEV).requires_grad_()
+    out = ops.fused_dynamic_cat(xd, kd, K, DIL)
+    assert out.dtype == torch.bfloat16
+    out.backward(g.to(DEV))
+    assert xd.grad.dtype == torch.float32 and kd.grad.dtype == torch.bfloat16
+    assert_close(out, ref.dynamic_cat(x.double(), k.double(), K), 2e-2, 1e-2, "mixed out")
+    dx, dk = ref.dynamic_cat_backward(x.double(), k.double(), g.double(), K)
+    assert_close(xd.grad, dx, 2e-4, 1e-4, "mixed dx")
+    assert_close(kd.grad, dk, 2e-2, 1e-2, "mixed dk")
+
+
+# ---------------------------------------------------------------- fused generator
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("K", [1, 3])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_generator_matches_oracle(shape, K, dtype):
+    n, c, h, w = shape
+    say(f"generator shape={shape} K={K} dtype={dtype}")
+    x = randn(shape, 30, dtype)
+    y = randn(shape, 31, dtype)
+    wt, b = default_generator_params(c, K, 32, dtype)
+    g = randn((n, 4 * c, h, w), 33, dtype)
+    xd, yd = x.to(DEV).requires_grad_(), y.to(DEV).requires_grad_()
+    wd, bd = wt.to(DEV).requires_grad_(), b.to(DEV).requires_grad_()
+    out = ops.fused_generator_dynamic_cat(xd, yd, wd, bd, K, DIL)
+    assert out.dtype == dtype
+    out.backward(g.to(DEV))
+
+    x64, y64, w64, b64, g64 = (v.double() for v in (x, y, wt, b, g))
+    kern = ref.generated_kernels(y64, w64, b64, K)
+    if dtype != torch.float32:
+        kern = kern.to(dtype).double()  # the generated taps are rounded to the input dtype
+    atol, rtol = TOL["gen_fwd"][dtype]
+    assert_close(out, ref.dynamic_cat(x64, kern, K), atol, rtol, "gen out")
+    dx, dy, dw, db = ref.generator_dynamic_cat_backward(x64, y64, w64, b64, g64, K)
+    atol, rtol = TOL["gen_bwd"][dtype]
+    # gradient magnitudes scale with the number of summed terms; compare relative to the max
+    for name, a, e in (("dx", xd.grad, dx), ("dy", yd.grad, dy), ("dw", wd.grad, dw), ("db", bd.grad, db)):
+        scale = max(1.0, e.abs().max().item())
+        assert_close(a, e, atol * scale, rtol, f"gen {name}")
+
+
+def test_generator_inference_has_no_autograd_graph():
+    x = randn((1, 8, 9, 16), 40).to(DEV)
+    y = randn((1, 8, 9, 16), 41).to(DEV)
+    wt, b = default_generator_params(8, 3, 42, torch.float32)
+    with torch.no_grad():
+        out = ops.fused_generator_dynamic_cat(x, y, wt.to(DEV), b.to(DEV), 3, DIL)
+    assert out.grad_fn is None
+    with torch.inference_mode():
+        out2 = ops.fused_generator_dynamic_cat(x, y, wt.to(DEV), b.to(DEV), 3, DIL)
+    assert torch.equal(out, out2)
+
+
+def test_generator_split_weight_gradient_matches_direct():
+    """Shapes above 2048 tokens use split fp32 partials; compare to the oracle."""
+    shape = (2, 32, 40, 64)  # 5120 tokens -> 3 splits
+    n, c, h, w = shape
+    x = randn(shape, 50)
+    y = randn(shape, 51)
+    wt, b = default_generator_params(c, 3, 52, torch.float32)
+    g = randn((n, 4 * c, h, w), 53)
+    wd, bd = wt.to(DEV).requires_grad_(), b.to(DEV).requires_grad_()
+    out = ops.fused_generator_dynamic_cat(x.to(DEV), y.to(DEV), wd, bd, 3, DIL)
+    out.backward(g.to(DEV))
+    _, _, dw, db = ref.generator_dynamic_cat_backward(x.double(), y.double(), wt.double(), b.double(), g.double(), 3)
+    assert_close(wd.grad, dw, 3e-3 * dw.abs().max().item(), 3e-3, "split dw")
+    assert_close(bd.grad, db, 3e-3 * db.abs().max().item(), 3e-3, "split db")
+
+
+def test_deterministic_backward():
+    shape = (1, 64, 64, 64)
+    x = randn(shape, 60).to(DEV)
+    y = randn(shape, 61).to(DEV)
+    wt, b = default_generator_params(64, 3, 62, torch.float32)
+    g = randn((1, 256, 64, 64), 63).to(DEV)
+    grads = []
+    for _ in range(2):
+        wd, bd = wt.to(DEV).requires_grad_(), b.to(DEV).requires_grad_()
+        xd, yd = x.clone().requires_grad_(), y.clone().requires_grad_()
+        ops.fused_generator_dynamic_cat(xd, yd, wd, bd, 3, DIL).backward(g)
+        grads.append([v.grad.clone() for v in (xd, yd, wd, bd)])
+    for a, b2 in zip(*grads):
+        assert torch.equal(a, b2)
