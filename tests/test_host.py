@@ -1,0 +1,115 @@
+"""Host-side tests (no GPU): the C-ABI library loads and exports every symbol
+declared in include/ddpm_hip.h, argument validation needs no device, the
+routing rules mirror the reference's (triton_impl.py:311-329), and GPU
+tensors never fall back to the CPU branch."""
+
+import os
+import re
+
+import pytest
+import torch
+
+import dynamicconvolutionoperator_amd as dco
+from dynamicconvolutionoperator_amd import _lib, module
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_symbols():
+    text = open(os.path.join(ROOT, "include", "ddpm_hip.h")).read()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(ddpm_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_bound_symbols():
+    assert _declared_symbols() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+
+
+def test_host_only_queries():
+    lib = _lib.load()
+    assert lib.ddpm_abi_version() == 1
+    assert b"invalid argument" in lib.ddpm_status_string(10001)
+    assert lib.ddpm_gen_supported(64, 3, 5) == 1
+    assert lib.ddpm_gen_supported(65, 3, 5) == 0
+    assert lib.ddpm_gen_supported(64, 5, 5) == 0
+    # 16 splits x 27 (branch, tap) x 64 x (64 + 1) fp32 partials at 256x256
+    assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 64, 256, 256, 3) == 16 * 27 * 64 * 65 * 4
+    assert lib.ddpm_gen_bwd_w_workspace_bytes(2, 24, 15, 17, 3) == 0  # direct write
+
+
+def test_entry_points_validate_arguments_before_touching_the_device():
+    lib = _lib.load()
+    null = None
+    # even kernel size / bad dtype / null pointers are rejected host-side
+    assert lib.ddpm_filter_fwd(null, null, null, 1, 1, 4, 4, 2, 1, 3, 5, 0, 0, null) == 10001
+    assert lib.ddpm_filter_fwd(null, null, null, 1, 1, 4, 4, 3, 1, 3, 5, 7, 0, null) == 10001
+    assert lib.ddpm_filter_fwd(null, null, null, 1, 1, 4, 4, 3, 1, 3, 5, 0, 0, null) == 10001
+    assert lib.ddpm_gen_fwd(null, null, null, null, null, 1, 65, 4, 4, 3, 1, 3, 5, 0, null) == 10002
+    assert lib.ddpm_gen_bwd_w(null, null, null, null, null, null, 0, 1, 64, 256, 256, 3, 1, 3, 5, 0, null) != 0
+    # empty tensors are a no-op
+    assert lib.ddpm_filter_fwd(null, null, null, 0, 4, 4, 4, 3, 1, 3, 5, 0, 0, null) == 0
+
+
+class _FakeTensor:
+    def __init__(self, shape, dtype=torch.float32):
+        self.shape = shape
+        self.dtype = dtype
+        self.device = torch.device("cpu")
+
+
+@pytest.mark.parametrize(
+    "tokens_shape, dtype, k, flag, grad, autocast, expect",
+    [
+        ((1, 64, 256, 256), torch.float32, 3, None, True, False, "fused"),  # > 16384 tokens
+        ((1, 64, 128, 128), torch.float32, 3, None, True, False, "fused"),  # == 16384, fp32
+        ((1, 64, 128, 128), torch.bfloat16, 3, None, True, False, "materialized"),  # == 16384 bf16
+        ((1, 64, 64, 64), torch.float32, 3, None, True, False, "materialized"),  # small, training
+        ((1, 64, 64, 64), torch.float32, 3, None, False, False, "fused"),  # inference
+        ((1, 64, 64, 64), torch.float32, 3, True, True, False, "fused"),  # forced fused
+        ((1, 64, 256, 256), torch.float32, 3, False, True, False, "materialized"),  # forced off
+        ((1, 64, 256, 256), torch.float32, 5, True, True, False, "materialized"),  # K > 3
+        ((1, 64, 256, 256), torch.float32, 5, None, False, False, "materialized"),  # K > 3 inference
+        ((1, 64, 256, 256), torch.float32, 3, None, False, True, "materialized"),  # autocast
+    ],
+)
+def test_routing_rules(monkeypatch, tokens_shape, dtype, k, flag, grad, autocast, expect):
+    c = tokens_shape[1]
+    m = module.DDPM(c, k, fused_generator_training=flag).to(dtype)
+    x = _FakeTensor(tokens_shape, dtype)
+    monkeypatch.setattr(torch, "is_autocast_enabled", lambda *a, **k: autocast)
+    supported = lambda ch, ks, dil: ks <= 3 and ch <= 64  # noqa: E731
+    with torch.set_grad_enabled(grad):
+        assert m._route(x, x, supported) == expect
+
+
+def test_routing_dtype_mismatch_materializes():
+    m = module.DDPM(8, 3)  # fp32 parameters
+    x = _FakeTensor((1, 8, 64, 64), torch.bfloat16)
+    with torch.no_grad():
+        assert m._route(x, x, lambda *a: True) == "materialized"
+
+
+def test_gpu_tensors_fail_loudly_without_the_library(monkeypatch):
+    """A missing library must raise for device tensors, never fall back."""
+
+    def missing():
+        raise _lib.HipLibraryError("libddpm_hip.so is not built")
+
+    monkeypatch.setattr(module, "_load_hip_ops", missing)
+    m = module.DDPM(4, 3)
+
+    x = torch.randn(1, 4, 5, 5)
+    # DDPM.forward routes on x.is_cuda; emulate a device tensor's routing
+    monkeypatch.setattr(torch.Tensor, "is_cuda", property(lambda self: True))
+    with pytest.raises(_lib.HipLibraryError):
+        m(x, x.clone())
+
+
+def test_public_api_names():
+    for name in ("DDPM", "fused_dynamic_cat", "fused_generator_dynamic_cat"):
+        assert hasattr(dco, name)
