@@ -19,6 +19,9 @@ typedef _Float16 f16;
 typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 enum DType : int { kF32 = 0, kBF16 = 1, kF16 = 2 };
 
@@ -49,6 +52,25 @@ __device__ __forceinline__ float quant<float>(float v) {
   return v;
 }
 
+// Two fp32 values rounded to nearest-even bf16, packed low/high
+// (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const bf16x2 r = __builtin_convertvector((f32x2){a, b}, bf16x2);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// Splits two fp32 values into bf16 pairs hi + lo with a ~= hi_a + lo_a:
+// hi keeps the top 16 bits of the fp32 pattern (so a - hi is exact in fp32)
+// and lo is that remainder rounded to nearest-even bf16; |a - hi - lo| <=
+// 2^-17 |a|.  Six VALU instructions per pair (2 and, perm, 2 sub, cvt_pk).
+__device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
+  hi = __builtin_amdgcn_perm(ub, ua, 0x07060302u);  // [hi16(a) | hi16(b) << 16]
+  const float la = a - __uint_as_float(ua & 0xffff0000u);
+  const float lb = b - __uint_as_float(ub & 0xffff0000u);
+  lo = pack_bf16x2(la, lb);
+}
+
 // ---------------------------------------------------------------------------
 // MFMA 16x16x32 (gfx950), lane layout (verified on the device):
 //   A (16x32): lane l holds A[l&15][8*(l>>4) + e], e=0..7
@@ -66,12 +88,11 @@ struct Mma<float> {
   typedef bf16 E;
   typedef bf16x8 V;
   static __device__ __forceinline__ void pack(const float (&v)[8], V (&o)[2]) {
+    uint32_t hi[4], lo[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const bf16 h = (bf16)v[e];
-      o[0][e] = h;
-      o[1][e] = (bf16)(v[e] - (float)h);
-    }
+    for (int e = 0; e < 4; ++e) split_bf16x2(v[2 * e], v[2 * e + 1], hi[e], lo[e]);
+    o[0] = __builtin_bit_cast(V, (u32x4){hi[0], hi[1], hi[2], hi[3]});
+    o[1] = __builtin_bit_cast(V, (u32x4){lo[0], lo[1], lo[2], lo[3]});
   }
   static __device__ __forceinline__ f32x4 mac(const V (&a)[2], const V (&b)[2], f32x4 acc) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[0], acc, 0, 0, 0);
@@ -87,8 +108,10 @@ struct Mma<bf16> {
   typedef bf16 E;
   typedef bf16x8 V;
   static __device__ __forceinline__ void pack(const float (&v)[8], V (&o)[1]) {
+    u32x4 p;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[0][e] = (bf16)v[e];
+    for (int e = 0; e < 4; ++e) p[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+    o[0] = __builtin_bit_cast(V, p);
   }
   static __device__ __forceinline__ f32x4 mac(const V (&a)[1], const V (&b)[1], f32x4 acc) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], acc, 0, 0, 0);
@@ -137,6 +160,51 @@ struct VecIO {
     }
   }
 };
+
+// ---------------------------------------------------------------------------
+// Buffer loads (gfx9 raw buffers): a load whose byte offset is at or beyond
+// the resource's num_records returns zero, so out-of-image pixels, padded
+// channels and halo columns are read branch-free by pointing their offset
+// past the end (kOob) or by giving a whole row num_records = 0.
+// ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t BufRes;
+constexpr uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ BufRes make_buf(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+template <typename T>
+__device__ __forceinline__ float buf_load1(BufRes r, uint32_t off) {
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  } else {
+    const unsigned short s = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    return to_f(__builtin_bit_cast(T, s));
+  }
+}
+
+// 8 consecutive elements at byte offset `off` (16-byte aligned for 2-byte
+// types, 16-byte aligned pairs for fp32), converted to fp32.
+template <typename T>
+__device__ __forceinline__ void buf_load8(BufRes r, uint32_t off, float (&v)[8]) {
+  if constexpr (sizeof(T) == 4) {
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16u, 0, 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = __uint_as_float(a[e]);
+      v[4 + e] = __uint_as_float(b[e]);
+    }
+  } else {
+    typedef T T8 __attribute__((ext_vector_type(8)));
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    const T8 t = __builtin_bit_cast(T8, a);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = to_f(t[e]);
+  }
+}
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).
 // Remap the hardware block id so that each XCD receives one contiguous range of

@@ -329,205 +329,6 @@ __global__ __launch_bounds__(kBwdThreads) void gen_bwd_y_kernel(const T* __restr
   }
 }
 
-// ---------------------------------------------------------------------------
-// dW / db partial: one workgroup per (branch*tap, split); its 4 waves take
-// interleaved 32-token steps of the split and are reduced through LDS in a
-// fixed order at the end (deterministic, no atomics).  M = output channels c,
-// N = input channels i, K = tokens.
-// ---------------------------------------------------------------------------
-struct WGradGeom {
-  int N, C, H, W, K;
-  int d0, d1, d2;
-  int splits;
-  int tokens_per_split;  // multiple of 32
-  int64_t tokens;        // N*H*W
-  int direct;            // write grad_weight/grad_bias directly (splits == 1)
-  int fast;              // W % 8 == 0: 8-token runs stay inside one image row
-};
-
-template <typename T, int KS, int MB, bool FAST>
-__global__ __launch_bounds__(kBwdThreads) void gen_bwd_w_partial_kernel(
-    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ gout,
-    float* __restrict__ pw, float* __restrict__ pb, T* __restrict__ dw_out, T* __restrict__ db_out,
-    WGradGeom g) {
-  typedef Mma<T> M;
-  typedef typename M::V V;
-  constexpr int KK = KS * KS;
-  constexpr int r = KS / 2;
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  float* __restrict__ red = reinterpret_cast<float*>(smem);  // [MB*16][MB*16 + 1] + [4][MB*16]
-
-  const int bt = blockIdx.x;      // branch * KK + tap
-  const int split = blockIdx.y;
-  const int b = bt / KK, t = bt - b * KK;
-  const int ki = t / KS, kj = t % KS;
-  const int d = dil_of(b, g.d0, g.d1, g.d2);
-  const int dh = (ki - r) * d, dw = (kj - r) * d;
-  const int C = g.C;
-  const int64_t HW = (int64_t)g.H * g.W;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int col16 = lane & 15, quad = lane >> 4;
-
-  f32x4 acc[MB][MB];
-#pragma unroll
-  for (int mc = 0; mc < MB; ++mc)
-#pragma unroll
-    for (int mi = 0; mi < MB; ++mi) acc[mc][mi] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float bacc[MB];
-#pragma unroll
-  for (int mc = 0; mc < MB; ++mc) bacc[mc] = 0.f;
-
-  const int64_t tbeg = (int64_t)split * g.tokens_per_split;
-  int64_t tend = tbeg + g.tokens_per_split;
-  if (tend > g.tokens) tend = g.tokens;
-
-  for (int64_t t0 = tbeg + 32 * wave; t0 < tend; t0 += 32 * 4) {
-    const int64_t tk = t0 + 8 * quad;  // first of this lane's 8 tokens
-    float yv[MB][8];
-    float dk[MB][8];
-    if constexpr (FAST) {
-      // 8 tokens inside one row: n, h fixed, w .. w+7 (W % 8 == 0, tk % 8 == 0)
-      const bool any = tk < tend;
-      const int64_t nn = any ? tk / HW : 0;
-      const int64_t p = tk - nn * HW;
-      const int hh = (int)(p / g.W), ww = (int)(p - (int64_t)hh * g.W);
-      const int nh = hh + dh;
-      const bool nh_ok = any && (unsigned)nh < (unsigned)g.H;
-      const T* __restrict__ yb = y + nn * C * HW + p;
-      const T* __restrict__ gb = gout + (nn * 4 * C + (int64_t)(b + 1) * C) * HW + p;
-      const T* __restrict__ xb = x + nn * C * HW + (int64_t)nh * g.W;
-#pragma unroll
-      for (int m = 0; m < MB; ++m) {
-        const int ch = m * 16 + col16;  // row c for A, col i for B (same lane index)
-        const bool ch_ok = any && ch < C;
-        if (ch_ok) {
-          VecIO<T, 8>::load(yb + (int64_t)ch * HW, yv[m]);
-          float gv[8];
-          VecIO<T, 8>::load(gb + (int64_t)ch * HW, gv);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int nw = ww + e + dw;
-            const float xv =
-                (nh_ok && (unsigned)nw < (unsigned)g.W) ? to_f(xb[(int64_t)ch * HW + nw]) : 0.f;
-            dk[m][e] = gv[e] * xv;
-          }
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            yv[m][e] = 0.f;
-            dk[m][e] = 0.f;
-          }
-        }
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int64_t tt = tk + e;
-        const bool ok = tt < tend;
-        const int64_t nn = ok ? tt / HW : 0;
-        const int64_t p = tt - nn * HW;
-        const int hh = (int)(p / g.W), ww = (int)(p - (int64_t)hh * g.W);
-        const int nh = hh + dh, nw = ww + dw;
-        const bool nok = ok && (unsigned)nh < (unsigned)g.H && (unsigned)nw < (unsigned)g.W;
-#pragma unroll
-        for (int m = 0; m < MB; ++m) {
-          const int ch = m * 16 + col16;
-          const bool cok = ok && ch < C;
-          yv[m][e] = cok ? to_f(y[(nn * C + ch) * HW + p]) : 0.f;
-          const float gv =
-              cok ? to_f(gout[(nn * 4 * C + (int64_t)(b + 1) * C + ch) * HW + p]) : 0.f;
-          const float xv = (cok && nok) ? to_f(x[(nn * C + ch) * HW + (int64_t)nh * g.W + nw]) : 0.f;
-          dk[m][e] = gv * xv;
-        }
-      }
-    }
-    V afr[MB][M::P], bfr[MB][M::P];
-#pragma unroll
-    for (int m = 0; m < MB; ++m) {
-      M::pack(dk[m], afr[m]);
-      M::pack(yv[m], bfr[m]);
-      // db uses the operand-precision dK, like the weight gradient
-#pragma unroll
-      for (int e = 0; e < 8; ++e) bacc[m] += quant<T>(dk[m][e]);
-    }
-#pragma unroll
-    for (int mc = 0; mc < MB; ++mc)
-#pragma unroll
-      for (int mi = 0; mi < MB; ++mi) acc[mc][mi] = M::mac(afr[mc], bfr[mi], acc[mc][mi]);
-  }
-
-  // ---- deterministic reduction of the 4 waves (fixed order 0,1,2,3)
-  constexpr int NO = MB * 16;
-  constexpr int RS = NO + 1;
-  float* __restrict__ rb = red + NO * RS;  // bias partials [4 waves][4 quads][NO]
-#pragma unroll
-  for (int m = 0; m < MB; ++m) rb[(wave * 4 + quad) * NO + m * 16 + col16] = bacc[m];
-  for (int w = 0; w < 4; ++w) {
-    if (wave == w) {
-#pragma unroll
-      for (int mc = 0; mc < MB; ++mc)
-#pragma unroll
-        for (int mi = 0; mi < MB; ++mi)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int c = mc * 16 + 4 * quad + e, i = mi * 16 + col16;
-            float* dst = red + c * RS + i;
-            *dst = (w == 0 ? 0.f : *dst) + acc[mc][mi][e];
-          }
-    }
-    __syncthreads();
-  }
-  // write out: NO x NO weights + NO biases
-  for (int idx = tid; idx < NO * NO; idx += kBwdThreads) {
-    const int c = idx / NO, i = idx - c * NO;
-    if (c >= C || i >= C) continue;
-    const float v = red[c * RS + i];
-    if (g.direct)
-      dw_out[((int64_t)(b * C + c) * KK + t) * C + i] = from_f<T>(v);
-    else
-      pw[(((int64_t)split * 3 * KK + bt) * C + c) * C + i] = v;
-  }
-  for (int c = tid; c < NO; c += kBwdThreads) {
-    if (c >= C) continue;
-    float v = 0.f;
-    for (int w = 0; w < 16; ++w) v += rb[w * NO + c];
-    if (g.direct)
-      db_out[(int64_t)(b * C + c) * KK + t] = from_f<T>(v);
-    else
-      pb[((int64_t)split * 3 * KK + bt) * C + c] = v;
-  }
-}
-
-// Fixed-order sum of the split partials, written in Conv2d parameter layout.
-template <typename T>
-__global__ __launch_bounds__(256) void gen_bwd_w_reduce_kernel(const float* __restrict__ pw,
-                                                                 const float* __restrict__ pb,
-                                                                 T* __restrict__ dw_out,
-                                                                 T* __restrict__ db_out, int C,
-                                                                 int KK, int splits) {
-  const int64_t per = (int64_t)3 * KK * C * C;
-  const int64_t perb = (int64_t)3 * KK * C;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx < per) {
-    float v = 0.f;
-    for (int s = 0; s < splits; ++s) v += pw[s * per + idx];
-    // idx = (bt*C + c)*C + i  ->  row o = (b*C + c)*KK + t
-    const int64_t i = idx % C;
-    const int64_t c = (idx / C) % C;
-    const int64_t bt = idx / ((int64_t)C * C);
-    const int64_t b = bt / KK, t = bt % KK;
-    dw_out[((b * C + c) * KK + t) * C + i] = from_f<T>(v);
-  } else if (idx < per + perb) {
-    const int64_t j = idx - per;
-    float v = 0.f;
-    for (int s = 0; s < splits; ++s) v += pb[s * perb + j];
-    const int64_t c = j % C, bt = j / C;
-    const int64_t b = bt / KK, t = bt % KK;
-    db_out[(b * C + c) * KK + t] = from_f<T>(v);
-  }
-}
-
 namespace {
 
 template <typename F>
@@ -575,29 +376,6 @@ int bwd_geom(GenGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int k, int 
   g.tiles_w = (int)((w + kBwdTW - 1) / kBwdTW);
   g.tiles = g.tiles_w * (int)((h + kBwdTH - 1) / kBwdTH);
   return kOk;
-}
-
-void wgrad_geom(WGradGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int k, int d0, int d1,
-                int d2) {
-  g.N = (int)n;
-  g.C = (int)c;
-  g.H = (int)h;
-  g.W = (int)w;
-  g.K = k;
-  g.d0 = d0;
-  g.d1 = d1;
-  g.d2 = d2;
-  g.tokens = n * h * w;
-  // At most 16 fp32 partials; about 2048 tokens per split below that.
-  int64_t splits = (g.tokens + 2047) / 2048;
-  if (splits < 1) splits = 1;
-  if (splits > 16) splits = 16;
-  g.splits = (int)splits;
-  int64_t tps = (g.tokens + splits - 1) / splits;
-  tps = (tps + 127) / 128 * 128;  // 4 waves x 32-token steps
-  g.tokens_per_split = (int)tps;
-  g.direct = splits == 1;
-  g.fast = (w % 8) == 0;
 }
 
 }  // namespace
@@ -656,66 +434,6 @@ extern "C" int ddpm_gen_bwd_y(const void* x, const void* weight, const void* gra
         hipLaunchKernelGGL((gen_bwd_y_kernel<T, KS, MB>), dim3((unsigned)((int64_t)g.N * g.tiles)),
                            dim3(kBwdThreads), lds, stream, (const T*)x, (const T*)weight,
                            (const T*)grad_out, (T*)grad_y, g);
-        return (int)hipGetLastError();
-      });
-    });
-  });
-}
-
-extern "C" int64_t ddpm_gen_bwd_w_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w,
-                                                  int kernel_size) {
-  if (n <= 0 || c <= 0 || h <= 0 || w <= 0 || kernel_size < 1) return 0;
-  WGradGeom g;
-  wgrad_geom(g, n, c, h, w, kernel_size, 1, 1, 1);
-  if (g.direct) return 0;
-  const int64_t kk = (int64_t)kernel_size * kernel_size;
-  return (int64_t)g.splits * 3 * kk * c * (c + 1) * (int64_t)sizeof(float);
-}
-
-extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out,
-                              void* grad_weight, void* grad_bias, void* workspace,
-                              int64_t workspace_bytes, int64_t n, int64_t c, int64_t h, int64_t w,
-                              int kernel_size, int d0, int d1, int d2, int dtype,
-                              hipStream_t stream) {
-  if (dtype < kF32 || dtype > kF16) return kBadArgument;
-  GenGeom gg;
-  int st = gen_make_geom(gg, n, c, h, w, kernel_size, d0, d1, d2);
-  if (st != kOk) return st;
-  if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
-  if (!x || !y || !grad_out || !grad_weight || !grad_bias) return kBadArgument;
-  WGradGeom g;
-  wgrad_geom(g, n, c, h, w, kernel_size, d0, d1, d2);
-  const int64_t need = ddpm_gen_bwd_w_workspace_bytes(n, c, h, w, kernel_size);
-  if (need > 0 && (!workspace || workspace_bytes < need)) return kWorkspaceTooSmall;
-  if (g.fast && (((uintptr_t)x | (uintptr_t)y | (uintptr_t)grad_out) % (8 * (dtype == kF32 ? 4 : 2))))
-    g.fast = 0;
-  const int mb = (int)((c + 15) / 16);
-  const int kk = kernel_size * kernel_size;
-  float* pw = (float*)workspace;
-  float* pb = pw ? pw + (int64_t)g.splits * 3 * kk * c * c : nullptr;
-  return with_type(dtype, [&](auto tag) {
-    using T = decltype(tag);
-    return with_ks(kernel_size, [&](auto ks) {
-      constexpr int KS = decltype(ks)::value;
-      return with_mb(mb, [&](auto mbc) {
-        constexpr int MB = decltype(mbc)::value;
-        constexpr int NO = MB * 16;
-        const size_t lds = (size_t)(NO * (NO + 1) + 16 * NO) * sizeof(float);
-        const dim3 grid(3 * KS * KS, g.splits);
-        if (g.fast)
-          hipLaunchKernelGGL((gen_bwd_w_partial_kernel<T, KS, MB, true>), grid, dim3(kBwdThreads),
-                             lds, stream, (const T*)x, (const T*)y, (const T*)grad_out, pw, pb,
-                             (T*)grad_weight, (T*)grad_bias, g);
-        else
-          hipLaunchKernelGGL((gen_bwd_w_partial_kernel<T, KS, MB, false>), grid,
-                             dim3(kBwdThreads), lds, stream, (const T*)x, (const T*)y,
-                             (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g);
-        int e = (int)hipGetLastError();
-        if (e != 0 || g.direct) return e;
-        const int64_t total = (int64_t)3 * kk * c * c + (int64_t)3 * kk * c;
-        hipLaunchKernelGGL((gen_bwd_w_reduce_kernel<T>), dim3((unsigned)((total + 255) / 256)),
-                           dim3(256), 0, stream, pw, pb, (T*)grad_weight, (T*)grad_bias, (int)c,
-                           kk, g.splits);
         return (int)hipGetLastError();
       });
     });
