@@ -285,7 +285,7 @@ def main():
         sys.exit(2)
     lib = _lib.load()
     entries = [n for n in _lib.SIGNATURES if n.startswith(("ddpm_gen_fwd", "ddpm_gen_bwd_x", "ddpm_gen_bwd_y", "ddpm_gen_bwd_w", "ddpm_filter_"))]
-    entries = [n for n in entries if n != "ddpm_gen_bwd_w_workspace_bytes"]
+    entries = [n for n in entries if not n.endswith("_workspace_bytes")]
     timer = LaunchTimer(lib, entries)
 
     # ---- headline: fp32 fused recompute training step

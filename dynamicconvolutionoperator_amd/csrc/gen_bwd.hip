@@ -1,9 +1,9 @@
 // Fused recompute backward of generator + dynamic dilated filter + concat.
 //
-// Counterparts of _generator_dynamic_cat_bwd_x / _bwd_y /
-// _bwd_weight_partial / _bwd_weight_reduce (_triton_kernels.py:430-811,
-// launched at :927-1053).  Nothing but x, y, W, b and grad_cat is read; the
-// dynamic kernels and their gradient dK = dL/dgen are formed on chip only.
+// Counterpart of _generator_dynamic_cat_bwd_x (_triton_kernels.py:430-531,
+// launched at :944-961); the y and weight gradients live in gen_bwd_y.hip and
+// gen_bwd_w.hip.  Nothing but y, W, b and grad_cat is read; the dynamic
+// kernels are recomputed on chip only.
 //
 //   gen[(b,c,t), p] = W[(b,c,t), :] . y[:, p] + bias[(b,c,t)]
 //   dK[(b,c,t), p]  = gO_b[c, p] * x[c, p + off(b,t)]
@@ -188,147 +188,6 @@ __global__ __launch_bounds__(kBwdThreads) void gen_bwd_x_kernel(const T* __restr
   }
 }
 
-// ---------------------------------------------------------------------------
-// dY: M = input channels i (all MB blocks), N = 16 pixels, K = output
-// channels c for each (b, tap).  B operand dK = gO_b[c,p] * x[c, p+off] is
-// formed in registers; the A operand W_bt^T is staged per (b, tap) in LDS,
-// pre-split into MFMA parts and shared by the 4 waves.
-// ---------------------------------------------------------------------------
-template <typename T, int KS, int MB>
-__global__ __launch_bounds__(kBwdThreads) void gen_bwd_y_kernel(const T* __restrict__ x,
-                                                                  const T* __restrict__ wt,
-                                                                  const T* __restrict__ gout,
-                                                                  T* __restrict__ gy, GenGeom g) {
-  typedef Mma<T> M;
-  typedef typename M::V V;
-  typedef typename M::E E;
-  constexpr int KK = KS * KS;
-  constexpr int r = KS / 2;
-  constexpr int KSTEPS = (MB + 1) / 2;
-  constexpr int CP = KSTEPS * 32;  // padded K extent
-  constexpr int LSTR = CP + 8;     // LDS row stride (elements), keeps 16 B alignment
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  // [2 buffers][P parts][MB*16 rows i][LSTR cols c]
-  E* __restrict__ ws = reinterpret_cast<E*>(smem);
-  constexpr int PART = MB * 16 * LSTR;
-
-  const int bid = xcd_remap(blockIdx.x, gridDim.x);
-  const int tile = bid % g.tiles;
-  const int n = bid / g.tiles;
-  const int ty = tile / g.tiles_w, tx = tile - ty * g.tiles_w;
-  const int h0 = ty * kBwdTH, w0 = tx * kBwdTW;
-  const int C = g.C;
-  const int64_t HW = (int64_t)g.H * g.W;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int col16 = lane & 15, quad = lane >> 4;
-  const T* __restrict__ xn = x + (int64_t)n * C * HW;
-  const T* __restrict__ go = gout + (int64_t)n * 4 * C * HW;
-
-  // Stage W_bt^T (rows i, cols c), split into MFMA parts, into buffer `buf`.
-  auto stage = [&](int bt, int buf) {
-    const int b = bt / KK, t = bt - b * KK;
-    E* __restrict__ dst = ws + buf * (M::P * PART);
-    for (int idx = tid; idx < MB * 16 * CP; idx += kBwdThreads) {
-      const int i = idx % (MB * 16), c = idx / (MB * 16);  // coalesced over i
-      float v = 0.f;
-      if (i < C && c < C) v = to_f(wt[((int64_t)(b * C + c) * KK + t) * C + i]);
-      if constexpr (M::P == 2) {
-        const bf16 h = (bf16)v;
-        dst[i * LSTR + c] = h;
-        dst[PART + i * LSTR + c] = (bf16)(v - (float)h);
-      } else {
-        dst[i * LSTR + c] = (E)v;
-      }
-    }
-  };
-
-  f32x4 acc[kBwdNB][MB];
-#pragma unroll
-  for (int blk = 0; blk < kBwdNB; ++blk)
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[blk][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  stage(0, 0);
-  for (int b = 0; b < 3; ++b) {
-    const int d = dil_of(b, g.d0, g.d1, g.d2);
-    const T* __restrict__ gob = go + (int64_t)(b + 1) * C * HW;
-    // branch gradient at this wave's pixels for the lane's K slots (c)
-    float gv[kBwdNB][KSTEPS][8];
-#pragma unroll
-    for (int blk = 0; blk < kBwdNB; ++blk) {
-      const int gh = h0 + wave * kBwdRPW + blk / kBwdCPW;
-      const int gw = w0 + (blk % kBwdCPW) * 16 + col16;
-      const bool ok = gh < g.H && gw < g.W;
-#pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int c = 32 * kk + 8 * quad + e;
-          gv[blk][kk][e] =
-              (ok && c < C) ? to_f(gob[(int64_t)c * HW + (int64_t)gh * g.W + gw]) : 0.f;
-        }
-    }
-    for (int t = 0; t < KK; ++t) {
-      const int bt = b * KK + t;
-      const int buf = bt & 1;
-      __syncthreads();  // buffer buf complete; buffer buf^1 free
-      if (bt + 1 < 3 * KK) stage(bt + 1, buf ^ 1);
-      const int ki = t / KS, kj = t % KS;
-      const int dh = (ki - r) * d, dw = (kj - r) * d;
-      const E* __restrict__ src = ws + buf * (M::P * PART);
-#pragma unroll
-      for (int blk = 0; blk < kBwdNB; ++blk) {
-        const int gh = h0 + wave * kBwdRPW + blk / kBwdCPW;
-        const int gw = w0 + (blk % kBwdCPW) * 16 + col16;
-        const int nh = gh + dh, nw = gw + dw;
-        const bool ok = gh < g.H && gw < g.W && (unsigned)nh < (unsigned)g.H &&
-                        (unsigned)nw < (unsigned)g.W;
-        const int64_t np = (int64_t)nh * g.W + nw;
-        V bfrag[KSTEPS][M::P];
-#pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
-          float v[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int c = 32 * kk + 8 * quad + e;
-            v[e] = (ok && c < C) ? gv[blk][kk][e] * to_f(xn[(int64_t)c * HW + np]) : 0.f;
-          }
-          M::pack(v, bfrag[kk]);
-        }
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-          for (int kk = 0; kk < KSTEPS; ++kk) {
-            V a[M::P];
-#pragma unroll
-            for (int pp = 0; pp < M::P; ++pp)
-              a[pp] = *reinterpret_cast<const V*>(src + pp * PART + (mb * 16 + col16) * LSTR +
-                                                  32 * kk + 8 * quad);
-            acc[blk][mb] = M::mac(a, bfrag[kk], acc[blk][mb]);
-          }
-        }
-      }
-    }
-  }
-
-#pragma unroll
-  for (int blk = 0; blk < kBwdNB; ++blk) {
-    const int gh = h0 + wave * kBwdRPW + blk / kBwdCPW;
-    const int gw = w0 + (blk % kBwdCPW) * 16 + col16;
-    if (gh < g.H && gw < g.W) {
-      T* __restrict__ yo = gy + (int64_t)n * C * HW + (int64_t)gh * g.W + gw;
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = mb * 16 + 4 * quad + e;
-          if (i < C) yo[(int64_t)i * HW] = from_f<T>(acc[blk][mb][e]);
-        }
-    }
-  }
-}
-
 namespace {
 
 template <typename F>
@@ -405,35 +264,6 @@ extern "C" int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bia
         hipLaunchKernelGGL((gen_bwd_x_kernel<T, KS, MB>), dim3((unsigned)((int64_t)g.N * g.tiles)),
                            dim3(kBwdThreads), lds, stream, (const T*)y, (const T*)weight,
                            (const T*)bias, (const T*)grad_out, (T*)grad_x, g);
-        return (int)hipGetLastError();
-      });
-    });
-  });
-}
-
-extern "C" int ddpm_gen_bwd_y(const void* x, const void* weight, const void* grad_out,
-                              void* grad_y, int64_t n, int64_t c, int64_t h, int64_t w,
-                              int kernel_size, int d0, int d1, int d2, int dtype,
-                              hipStream_t stream) {
-  if (dtype < kF32 || dtype > kF16) return kBadArgument;
-  GenGeom g;
-  int st = bwd_geom(g, n, c, h, w, kernel_size, d0, d1, d2);
-  if (st != kOk) return st;
-  if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
-  if (!x || !weight || !grad_out || !grad_y) return kBadArgument;
-  const int mb = (int)((c + 15) / 16);
-  return with_type(dtype, [&](auto tag) {
-    using T = decltype(tag);
-    return with_ks(kernel_size, [&](auto ks) {
-      constexpr int KS = decltype(ks)::value;
-      return with_mb(mb, [&](auto mbc) {
-        constexpr int MB = decltype(mbc)::value;
-        constexpr int KSTEPS = (MB + 1) / 2;
-        constexpr int LSTR = KSTEPS * 32 + 8;
-        const size_t lds = (size_t)2 * Mma<T>::P * MB * 16 * LSTR * 2;
-        hipLaunchKernelGGL((gen_bwd_y_kernel<T, KS, MB>), dim3((unsigned)((int64_t)g.N * g.tiles)),
-                           dim3(kBwdThreads), lds, stream, (const T*)x, (const T*)weight,
-                           (const T*)grad_out, (T*)grad_y, g);
         return (int)hipGetLastError();
       });
     });

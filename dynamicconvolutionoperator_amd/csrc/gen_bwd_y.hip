@@ -1,0 +1,384 @@
+// Gradient with respect to y of the fused op (recompute backward).
+//
+// Counterpart of _generator_dynamic_cat_bwd_y (_triton_kernels.py:534-623,
+// launched at :963-971):
+//
+//   dY[i, p] = sum_{b, t, c} W[(b,c,t), i] * dK[(b,c,t), p]
+//   dK[(b,c,t), p] = gO_b[c, p] * x[c, p + off(b,t)]
+//
+// A GEMM with M = i, N = pixels and K = (b, t, c) whose B operand dK is
+// formed on chip and never stored.  Work decomposition (CDNA4):
+//   * one workgroup per image-row segment of 256 pixels; 8 waves, two per
+//     SIMD, each owning 32 pixels (two MFMA column blocks) x all C i;
+//   * the K loop runs in stages (branch b, 32-channel chunk, tap row ki): a
+//     stage needs one x row (h + dh) of 32 channels, 256 + 16 columns, and
+//     the K-slice of the weight for its K taps; both are copied global -> LDS
+//     by buffer loads that write LDS directly (16-byte lanes; out-of-image
+//     reads return zero), one stage ahead into a second buffer;
+//   * the weight is pre-split (bf16 hi/lo for fp32) and pre-transposed by a
+//     small packing kernel into MFMA A-fragment order, so a fragment is one
+//     16-byte LDS read per lane;
+//   * MFMA slot k = 8*quad + e of a 32-channel chunk holds channel 4*e + quad
+//     (A and B alike): a lane's 8 B-operand reads are 4 channels apart, and
+//     with an x-row pitch of 16 (mod 64) dwords every read is bank-conflict
+//     free;
+//   * v_mfma_f32_16x16x32_{bf16,f16}; fp32 operands run as three bf16
+//     products (hi*hi + hi*lo + lo*hi).
+
+#include "gen_common.h"
+#include <type_traits>
+
+namespace ddpm {
+
+constexpr int kYtWaves = 8;
+constexpr int kYtThreads = 64 * kYtWaves;
+constexpr int kYtTW = 32 * kYtWaves;        // output columns per workgroup
+constexpr int kYtPad = 8;                   // staged column halo (>= dilation)
+constexpr int kYtLW = kYtTW + 2 * kYtPad;   // staged x columns (272)
+constexpr int kYtMaxDil = kYtPad;
+
+struct YGeom {
+  int N, C, H, W;
+  int d0, d1, d2;
+  int col_tiles;  // ceil(W / kYtTW)
+  int nc32;       // ceil(C / 32)
+  int x4;         // x rows can be copied in 16-byte lanes (W % 8 == 0, aligned base)
+};
+
+// Packed weight for the A fragments: 16-byte units
+//   [b][cc][t][ib][part][lane]   lane (i = ib*16 + (lane & 15), q = lane >> 4)
+// holding W[(b*C + c)*KK + t][i] for c = cc*32 + 4*e + q, e = 0..7.
+template <typename T>
+__host__ __device__ constexpr int yt_parts() {
+  return sizeof(T) == 4 ? 2 : 1;
+}
+
+template <typename T, int KS, int MB>
+__global__ __launch_bounds__(256) void gen_pack_wt_kernel(const T* __restrict__ wt,
+                                                          uint32_t* __restrict__ pk, int C,
+                                                          int nc32) {
+  constexpr int KK = KS * KS;
+  constexpr int P = yt_parts<T>();
+  const int total = 3 * nc32 * KK * MB * 64;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int lane = idx & 63;
+  int rest = idx >> 6;
+  const int ib = rest % MB;
+  rest /= MB;
+  const int t = rest % KK;
+  rest /= KK;
+  const int cc = rest % nc32;
+  const int b = rest / nc32;
+  const int i = ib * 16 + (lane & 15), q = lane >> 4;
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int c = cc * 32 + 4 * e + q;
+    v[e] = (i < C && c < C) ? to_f(wt[((int64_t)(b * C + c) * KK + t) * C + i]) : 0.f;
+  }
+  typename Mma<T>::V o[P];
+  Mma<T>::pack(v, o);
+  u32x4* __restrict__ dst = reinterpret_cast<u32x4*>(pk);
+  const int64_t unit = ((((int64_t)(b * nc32 + cc) * KK + t) * MB + ib) * P) * 64 + lane;
+#pragma unroll
+  for (int part = 0; part < P; ++part) dst[unit + part * 64] = __builtin_bit_cast(u32x4, o[part]);
+}
+
+// One LDS staging buffer (dwords): x rows [32 channels][kXS] then the
+// weight slice [KS taps][MB][P][64 lanes][4 dwords].
+template <typename T, int KS, int MB>
+struct YtLds {
+  static constexpr int kE = (int)sizeof(T);
+  static constexpr int kPerD = 4 / kE;
+  static constexpr int kXD = kYtLW / kPerD;                      // dwords per staged row
+  // pitch = 16 (mod 64) dwords for fp32 rows, 32 (mod 128) elements (16 mod 64
+  // dwords) for 2-byte rows; a multiple of 4 dwords (16-byte copies)
+  static constexpr int kXS = kXD + ((16 - kXD % 64) + 64) % 64;
+  static constexpr int kXChunks = kXD / 4;                       // 16-byte chunks per row
+  static constexpr int kXOff = 0;
+  static constexpr int kAOff = 32 * kXS;
+  static constexpr int kAUnits = KS * MB * yt_parts<T>() * 64;   // 16-byte units
+  static constexpr int kBuf = kAOff + 4 * kAUnits;
+};
+
+template <typename T, int KS, int MB>
+__global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restrict__ x,
+                                                               const uint32_t* __restrict__ pk,
+                                                               const T* __restrict__ gout,
+                                                               T* __restrict__ gy, YGeom g) {
+  typedef Mma<T> M;
+  typedef typename M::V V;
+  typedef YtLds<T, KS, MB> L;
+  constexpr int KK = KS * KS;
+  constexpr int r = KS / 2;
+  constexpr int P = M::P;
+  constexpr int E = (int)sizeof(T);
+  extern __shared__ __attribute__((aligned(16))) uint32_t ysm[];
+
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int row = tile / g.col_tiles;  // image row n*H + h
+  const int w0 = (tile - row * g.col_tiles) * kYtTW;
+  const int n = row / g.H, h = row - n * g.H;
+  const int C = g.C, H = g.H, W = g.W;
+  const int64_t HW = (int64_t)H * W;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int col16 = lane & 15, quad = lane >> 4;
+  const int nstage = 3 * g.nc32 * KS;  // (b, cc, ki)
+  const uint32_t row_bytes = (uint32_t)(W * E);
+
+  // ---- stage s = ((b * nc32) + cc) * KS + ki -> LDS buffer `buf`
+  auto stage = [&](int s, int buf) {
+    const int ki = s % KS;
+    const int bc = s / KS;
+    const int cc = bc % g.nc32, b = bc / g.nc32;
+    const int d = dil_of(b, g.d0, g.d1, g.d2);
+    const int hh = h + (ki - r) * d;
+    uint32_t* __restrict__ dstb = ysm + buf * L::kBuf;
+    // x rows: 32 channels of row hh, columns w0 - pad .. w0 + TW + pad
+    if (g.x4) {
+#pragma unroll
+      for (int j = 0; j < 32 / kYtWaves; ++j) {
+        const int cr = wave + kYtWaves * j;
+        const int ch = cc * 32 + cr;
+        const bool ok = ch < C && (unsigned)hh < (unsigned)H;
+        const BufRes res =
+            make_buf(ok ? x + ((int64_t)n * C + ch) * HW + (int64_t)hh * W : x, ok ? row_bytes : 0u);
+#pragma unroll
+        for (int part = 0; part < (L::kXChunks + 63) / 64; ++part) {
+          // the last copy ends at the row end (it may overlap the previous one)
+          const int pc = 64 * part < L::kXChunks - 64 ? 64 * part : (L::kXChunks > 64 ? L::kXChunks - 64 : 0);
+          if (L::kXChunks >= 64 || lane < L::kXChunks)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                res, (__attribute__((address_space(3))) void*)(dstb + L::kXOff + cr * L::kXS + 4 * pc),
+                16, (uint32_t)(w0 - kYtPad + (pc + lane) * 4 * L::kPerD) * (uint32_t)E, 0, 0, 0);
+        }
+      }
+    } else {
+      // element-wise copy through registers (W % 8 != 0 or unaligned x)
+      T* __restrict__ dst = reinterpret_cast<T*>(dstb);
+      for (int idx = tid; idx < 32 * kYtLW; idx += kYtThreads) {
+        const int cr = idx / kYtLW, j = idx - cr * kYtLW;
+        const int ch = cc * 32 + cr, gw = w0 - kYtPad + j;
+        float v = 0.f;
+        if (ch < C && (unsigned)hh < (unsigned)H && (unsigned)gw < (unsigned)W)
+          v = to_f(x[((int64_t)n * C + ch) * HW + (int64_t)hh * W + gw]);
+        dst[(L::kXOff + cr * L::kXS) * L::kPerD + j] = from_f<T>(v);
+      }
+    }
+    // weight slice of the stage's K taps: contiguous in the packed weight
+    const uint32_t* src = pk + (int64_t)((bc * KK + ki * KS) * MB * P * 64) * 4;
+    const BufRes pres = make_buf(src, (uint32_t)(L::kAUnits * 16));
+#pragma unroll
+    for (int j = 0; j < (L::kAUnits / 64 + kYtWaves - 1) / kYtWaves; ++j) {
+      const int u = wave + kYtWaves * j;
+      if ((L::kAUnits / 64) % kYtWaves == 0 || u < L::kAUnits / 64)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            pres, (__attribute__((address_space(3))) void*)(dstb + L::kAOff + 256 * u), 16,
+            (uint32_t)(u * 64 + lane) * 16u, 0, 0, 0);
+    }
+  };
+
+  // ---- branch-gradient values of this lane: channel cc*32 + 4e + quad at
+  //      its two pixels (held for the KS stages of one (b, cc))
+  const int px0 = 32 * wave + col16;  // pixel of block 0 within the tile; block 1 is +16
+  float gv[2][8];
+  auto load_g = [&](int bc) {
+    const int cc = bc % g.nc32, b = bc / g.nc32;
+    const BufRes gres = make_buf(gout + ((int64_t)n * 4 * C + (int64_t)(b + 1) * C) * HW,
+                                 (uint32_t)(C * HW * (int64_t)E));
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      const int w = w0 + px0 + 16 * blk;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int ch = cc * 32 + 4 * e + quad;
+        const uint32_t off = (ch < C && w < W) ? (uint32_t)((int64_t)ch * HW + (int64_t)h * W + w) * E : kOob;
+        gv[blk][e] = buf_load1<T>(gres, off);
+      }
+    }
+  };
+
+  f32x4 acc[2][MB];
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int ib = 0; ib < MB; ++ib) acc[blk][ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  stage(0, 0);
+  load_g(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int s = 0; s < nstage; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < nstage) stage(s + 1, buf ^ 1);
+    const int ki = s % KS;
+    const int bc = s / KS;
+    const int b = bc / g.nc32;
+    const int d = dil_of(b, g.d0, g.d1, g.d2);
+    const uint32_t* __restrict__ bb = ysm + buf * L::kBuf;
+    // this lane's x elements: channel 4e + quad, column pad + px + dw
+    const uint32_t* __restrict__ xq = bb + L::kXOff + quad * L::kXS;
+#pragma unroll
+    for (int kj = 0; kj < KS; ++kj) {
+      const int dw = (kj - r) * d;
+      V afr[MB][P];
+#pragma unroll
+      for (int ib = 0; ib < MB; ++ib)
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp)
+          afr[ib][pp] = __builtin_bit_cast(
+              V, *reinterpret_cast<const u32x4*>(bb + L::kAOff +
+                                                 4 * ((((kj * MB) + ib) * P + pp) * 64 + lane)));
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+        const int col = kYtPad + px0 + 16 * blk + dw;
+        float dk[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float xv;
+          if constexpr (sizeof(T) == 4)
+            xv = __uint_as_float(xq[4 * e * L::kXS + col]);
+          else
+            xv = to_f(reinterpret_cast<const T*>(xq + 4 * e * L::kXS)[col]);
+          dk[e] = gv[blk][e] * xv;
+        }
+        V bfr[P];
+        M::pack(dk, bfr);
+#pragma unroll
+        for (int ib = 0; ib < MB; ++ib) acc[blk][ib] = M::mac(afr[ib], bfr, acc[blk][ib]);
+      }
+    }
+    // the next (b, cc) needs new branch-gradient values
+    if (ki == KS - 1 && s + 1 < nstage) load_g(bc + 1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // ---- store: lane holds dY[i = ib*16 + 4*quad + e][pixel col16 of block]
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const int w = w0 + px0 + 16 * blk;
+    if (w < W) {
+      T* __restrict__ yo = gy + (int64_t)n * C * HW + (int64_t)h * W + w;
+#pragma unroll
+      for (int ib = 0; ib < MB; ++ib)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = ib * 16 + 4 * quad + e;
+          if (i < C) yo[(int64_t)i * HW] = from_f<T>(acc[blk][ib][e]);
+        }
+    }
+  }
+}
+
+namespace {
+
+template <typename F>
+int yt_with_type(int dt, F&& f) {
+  switch (dt) {
+    case kF32:
+      return f(float());
+    case kBF16:
+      return f(bf16());
+    case kF16:
+      return f(f16());
+    default:
+      return kBadArgument;
+  }
+}
+
+template <typename F>
+int yt_with_mb(int mb, F&& f) {
+  switch (mb) {
+    case 1:
+      return f(std::integral_constant<int, 1>());
+    case 2:
+      return f(std::integral_constant<int, 2>());
+    case 3:
+      return f(std::integral_constant<int, 3>());
+    case 4:
+      return f(std::integral_constant<int, 4>());
+    default:
+      return kUnsupported;
+  }
+}
+
+int64_t yt_pack_bytes(int64_t c, int k, int dtype) {
+  const int64_t nc32 = (c + 31) / 32, mb = (c + 15) / 16;
+  return 3 * nc32 * (int64_t)k * k * mb * (dtype == kF32 ? 2 : 1) * 64 * 16;
+}
+
+}  // namespace
+}  // namespace ddpm
+
+using namespace ddpm;
+
+extern "C" int64_t ddpm_gen_bwd_y_workspace_bytes(int64_t c, int kernel_size) {
+  if (c <= 0 || c > 64 || kernel_size < 1) return 0;
+  return yt_pack_bytes(c, kernel_size, kF32);
+}
+
+extern "C" int ddpm_gen_bwd_y(const void* x, const void* weight, const void* grad_out,
+                              void* grad_y, void* workspace, int64_t workspace_bytes, int64_t n,
+                              int64_t c, int64_t h, int64_t w, int kernel_size, int d0, int d1,
+                              int d2, int dtype, hipStream_t stream) {
+  if (dtype < kF32 || dtype > kF16) return kBadArgument;
+  GenGeom gg;
+  int st = gen_make_geom(gg, n, c, h, w, kernel_size, d0, d1, d2);
+  if (st != kOk) return st;
+  if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
+  if (!x || !weight || !grad_out || !grad_y) return kBadArgument;
+  if (d0 > kYtMaxDil || d1 > kYtMaxDil || d2 > kYtMaxDil) return kUnsupported;
+  // 32-bit buffer offsets inside one image's [C][H][W] planes
+  if (c * h * w * (dtype == kF32 ? 4 : 2) > 0x7fffffffLL) return kUnsupported;
+  const int64_t need = yt_pack_bytes(c, kernel_size, dtype);
+  if (!workspace || workspace_bytes < need) return kWorkspaceTooSmall;
+  YGeom g;
+  g.N = (int)n;
+  g.C = (int)c;
+  g.H = (int)h;
+  g.W = (int)w;
+  g.d0 = d0;
+  g.d1 = d1;
+  g.d2 = d2;
+  g.col_tiles = (int)((w + kYtTW - 1) / kYtTW);
+  g.nc32 = (int)((c + 31) / 32);
+  const size_t esz = dtype == kF32 ? 4 : 2;
+  g.x4 = (w % 8 == 0) && ((uintptr_t)x % 16 == 0);
+  (void)esz;
+  const int64_t tiles = n * h * g.col_tiles;
+  if (tiles > 0x7fffffffLL) return kUnsupported;
+  const int mb = (int)((c + 15) / 16);
+  return yt_with_type(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    return yt_with_mb(mb, [&](auto mbc) {
+      constexpr int MB = decltype(mbc)::value;
+      auto launch = [&](auto ks) {
+        constexpr int KS = decltype(ks)::value;
+        typedef YtLds<T, KS, MB> L;
+        const int units = 3 * g.nc32 * KS * KS * MB * 64;
+        hipLaunchKernelGGL((gen_pack_wt_kernel<T, KS, MB>), dim3((units + 255) / 256), dim3(256), 0,
+                           stream, (const T*)weight, (uint32_t*)workspace, (int)c, g.nc32);
+        int e = (int)hipGetLastError();
+        if (e != 0) return e;
+        const size_t lds = (size_t)2 * L::kBuf * 4;
+        if (lds > 64 * 1024) {
+          const hipError_t ae = hipFuncSetAttribute(
+              reinterpret_cast<const void*>(&gen_bwd_y_kernel<T, KS, MB>),
+              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+          if (ae != hipSuccess) return (int)ae;
+        }
+        hipLaunchKernelGGL((gen_bwd_y_kernel<T, KS, MB>), dim3((unsigned)tiles), dim3(kYtThreads), lds,
+                           stream, (const T*)x, (const uint32_t*)workspace, (const T*)grad_out,
+                           (T*)grad_y, g);
+        return (int)hipGetLastError();
+      };
+      if (kernel_size == 1) return launch(std::integral_constant<int, 1>());
+      if (kernel_size == 3) return launch(std::integral_constant<int, 3>());
+      return (int)kUnsupported;
+    });
+  });
+}

@@ -207,9 +207,11 @@ class _GeneratorDynamicCat(torch.autograd.Function):
                 )
             if ctx.needs_input_grad[1]:
                 grad_y = torch.empty_like(y)
+                wsy_bytes = int(lib.ddpm_gen_bwd_y_workspace_bytes(c, k))
+                wsy = torch.empty(wsy_bytes, dtype=torch.uint8, device=x.device)
                 _lib.check(
-                    lib.ddpm_gen_bwd_y(_ptr(x), _ptr(weight), _ptr(grad_out), _ptr(grad_y), n, c,
-                                       h, w, k, *dil, dt, stream),
+                    lib.ddpm_gen_bwd_y(_ptr(x), _ptr(weight), _ptr(grad_out), _ptr(grad_y),
+                                       _ptr(wsy), wsy_bytes, n, c, h, w, k, *dil, dt, stream),
                     "ddpm_gen_bwd_y",
                 )
             if ctx.needs_input_grad[2] or ctx.needs_input_grad[3]:

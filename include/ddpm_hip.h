@@ -89,11 +89,19 @@ int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bias, const vo
                    void* grad_x, int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size,
                    int d0, int d1, int d2, int dtype, hipStream_t stream);
 
+/* Bytes of workspace ddpm_gen_bwd_y needs for its packed copy of the weight
+ * (bf16 hi/lo split, MFMA fragment order); valid for every dtype.
+ * Part of the launch set-up of _GeneratorDynamicCat.backward (_triton_kernels.py:963-971). */
+int64_t ddpm_gen_bwd_y_workspace_bytes(int64_t c, int kernel_size);
+
 /* grad_y = weight^T . dK with dK = grad_out[branch] * shifted x formed on chip.
+ * `workspace` (at least ddpm_gen_bwd_y_workspace_bytes) receives the packed
+ * weight; the call overwrites it.
  * Replaces _generator_dynamic_cat_bwd_y (_triton_kernels.py:534-623, launched at :963-971). */
-int ddpm_gen_bwd_y(const void* x, const void* weight, const void* grad_out, void* grad_y, int64_t n,
-                   int64_t c, int64_t h, int64_t w, int kernel_size, int d0, int d1, int d2,
-                   int dtype, hipStream_t stream);
+int ddpm_gen_bwd_y(const void* x, const void* weight, const void* grad_out, void* grad_y,
+                   void* workspace, int64_t workspace_bytes, int64_t n, int64_t c, int64_t h,
+                   int64_t w, int kernel_size, int d0, int d1, int d2, int dtype,
+                   hipStream_t stream);
 
 /* Bytes of fp32 workspace ddpm_gen_bwd_w needs for its split partials
  * (0 when it writes grad_weight / grad_bias directly).
