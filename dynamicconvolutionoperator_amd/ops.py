@@ -200,11 +200,15 @@ class _GeneratorDynamicCat(torch.autograd.Function):
         with torch.cuda.device(x.device):
             if ctx.needs_input_grad[0]:
                 grad_x = torch.empty_like(x)
+                wsx_bytes = int(lib.ddpm_gen_bwd_x_workspace_bytes(n, c, h, w, k))
+                wsx = torch.empty(wsx_bytes, dtype=torch.uint8, device=x.device)
                 _lib.check(
                     lib.ddpm_gen_bwd_x(_ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
-                                       _ptr(grad_x), n, c, h, w, k, *dil, dt, stream),
+                                       _ptr(grad_x), _ptr(wsx), wsx_bytes, n, c, h, w, k, *dil,
+                                       dt, stream),
                     "ddpm_gen_bwd_x",
                 )
+                del wsx
             if ctx.needs_input_grad[1]:
                 grad_y = torch.empty_like(y)
                 wsy_bytes = int(lib.ddpm_gen_bwd_y_workspace_bytes(c, k))

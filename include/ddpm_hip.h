@@ -83,11 +83,18 @@ int ddpm_gen_fwd(const void* x, const void* y, const void* weight, const void* b
                  int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size, int d0, int d1,
                  int d2, int dtype, hipStream_t stream);
 
+/* Bytes of workspace ddpm_gen_bwd_x needs: its packed weight and a
+ * channel-innermost (bf16 hi/lo for fp32) copy of y; valid for every dtype.
+ * Part of the launch set-up of _GeneratorDynamicCat.backward (_triton_kernels.py:944-961). */
+int64_t ddpm_gen_bwd_x_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size);
+
 /* grad_x of the fused op, recomputing the generator at the gathered pixels.
+ * `workspace` (at least ddpm_gen_bwd_x_workspace_bytes) is overwritten.
  * Replaces _generator_dynamic_cat_bwd_x (_triton_kernels.py:430-531, launched at :944-961). */
 int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bias, const void* grad_out,
-                   void* grad_x, int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size,
-                   int d0, int d1, int d2, int dtype, hipStream_t stream);
+                   void* grad_x, void* workspace, int64_t workspace_bytes, int64_t n, int64_t c,
+                   int64_t h, int64_t w, int kernel_size, int d0, int d1, int d2, int dtype,
+                   hipStream_t stream);
 
 /* Bytes of workspace ddpm_gen_bwd_y needs for its packed copy of the weight
  * (bf16 hi/lo split, MFMA fragment order); valid for every dtype.
