@@ -148,6 +148,18 @@ struct VecIO {
       for (int e = 0; e < VEC; ++e) v[e] = to_f(t[e]);
     }
   }
+  // Non-temporal variant for data read exactly once (streamed kernel planes):
+  // keeps them from displacing reused lines in L2 / MALL.
+  static __device__ __forceinline__ void load_nt(const T* p, float (&v)[VEC]) {
+    if constexpr (VEC == 1) {
+      v[0] = to_f(__builtin_nontemporal_load(p));
+    } else {
+      typedef T TV __attribute__((ext_vector_type(VEC)));
+      const TV t = __builtin_nontemporal_load(reinterpret_cast<const TV*>(p));
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[e] = to_f(t[e]);
+    }
+  }
   static __device__ __forceinline__ void store(T* p, const float (&v)[VEC]) {
     if constexpr (VEC == 1) {
       p[0] = from_f<T>(v[0]);

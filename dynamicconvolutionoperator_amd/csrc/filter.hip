@@ -1,15 +1,21 @@
 // Materialized dynamic dilated depthwise filter: forward, dX and dK.
 //
 // Counterparts of the reference's _dynamic_cat_fwd / _dynamic_cat_bwd_x /
-// _dynamic_cat_bwd_k (_triton_kernels.py:21-254), redesigned for CDNA4:
-//   * one workgroup = one (n, c) plane x one spatial tile of TH rows x TW cols;
-//   * the x (or branch-gradient) tile plus a halo of R = (K/2)*max(d) is staged
-//     once in LDS, so all three dilations read neighbours from LDS, zero padded;
-//   * the 3*K*K kernel planes stream through with VEC-wide coalesced loads
-//     (16 B per lane for fp32 when W % 4 == 0), FP32 accumulation;
-//   * outputs [x, d0, d1, d2] are written directly (no Unfold buffers).
-// All three kernels move HBM bytes proportional to (3K^2 + 5) planes and are
-// bandwidth bound.
+// _dynamic_cat_bwd_k (_triton_kernels.py:21-254), redesigned for CDNA4.  All
+// three are HBM-bandwidth bound (they move 3*K*K + 4 or + 5 planes):
+//   * one workgroup = one (n, c) plane x a tile of image rows (4 waves);
+//   * the plane the dilated taps read (x for the forward and dK, the three
+//     branch gradients for dX) is staged with its halo of R = (K/2)*max(d) in
+//     LDS as fp32, zero outside the image, so all dilations read it there;
+//   * forward / dK: a lane owns V consecutive pixels (16 bytes of kernel
+//     plane: V = 4 for fp32, 8 for 2-byte types) and streams its 3*K*K
+//     kernel planes with non-temporal vector loads issued before the x tile is
+//     staged; the LDS tile is stored phase-split (column j at phase j % V,
+//     index j / V) so each of a lane's V shifted reads is bank-conflict free;
+//   * dX is a gather (kernel planes read at the shifted source pixels): a lane
+//     owns one pixel in each of U column blocks of 64, so every load of a
+//     kernel plane is 64 consecutive elements;
+//   * FP32 accumulation; outputs written once, no Unfold buffers.
 
 #include "ddpm_common.h"
 
@@ -18,237 +24,323 @@ namespace ddpm {
 struct FilterGeom {
   int N, C, H, W, K;
   int d0, d1, d2;
-  int R;         // halo radius
-  int tpr_log2;  // log2(threads per tile row)
-  int TH, TW;    // tile rows / cols
+  int R;         // halo radius (rows and columns)
+  int CP;        // staged column pad: R rounded up to a multiple of V
+  int lpr_log2;  // log2(lanes per image row); rows per wave = 64 >> lpr_log2
+  int TH, TW;    // tile rows / columns
   int tiles_w, tiles;
-  int LH, LW;    // LDS tile rows / cols (TH + 2R, TW + 2R)
+  int LH;        // staged rows, TH + 2R
+  int PS;        // floats per phase of a staged row
+  int RS;        // floats per staged row (V * PS)
 };
 
 constexpr int kFilterThreads = 256;
-constexpr int kFilterMaxPasses = 4;  // tile height = rows per pass * passes
+constexpr int kFilterWaves = kFilterThreads / 64;
 
-// Stage plane[h0-R : h0+TH+R, w0-R : w0+TW+R] into LDS as fp32, zero outside
-// the image.  One wave per LDS row, lanes over columns (coalesced).
-template <typename T>
-__device__ __forceinline__ void stage_tile(float* __restrict__ s, const T* __restrict__ plane,
-                                           const FilterGeom& g, int h0, int w0) {
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  for (int i = wave; i < g.LH; i += kFilterThreads / 64) {
-    const int gh = h0 - g.R + i;
-    const bool row_ok = (unsigned)gh < (unsigned)g.H;
-    const T* __restrict__ src = plane + (int64_t)gh * g.W;
-    float* __restrict__ dst = s + i * g.LW;
-    for (int j = lane; j < g.LW; j += 64) {
-      const int gw = w0 - g.R + j;
-      float v = 0.f;
-      if (row_ok && (unsigned)gw < (unsigned)g.W) v = to_f(src[gw]);
-      dst[j] = v;
+template <typename T, int V>
+struct Vec {
+  typedef T type __attribute__((ext_vector_type(V)));
+};
+
+// V consecutive elements at byte offset `off` of a buffer as fp32 (zero when
+// the offset is past the end).
+template <typename T, int V>
+__device__ __forceinline__ void buf_loadv(BufRes r, uint32_t off, float (&v)[V]) {
+  constexpr int B = V * (int)sizeof(T);
+  if constexpr (B == 2 || B == 4) {
+    v[0] = buf_load1<T>(r, off);
+    if constexpr (V == 2) v[1] = buf_load1<T>(r, off + 2);
+  } else if constexpr (B == 8) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    const typename Vec<T, V>::type t = __builtin_bit_cast(typename Vec<T, V>::type, a);
+#pragma unroll
+    for (int e = 0; e < V; ++e) v[e] = to_f(t[e]);
+  } else if constexpr (B == 16) {
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    const typename Vec<T, V>::type t = __builtin_bit_cast(typename Vec<T, V>::type, a);
+#pragma unroll
+    for (int e = 0; e < V; ++e) v[e] = to_f(t[e]);
+  } else {
+    static_assert(B == 32, "unsupported vector width");
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16u, 0, 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = __uint_as_float(a[e]);
+      v[4 + e] = __uint_as_float(b[e]);
     }
   }
 }
 
-template <typename TX, typename TK, int KS, int VEC>
+// Stage plane[h0 - R .. h0 + TH + R) x [w0 - CP .. w0 + TW + CP) into LDS as
+// fp32 (zero outside the image), phase-split by V.  Items are (row, V-wide
+// column group); W % V == 0 so a group is inside or outside the image as a
+// whole.  Each thread issues a batch of branch-free buffer loads before
+// writing any of them, so the loads are in flight together.
+template <typename T, int V>
+__device__ __forceinline__ void stage_plane(float* __restrict__ s, const T* __restrict__ plane,
+                                            const FilterGeom& g, int h0, int w0) {
+  constexpr int NB = 8;
+  const int groups = (g.TW + 2 * g.CP) / V;
+  const int total = g.LH * groups;
+  const BufRes res = make_buf(plane, (uint32_t)((int64_t)g.H * g.W * (int64_t)sizeof(T)));
+  for (int base = 0; base < total; base += kFilterThreads * NB) {
+    float v[NB][V];
+    int dst[NB];
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int item = base + (int)threadIdx.x + kFilterThreads * k;
+      const int i = item / groups, m = item - i * groups;
+      const int gh = h0 - g.R + i, gc = w0 - g.CP + m * V;
+      const bool ok = item < total && (unsigned)gh < (unsigned)g.H && gc >= 0 && gc < g.W;
+      buf_loadv<T, V>(res, ok ? (uint32_t)((int64_t)gh * g.W + gc) * (uint32_t)sizeof(T) : kOob, v[k]);
+      dst[k] = item < total ? i * g.RS + m : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      if (dst[k] >= 0) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) s[dst[k] + e * g.PS] = v[k][e];
+      }
+    }
+  }
+}
+
+// Staged value at tile row `lrow` (0 = first staged row) and staged column j.
+template <int V>
+__device__ __forceinline__ float staged(const float* __restrict__ s, const FilterGeom& g, int lrow,
+                                        int j) {
+  if constexpr (V == 1) {
+    return s[lrow * g.RS + j];
+  } else {
+    return s[lrow * g.RS + (j & (V - 1)) * g.PS + (j / V)];
+  }
+}
+
+template <typename TX, typename TK, int KS, int V>
 __global__ __launch_bounds__(kFilterThreads) void filter_fwd_kernel(const TX* __restrict__ x,
                                                                       const TK* __restrict__ kern,
                                                                       TK* __restrict__ out,
                                                                       FilterGeom g) {
+  typedef typename Vec<TK, V>::type KV;
   extern __shared__ float xs[];
-  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int bid = blockIdx.x;
   const int plane = bid / g.tiles;
   const int tile = bid - plane * g.tiles;
   const int n = plane / g.C, c = plane - n * g.C;
   const int ty = tile / g.tiles_w, tx = tile - ty * g.tiles_w;
   const int h0 = ty * g.TH, w0 = tx * g.TW;
   const int64_t HW = (int64_t)g.H * g.W;
-
-  stage_tile<TX>(xs, x + (int64_t)plane * HW, g, h0, w0);
-  __syncthreads();
-
   const int K = KS > 0 ? KS : g.K;
   const int KK = K * K, r = K / 2;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int lpr = 1 << g.lpr_log2;
+  const int trow = wave * (64 >> g.lpr_log2) + (lane >> g.lpr_log2);
+  const int cl = lane & (lpr - 1);
+  const int gh = h0 + trow, gw = w0 + V * cl;
+  const bool active = gh < g.H && gw < g.W && trow < g.TH;
+  const int64_t p = (int64_t)gh * g.W + gw;
   const int64_t bstride = (int64_t)g.C * KK * HW;
-  const TK* __restrict__ kp = kern + ((int64_t)n * 3 * g.C + c) * KK * HW;
-  TK* __restrict__ op = out + ((int64_t)n * 4 * g.C + c) * HW;
-  const int64_t ostride = (int64_t)g.C * HW;
+  const TK* __restrict__ kp = kern + ((int64_t)n * 3 * g.C + c) * KK * HW + p;
 
-  const int tpr = 1 << g.tpr_log2;
-  const int tcol = (threadIdx.x & (tpr - 1)) * VEC;
-  const int rpp = kFilterThreads >> g.tpr_log2;
-  const int gw = w0 + tcol;
-  if (gw >= g.W) return;  // no barrier below
-  for (int trow = threadIdx.x >> g.tpr_log2; trow < g.TH; trow += rpp) {
-    const int gh = h0 + trow;
-    if (gh >= g.H) break;
-    const int64_t p = (int64_t)gh * g.W + gw;
-    const float* __restrict__ xc = xs + (trow + g.R) * g.LW + tcol + g.R;
-    float acc[3][VEC];
+  // K <= 3: all 3*K*K kernel vectors are requested before the x tile is
+  // staged, so the streamed loads overlap the staging
+  constexpr int PRE = (KS > 0 && KS <= 3) ? 3 * KS * KS : 1;
+  KV kpre[PRE];
+  if constexpr (KS > 0 && KS <= 3) {
+    if (active) {
 #pragma unroll
-    for (int b = 0; b < 3; ++b)
+      for (int b = 0; b < 3; ++b)
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) acc[b][v] = 0.f;
+        for (int t = 0; t < KS * KS; ++t)
+          kpre[b * KS * KS + t] =
+              __builtin_nontemporal_load(reinterpret_cast<const KV*>(kp + b * bstride + t * HW));
+    }
+  }
+  stage_plane<TX, V>(xs, x + (int64_t)plane * HW, g, h0, w0);
+  __syncthreads();
+  if (!active) return;  // no barrier below
+
+  TK* __restrict__ op = out + ((int64_t)n * 4 * g.C + c) * HW + p;
+  const int64_t ostride = (int64_t)g.C * HW;
+  const int jc = g.CP + V * cl;  // staged column of this lane's first pixel
+  {
+    float xv[V];
 #pragma unroll
-    for (int b = 0; b < 3; ++b) {
-      const int d = dil_of(b, g.d0, g.d1, g.d2);
-      const TK* __restrict__ kb = kp + b * bstride + p;
+    for (int v = 0; v < V; ++v) xv[v] = staged<V>(xs, g, trow + g.R, jc + v);
+    VecIO<TK, V>::store(op, xv);
+  }
 #pragma unroll
-      for (int ki = 0; ki < (KS > 0 ? KS : 1); ++ki) {
-        for (int kir = (KS > 0 ? ki : 0); kir < (KS > 0 ? ki + 1 : K); ++kir) {
-          const float* __restrict__ xr = xc + (kir - r) * d * g.LW;
+  for (int b = 0; b < 3; ++b) {
+    const int d = dil_of(b, g.d0, g.d1, g.d2);
+    float acc[V];
 #pragma unroll
-          for (int kj = 0; kj < (KS > 0 ? KS : 1); ++kj) {
-            for (int kjr = (KS > 0 ? kj : 0); kjr < (KS > 0 ? kj + 1 : K); ++kjr) {
-              float kv[VEC];
-              VecIO<TK, VEC>::load(kb + (int64_t)(kir * K + kjr) * HW, kv);
-              const float* __restrict__ xq = xr + (kjr - r) * d;
+    for (int v = 0; v < V; ++v) acc[v] = 0.f;
+    for (int ki = 0; ki < K; ++ki) {
+      const int lrow = trow + g.R + (ki - r) * d;
+      for (int kj = 0; kj < K; ++kj) {
+        const int t = ki * K + kj;
+        KV kv;
+        if constexpr (KS > 0 && KS <= 3)
+          kv = kpre[b * KS * KS + t];
+        else
+          kv = __builtin_nontemporal_load(reinterpret_cast<const KV*>(kp + b * bstride + t * HW));
+        const int j0 = jc + (kj - r) * d;
 #pragma unroll
-              for (int v = 0; v < VEC; ++v) acc[b][v] = fmaf(kv[v], xq[v], acc[b][v]);
-            }
-          }
-        }
+        for (int v = 0; v < V; ++v) acc[v] = fmaf(to_f(kv[v]), staged<V>(xs, g, lrow, j0 + v), acc[v]);
       }
     }
-    float xv[VEC];
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) xv[v] = xc[v];
-    VecIO<TK, VEC>::store(op + p, xv);
-#pragma unroll
-    for (int b = 0; b < 3; ++b) VecIO<TK, VEC>::store(op + (b + 1) * ostride + p, acc[b]);
+    VecIO<TK, V>::store(op + (b + 1) * ostride, acc);
   }
 }
 
-template <typename TX, typename TK, int KS, int VEC>
+template <typename TX, typename TK, int KS, int V>
 __global__ __launch_bounds__(kFilterThreads) void filter_bwd_k_kernel(const TX* __restrict__ x,
                                                                         const TK* __restrict__ gout,
                                                                         TK* __restrict__ gk,
                                                                         FilterGeom g) {
   extern __shared__ float xs[];
-  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int bid = blockIdx.x;
   const int plane = bid / g.tiles;
   const int tile = bid - plane * g.tiles;
   const int n = plane / g.C, c = plane - n * g.C;
   const int ty = tile / g.tiles_w, tx = tile - ty * g.tiles_w;
   const int h0 = ty * g.TH, w0 = tx * g.TW;
   const int64_t HW = (int64_t)g.H * g.W;
-
-  stage_tile<TX>(xs, x + (int64_t)plane * HW, g, h0, w0);
-  __syncthreads();
-
   const int K = KS > 0 ? KS : g.K;
   const int KK = K * K, r = K / 2;
-  const int64_t bstride = (int64_t)g.C * KK * HW;
-  TK* __restrict__ kp = gk + ((int64_t)n * 3 * g.C + c) * KK * HW;
-  const TK* __restrict__ gp = gout + ((int64_t)n * 4 * g.C + c) * HW;
-  const int64_t gstride = (int64_t)g.C * HW;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int lpr = 1 << g.lpr_log2;
+  const int trow = wave * (64 >> g.lpr_log2) + (lane >> g.lpr_log2);
+  const int cl = lane & (lpr - 1);
+  const int gh = h0 + trow, gw = w0 + V * cl;
+  const bool active = gh < g.H && gw < g.W && trow < g.TH;
+  const int64_t p = (int64_t)gh * g.W + gw;
 
-  const int tpr = 1 << g.tpr_log2;
-  const int tcol = (threadIdx.x & (tpr - 1)) * VEC;
-  const int rpp = kFilterThreads >> g.tpr_log2;
-  const int gw = w0 + tcol;
-  if (gw >= g.W) return;
-  for (int trow = threadIdx.x >> g.tpr_log2; trow < g.TH; trow += rpp) {
-    const int gh = h0 + trow;
-    if (gh >= g.H) break;
-    const int64_t p = (int64_t)gh * g.W + gw;
-    const float* __restrict__ xc = xs + (trow + g.R) * g.LW + tcol + g.R;
-    float go[3][VEC];
+  // branch gradients at this lane's pixels, requested before staging x
+  const TK* __restrict__ gp = gout + ((int64_t)n * 4 * g.C + c) * HW + p;
+  const int64_t gstride = (int64_t)g.C * HW;
+  float go[3][V];
+  if (active) {
 #pragma unroll
-    for (int b = 0; b < 3; ++b) VecIO<TK, VEC>::load(gp + (b + 1) * gstride + p, go[b]);
+    for (int b = 0; b < 3; ++b) VecIO<TK, V>::load(gp + (b + 1) * gstride, go[b]);
+  }
+  stage_plane<TX, V>(xs, x + (int64_t)plane * HW, g, h0, w0);
+  __syncthreads();
+  if (!active) return;
+
+  const int64_t bstride = (int64_t)g.C * KK * HW;
+  TK* __restrict__ kp = gk + ((int64_t)n * 3 * g.C + c) * KK * HW + p;
+  const int jc = g.CP + V * cl;
 #pragma unroll
-    for (int b = 0; b < 3; ++b) {
-      const int d = dil_of(b, g.d0, g.d1, g.d2);
-      TK* __restrict__ kb = kp + b * bstride + p;
+  for (int b = 0; b < 3; ++b) {
+    const int d = dil_of(b, g.d0, g.d1, g.d2);
+    for (int ki = 0; ki < K; ++ki) {
+      const int lrow = trow + g.R + (ki - r) * d;
+      for (int kj = 0; kj < K; ++kj) {
+        const int j0 = jc + (kj - r) * d;
+        float prod[V];
 #pragma unroll
-      for (int ki = 0; ki < (KS > 0 ? KS : 1); ++ki) {
-        for (int kir = (KS > 0 ? ki : 0); kir < (KS > 0 ? ki + 1 : K); ++kir) {
-          const float* __restrict__ xr = xc + (kir - r) * d * g.LW;
-#pragma unroll
-          for (int kj = 0; kj < (KS > 0 ? KS : 1); ++kj) {
-            for (int kjr = (KS > 0 ? kj : 0); kjr < (KS > 0 ? kj + 1 : K); ++kjr) {
-              const float* __restrict__ xq = xr + (kjr - r) * d;
-              float prod[VEC];
-#pragma unroll
-              for (int v = 0; v < VEC; ++v) prod[v] = go[b][v] * xq[v];
-              VecIO<TK, VEC>::store(kb + (int64_t)(kir * K + kjr) * HW, prod);
-            }
-          }
-        }
+        for (int v = 0; v < V; ++v) prod[v] = go[b][v] * staged<V>(xs, g, lrow, j0 + v);
+        VecIO<TK, V>::store(kp + b * bstride + (int64_t)(ki * K + kj) * HW, prod);
       }
     }
   }
 }
 
 // dX[c,q] = gO_x[c,q] + sum_b sum_tap k_b[c,tap,q-off] * gO_b[c,q-off]   (gather form)
-// The three branch-gradient tiles (+halo) are staged together in LDS; the
-// kernel planes are gathered at the shifted source pixels.
-template <typename TX, typename TK, int KS, int VEC>
+// The three branch-gradient tiles (+ halo) are staged together in LDS (V = 1
+// layout); the kernel planes are read at the shifted source pixels.  A lane
+// owns pixel lane + 64*u of its row for u < U.
+template <typename TX, typename TK, int KS, int U>
 __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_kernel(const TK* __restrict__ gout,
                                                                         const TK* __restrict__ kern,
                                                                         TX* __restrict__ gx,
                                                                         FilterGeom g) {
   extern __shared__ float gs[];
-  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int bid = blockIdx.x;
   const int plane = bid / g.tiles;
   const int tile = bid - plane * g.tiles;
   const int n = plane / g.C, c = plane - n * g.C;
   const int ty = tile / g.tiles_w, tx = tile - ty * g.tiles_w;
   const int h0 = ty * g.TH, w0 = tx * g.TW;
   const int64_t HW = (int64_t)g.H * g.W;
-
   const int K = KS > 0 ? KS : g.K;
   const int KK = K * K, r = K / 2;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int lpr = 1 << g.lpr_log2;  // lanes per row; lane pixels are lpr apart
+  const int trow = wave * (64 >> g.lpr_log2) + (lane >> g.lpr_log2);
+  const int cl = lane & (lpr - 1);
+  const int gh = h0 + trow;
+  const bool row_active = gh < g.H && trow < g.TH;
+
   const int64_t bstride = (int64_t)g.C * KK * HW;
   const TK* __restrict__ kp = kern + ((int64_t)n * 3 * g.C + c) * KK * HW;
   const TK* __restrict__ gp = gout + ((int64_t)n * 4 * g.C + c) * HW;
   const int64_t gstride = (int64_t)g.C * HW;
-  const int lplane = g.LH * g.LW;
+  const int lplane = g.LH * g.RS;
 
+  // kernel values at the gathered source pixels, requested before the
+  // branch-gradient tiles are staged (one image row of a tap's plane per
+  // resource: columns outside it read zero)
+  constexpr int NT = KS > 0 ? 3 * KS * KS : 1;
+  float kvs[KS > 0 ? NT : 1][U];
+  auto load_k = [&](int b, int ki, int kj, float (&kv)[U]) {
+    const int d = dil_of(b, g.d0, g.d1, g.d2);
+    const int dh = (ki - r) * d, dw = (kj - r) * d;
+    const int sh = gh - dh;
+    const bool sh_ok = row_active && (unsigned)sh < (unsigned)g.H;
+    const TK* kt = kp + b * bstride + (int64_t)(ki * K + kj) * HW;
+    const BufRes res = make_buf(sh_ok ? kt + (int64_t)sh * g.W : kt, sh_ok ? (uint32_t)(g.W * sizeof(TK)) : 0u);
 #pragma unroll
-  for (int b = 0; b < 3; ++b) stage_tile<TK>(gs + b * lplane, gp + (b + 1) * gstride, g, h0, w0);
+    for (int u = 0; u < U; ++u)
+      kv[u] = buf_load1<TK>(res, (uint32_t)(w0 + cl + lpr * u - dw) * (uint32_t)sizeof(TK));
+  };
+  if constexpr (KS > 0) {
+#pragma unroll
+    for (int b = 0; b < 3; ++b)
+#pragma unroll
+      for (int t = 0; t < KS * KS; ++t) load_k(b, t / KS, t % KS, kvs[b * KS * KS + t]);
+  }
+#pragma unroll
+  for (int b = 0; b < 3; ++b) stage_plane<TK, 1>(gs + b * lplane, gp + (b + 1) * gstride, g, h0, w0);
   __syncthreads();
+  if (!row_active) return;
 
-  const int tpr = 1 << g.tpr_log2;
-  const int tcol = (threadIdx.x & (tpr - 1)) * VEC;
-  const int rpp = kFilterThreads >> g.tpr_log2;
-  const int gw = w0 + tcol;
-  if (gw >= g.W) return;
-  TX* __restrict__ xo = gx + (int64_t)plane * HW;
-  for (int trow = threadIdx.x >> g.tpr_log2; trow < g.TH; trow += rpp) {
-    const int gh = h0 + trow;
-    if (gh >= g.H) break;
-    const int64_t p = (int64_t)gh * g.W + gw;
-    float acc[VEC];
-    VecIO<TK, VEC>::load(gp + p, acc);
+  float acc[U];
 #pragma unroll
-    for (int b = 0; b < 3; ++b) {
-      const int d = dil_of(b, g.d0, g.d1, g.d2);
-      const TK* __restrict__ kb = kp + b * bstride;
-      const float* __restrict__ gc = gs + b * lplane + (trow + g.R) * g.LW + tcol + g.R;
+  for (int u = 0; u < U; ++u) {
+    const int gw = w0 + cl + lpr * u;
+    acc[u] = (gw < g.W) ? to_f(gp[(int64_t)gh * g.W + gw]) : 0.f;
+  }
 #pragma unroll
-      for (int ki = 0; ki < (KS > 0 ? KS : 1); ++ki) {
-        for (int kir = (KS > 0 ? ki : 0); kir < (KS > 0 ? ki + 1 : K); ++kir) {
-          const int sh = gh - (kir - r) * d;  // source row of the gathered term
-          const bool sh_ok = (unsigned)sh < (unsigned)g.H;
-          const float* __restrict__ gr = gc - (kir - r) * d * g.LW;
+  for (int b = 0; b < 3; ++b) {
+    const int d = dil_of(b, g.d0, g.d1, g.d2);
+    const float* __restrict__ gb = gs + b * lplane;
+    for (int ki = 0; ki < K; ++ki) {
+      const int dh = (ki - r) * d;
+      const int lrow = trow + g.R - dh;
+      for (int kj = 0; kj < K; ++kj) {
+        const int dw = (kj - r) * d;
+        float kv[U];
+        if constexpr (KS > 0) {
 #pragma unroll
-          for (int kj = 0; kj < (KS > 0 ? KS : 1); ++kj) {
-            for (int kjr = (KS > 0 ? kj : 0); kjr < (KS > 0 ? kj + 1 : K); ++kjr) {
-              const int dw = (kjr - r) * d;
-              const TK* __restrict__ kt = kb + (int64_t)(kir * K + kjr) * HW + (int64_t)sh * g.W;
-#pragma unroll
-              for (int v = 0; v < VEC; ++v) {
-                const int sw = gw + v - dw;
-                float kv = 0.f;
-                if (sh_ok && (unsigned)sw < (unsigned)g.W) kv = to_f(kt[sw]);
-                acc[v] = fmaf(kv, gr[v - dw], acc[v]);
-              }
-            }
-          }
+          for (int u = 0; u < U; ++u) kv[u] = kvs[(b * K + ki) * K + kj][u];
+        } else {
+          load_k(b, ki, kj, kv);
         }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          acc[u] = fmaf(kv[u], gb[lrow * g.RS + g.CP + cl + lpr * u - dw], acc[u]);
       }
     }
-    VecIO<TX, VEC>::store(xo + p, acc);
+  }
+  TX* __restrict__ xo = gx + (int64_t)plane * HW + (int64_t)gh * g.W;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int gw = w0 + cl + lpr * u;
+    if (gw < g.W) xo[gw] = from_f<TX>(acc[u]);
   }
 }
 
@@ -268,13 +360,15 @@ int ilog2(int v) {
   return l;
 }
 
-constexpr size_t kFilterMaxLds = 64 * 1024;
+constexpr size_t kFilterMaxLds = 160 * 1024;
 
+// Tiling for a lane width of `lw` pixels (V consecutive, or U strided) and
+// `planes` staged planes.
 int make_geom(FilterGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int k, int d0, int d1,
-              int d2, int vec, int lds_planes) {
+              int d2, int vec, int lw, int planes) {
   if (n < 0 || c < 0 || h < 0 || w < 0) return kBadArgument;
   if (k < 1 || (k % 2) == 0 || d0 < 1 || d1 < 1 || d2 < 1) return kBadArgument;
-  if (c > (1 << 24) || h > (1 << 20) || w > (1 << 20) || h * w > (int64_t)1 << 31) return kUnsupported;
+  if (c > (1 << 24) || h > (1 << 20) || w > (1 << 20) || h * w > ((int64_t)1 << 29)) return kUnsupported;
   g.N = (int)n;
   g.C = (int)c;
   g.H = (int)h;
@@ -285,26 +379,20 @@ int make_geom(FilterGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int k, 
   g.d2 = d2;
   int dmax = d0 > d1 ? d0 : d1;
   dmax = dmax > d2 ? dmax : d2;
+  if ((int64_t)(k / 2) * dmax > 4096) return kUnsupported;
   g.R = (k / 2) * dmax;
-  const int tpc = (int)((w + vec - 1) / vec);
-  int tpr = pow2ceil(tpc);
-  if (tpr > 64) tpr = 64;
-  g.tpr_log2 = ilog2(tpr);
-  g.TW = tpr * vec;
-  const int rpp = kFilterThreads / tpr;
-  int passes = 16 / rpp;
-  if (passes < 1) passes = 1;
-  if (passes > kFilterMaxPasses) passes = kFilterMaxPasses;
-  // Do not make tiles taller than the image needs.
-  while (passes > 1 && rpp * (passes - 1) >= h) --passes;
-  for (;;) {
-    g.TH = rpp * passes;
-    g.LH = g.TH + 2 * g.R;
-    g.LW = g.TW + 2 * g.R;
-    if ((size_t)lds_planes * g.LH * g.LW * sizeof(float) <= kFilterMaxLds) break;
-    if (passes == 1) return kUnsupported;
-    --passes;
-  }
+  g.CP = (g.R + vec - 1) / vec * vec;
+  int lpr = pow2ceil((int)((w + lw - 1) / lw));
+  if (lpr > 64) lpr = 64;
+  g.lpr_log2 = ilog2(lpr);
+  g.TW = lpr * lw;
+  g.TH = kFilterWaves * (64 / lpr);  // each wave covers 64 / lpr image rows
+  g.LH = g.TH + 2 * g.R;
+  const int cols = g.TW + 2 * g.CP;
+  g.PS = (cols + vec - 1) / vec;
+  if (vec > 1) g.PS += ((64 / vec) - g.PS % 64 + 64) % 64;  // phases 64/V banks apart
+  g.RS = vec * g.PS;
+  if ((size_t)planes * g.LH * g.RS * sizeof(float) > kFilterMaxLds) return kUnsupported;
   g.tiles_w = (int)((w + g.TW - 1) / g.TW);
   const int tiles_h = (int)((h + g.TH - 1) / g.TH);
   g.tiles = g.tiles_w * tiles_h;
@@ -328,50 +416,55 @@ int with_type(int dt, F&& f) {
 
 enum class FilterOp { kFwd, kBwdX, kBwdK };
 
-template <typename TX, typename TK, int KS, int VEC>
-void launch_one(FilterOp op, const void* a, const void* b, void* o, const FilterGeom& g,
-                hipStream_t stream) {
-  const dim3 grid((unsigned)((int64_t)g.tiles * g.N * g.C));
-  const dim3 block(kFilterThreads);
-  const size_t lds = (size_t)(op == FilterOp::kBwdX ? 3 : 1) * g.LH * g.LW * sizeof(float);
+template <typename Kern, typename... Args>
+int launch_kernel(Kern kern, const FilterGeom& g, size_t lds, hipStream_t stream, Args... args) {
+  if (lds > 64 * 1024) {
+    const hipError_t ae = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (ae != hipSuccess) return (int)ae;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)((int64_t)g.tiles * g.N * g.C)), dim3(kFilterThreads), lds,
+                     stream, args...);
+  return (int)hipGetLastError();
+}
+
+template <typename TX, typename TK, int KS>
+int launch_ks(FilterOp op, const void* a, const void* b, void* o, const FilterGeom& g, int vec,
+              hipStream_t stream) {
+  const size_t lds1 = (size_t)g.LH * g.RS * sizeof(float);
   switch (op) {
     case FilterOp::kFwd:
-      hipLaunchKernelGGL((filter_fwd_kernel<TX, TK, KS, VEC>), grid, block, lds, stream,
-                         (const TX*)a, (const TK*)b, (TK*)o, g);
-      break;
+      if (vec == 8)
+        return launch_kernel(filter_fwd_kernel<TX, TK, KS, 8>, g, lds1, stream, (const TX*)a, (const TK*)b, (TK*)o, g);
+      if (vec == 4)
+        return launch_kernel(filter_fwd_kernel<TX, TK, KS, 4>, g, lds1, stream, (const TX*)a, (const TK*)b, (TK*)o, g);
+      return launch_kernel(filter_fwd_kernel<TX, TK, KS, 1>, g, lds1, stream, (const TX*)a, (const TK*)b, (TK*)o, g);
     case FilterOp::kBwdK:
-      hipLaunchKernelGGL((filter_bwd_k_kernel<TX, TK, KS, VEC>), grid, block, lds, stream,
-                         (const TX*)a, (const TK*)b, (TK*)o, g);
-      break;
+      if (vec == 8)
+        return launch_kernel(filter_bwd_k_kernel<TX, TK, KS, 8>, g, lds1, stream, (const TX*)a, (const TK*)b, (TK*)o, g);
+      if (vec == 4)
+        return launch_kernel(filter_bwd_k_kernel<TX, TK, KS, 4>, g, lds1, stream, (const TX*)a, (const TK*)b, (TK*)o, g);
+      return launch_kernel(filter_bwd_k_kernel<TX, TK, KS, 1>, g, lds1, stream, (const TX*)a, (const TK*)b, (TK*)o, g);
     case FilterOp::kBwdX:
-      hipLaunchKernelGGL((filter_bwd_x_kernel<TX, TK, KS, VEC>), grid, block, lds, stream,
-                         (const TK*)a, (const TK*)b, (TX*)o, g);
-      break;
+      if (vec == 4)
+        return launch_kernel(filter_bwd_x_kernel<TX, TK, KS, 4>, g, 3 * lds1, stream, (const TK*)a, (const TK*)b, (TX*)o, g);
+      return launch_kernel(filter_bwd_x_kernel<TX, TK, KS, 1>, g, 3 * lds1, stream, (const TK*)a, (const TK*)b, (TX*)o, g);
   }
+  return kBadArgument;
 }
 
 template <typename TX, typename TK>
-void launch_typed(FilterOp op, const void* a, const void* b, void* o, const FilterGeom& g, int vec,
-                  hipStream_t stream) {
-  if (vec == 4) {
-    switch (g.K) {
-      case 1:
-        return launch_one<TX, TK, 1, 4>(op, a, b, o, g, stream);
-      default:
-        return launch_one<TX, TK, 3, 4>(op, a, b, o, g, stream);
-    }
-  }
+int launch_typed(FilterOp op, const void* a, const void* b, void* o, const FilterGeom& g, int vec,
+                 hipStream_t stream) {
   switch (g.K) {
     case 1:
-      return launch_one<TX, TK, 1, 1>(op, a, b, o, g, stream);
+      return launch_ks<TX, TK, 1>(op, a, b, o, g, vec, stream);
     case 3:
-      return launch_one<TX, TK, 3, 1>(op, a, b, o, g, stream);
+      return launch_ks<TX, TK, 3>(op, a, b, o, g, vec, stream);
     case 5:
-      return launch_one<TX, TK, 5, 1>(op, a, b, o, g, stream);
-    case 7:
-      return launch_one<TX, TK, 7, 1>(op, a, b, o, g, stream);
+      return launch_ks<TX, TK, 5>(op, a, b, o, g, vec, stream);
     default:
-      return launch_one<TX, TK, 0, 1>(op, a, b, o, g, stream);
+      return launch_ks<TX, TK, 0>(op, a, b, o, g, vec, stream);
   }
 }
 
@@ -385,36 +478,30 @@ int run_filter(FilterOp op, const void* a, const void* b, void* o, int64_t n, in
   if (x_dtype < kF32 || x_dtype > kF16 || k_dtype < kF32 || k_dtype > kF16) return kBadArgument;
   if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
   if (!a || !b || !o) return kBadArgument;
-  // 4-wide vectors need W % 4 == 0 (so rows start aligned) and aligned bases
-  // for the streamed kernel / gradient / output planes; K <= 3 keeps the
-  // per-thread tap registers bounded.
-  const size_t kv = 4 * esize(k_dtype), xv = 4 * esize(x_dtype);
-  bool vec4 = (w % 4 == 0) && k <= 3;
-  switch (op) {
-    case FilterOp::kFwd:
-      vec4 = vec4 && aligned(b, kv) && aligned(o, kv);
-      break;
-    case FilterOp::kBwdK:
-      vec4 = vec4 && aligned(b, kv) && aligned(o, kv);
-      break;
-    case FilterOp::kBwdX:
-      vec4 = vec4 && aligned(a, kv) && aligned(o, xv);
-      break;
+  int vec = 1, lw = 1;
+  if (op == FilterOp::kBwdX) {
+    // gather: U = 4 pixels per lane, 64 lanes apart (K <= 3 keeps the
+    // in-flight kernel values within the register budget); unvectorized
+    vec = 1;
+    lw = (w >= 256 && k <= 3) ? 4 : 1;
+  } else {
+    // 16 bytes of kernel plane per lane where rows and bases allow it
+    const int v = k_dtype == kF32 ? 4 : 8;
+    // `a` is x for both; its V-wide groups are read as one vector
+    const bool ok = (w % v == 0) && aligned(b, 16) && aligned(o, 16) &&
+                    aligned(a, (size_t)v * esize(x_dtype));
+    if (ok) vec = lw = v;
   }
-  const int vec = vec4 ? 4 : 1;
   FilterGeom g;
-  int st = make_geom(g, n, c, h, w, k, d0, d1, d2, vec, op == FilterOp::kBwdX ? 3 : 1);
+  int st = make_geom(g, n, c, h, w, k, d0, d1, d2, vec, lw, op == FilterOp::kBwdX ? 3 : 1);
   if (st != kOk) return st;
-  st = with_type(x_dtype, [&](auto tx) {
+  return with_type(x_dtype, [&](auto tx) {
     using TX = decltype(tx);
     return with_type(k_dtype, [&](auto tk) {
       using TK = decltype(tk);
-      launch_typed<TX, TK>(op, a, b, o, g, vec, stream);
-      return (int)kOk;
+      return launch_typed<TX, TK>(op, a, b, o, g, op == FilterOp::kBwdX ? lw : vec, stream);
     });
   });
-  if (st != kOk) return st;
-  return (int)hipGetLastError();
 }
 
 }  // namespace
