@@ -1,5 +1,5 @@
 // Library-level C-ABI helpers: status strings, ABI version, support queries.
-#include "ddpm_common.h"
+#include "gen_common.h"
 
 using namespace ddpm;
 
@@ -23,11 +23,15 @@ extern "C" const char* ddpm_status_string(int code) {
 // 1 when the fused generator kernels (forward and recompute backward) handle
 // this channel count, kernel size and largest dilation, else 0 (the caller
 // then materializes the dynamic kernels and uses the ddpm_filter_* entry
-// points).  The forward's fp32 halo tile of (8+2R) x (32+2R) pixels x 16
-// channels, R = (K/2)*max_dilation, must fit 64 KB of LDS.
+// points).  The backward kernels stage a column halo of kGenMaxDil pixels,
+// and the forward's halo tile (16+2R) x (32+2R) pixels x 16 channels, R =
+// (K/2)*max_dilation, must fit the 160 KB of LDS of one workgroup.
 extern "C" int ddpm_gen_supported(int64_t c, int kernel_size, int max_dilation) {
   if (c < 1 || c > 64 || !(kernel_size == 1 || kernel_size == 3) || max_dilation < 1) return 0;
+  if (kernel_size == 1) return 1;
+  if (max_dilation > kGenMaxDil) return 0;
   const int64_t r = (int64_t)(kernel_size / 2) * max_dilation;
-  const int64_t lds = (8 + 2 * r) * (32 + 2 * r) * 16 * 4 + 3 * kernel_size * kernel_size * 16 * 4;
-  return lds <= 64 * 1024 ? 1 : 0;
+  const int64_t plane = ((16 + 2 * r) * (32 + 2 * r) * 4 * 4 + 255) / 256 * 256;
+  const int64_t lds = 4 * plane + 2 * 2 * 2 * 64 * 16 + 3 * kernel_size * kernel_size * 16 * 4;
+  return lds <= 160 * 1024 ? 1 : 0;
 }

@@ -197,6 +197,18 @@ __device__ __forceinline__ float buf_load1(BufRes r, uint32_t off) {
   }
 }
 
+// Buffer stores follow the same rule: a store at or beyond num_records is
+// dropped, so masked lanes write nothing without a branch.
+template <typename T>
+__device__ __forceinline__ void buf_store1(BufRes r, uint32_t off, float v) {
+  if constexpr (sizeof(T) == 4) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, from_f<T>(v)), r, off,
+                                          0, 0);
+  }
+}
+
 // 8 consecutive elements at byte offset `off` (16-byte aligned for 2-byte
 // types, 16-byte aligned pairs for fp32), converted to fp32.
 template <typename T>

@@ -495,12 +495,12 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
   if (st != kOk) return st;
   if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
   if (!x || !y || !grad_out || !grad_weight || !grad_bias) return kBadArgument;
-  if (d0 > kWgMaxDil || d1 > kWgMaxDil || d2 > kWgMaxDil) return kUnsupported;
+  if (gg.d0 > kWgMaxDil || gg.d1 > kWgMaxDil || gg.d2 > kWgMaxDil) return kUnsupported;
   if (n * h > 0x7fffffffLL / 4) return kUnsupported;
   // 32-bit buffer offsets inside one image's [C][H][W] planes
   if (((c + 15) / 16) * 16 * h * w * (dtype == kF32 ? 4 : 2) > 0x7fffffffLL) return kUnsupported;
   WGradGeom g;
-  wgrad_geom(g, n, c, h, w, d0, d1, d2);
+  wgrad_geom(g, n, c, h, w, gg.d0, gg.d1, gg.d2);
   const int64_t need = ddpm_gen_bwd_w_workspace_bytes(n, c, h, w, kernel_size);
   if (need > 0 && (!workspace || workspace_bytes < need)) return kWorkspaceTooSmall;
   const size_t esz = dtype == kF32 ? 4 : 2;

@@ -325,9 +325,9 @@ extern "C" int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bia
   g.C = (int)c;
   g.H = (int)h;
   g.W = (int)w;
-  g.d0 = d0;
-  g.d1 = d1;
-  g.d2 = d2;
+  g.d0 = gg.d0;
+  g.d1 = gg.d1;
+  g.d2 = gg.d2;
   g.tiles_w = (int)((w + kXtCols - 1) / kXtCols);
   g.tiles = g.tiles_w * (int)((h + kXtRows - 1) / kXtRows);
   g.cp = (int)xt_cp(c);

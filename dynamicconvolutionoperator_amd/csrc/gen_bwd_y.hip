@@ -331,7 +331,7 @@ extern "C" int ddpm_gen_bwd_y(const void* x, const void* weight, const void* gra
   if (st != kOk) return st;
   if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
   if (!x || !weight || !grad_out || !grad_y) return kBadArgument;
-  if (d0 > kYtMaxDil || d1 > kYtMaxDil || d2 > kYtMaxDil) return kUnsupported;
+  if (gg.d0 > kYtMaxDil || gg.d1 > kYtMaxDil || gg.d2 > kYtMaxDil) return kUnsupported;
   // 32-bit buffer offsets inside one image's [C][H][W] planes
   if (c * h * w * (dtype == kF32 ? 4 : 2) > 0x7fffffffLL) return kUnsupported;
   const int64_t need = yt_pack_bytes(c, kernel_size, dtype);
@@ -341,9 +341,9 @@ extern "C" int ddpm_gen_bwd_y(const void* x, const void* weight, const void* gra
   g.C = (int)c;
   g.H = (int)h;
   g.W = (int)w;
-  g.d0 = d0;
-  g.d1 = d1;
-  g.d2 = d2;
+  g.d0 = gg.d0;
+  g.d1 = gg.d1;
+  g.d2 = gg.d2;
   g.col_tiles = (int)((w + kYtTW - 1) / kYtTW);
   g.nc32 = (int)((c + 31) / 32);
   const size_t esz = dtype == kF32 ? 4 : 2;

@@ -1,4 +1,4 @@
-// Geometry shared by the fused generator kernels (forward and backward).
+// Shape validation shared by the fused generator kernels (forward and backward).
 #pragma once
 
 #include "ddpm_common.h"
@@ -10,14 +10,14 @@ struct GenGeom {
   int d0, d1, d2;
   int R;        // halo radius (K/2)*max(d)
   int cblocks;  // ceil(C/16)
-  int tiles_w, tiles;
-  int LH, LW;   // LDS tile dims of the forward
-  int wvec;     // weight rows can be read with 16-byte vector loads
 };
 
-// Validates the shape for the fused kernels (K in {1,3}, C <= 64) and fills
-// the forward tiling.  Returns kOk, kBadArgument or kUnsupported.
+// Validates the shape for the fused kernels (K in {1,3}, C <= 64, dilations
+// >= 1) and fills the geometry.  Returns kOk, kBadArgument or kUnsupported.
 int gen_make_geom(GenGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int k, int d0, int d1,
                   int d2);
+
+// Largest dilation the fused backward kernels stage (their column halo).
+constexpr int kGenMaxDil = 8;
 
 }  // namespace ddpm

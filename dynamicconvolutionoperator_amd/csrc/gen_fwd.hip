@@ -10,76 +10,84 @@
 // q() rounds the generated tap to the input dtype (bf16/f16), as the
 // reference does before consuming it (_triton_kernels.py:332-335).
 //
-// Work decomposition: one workgroup = (image n, 16-channel block, spatial
-// tile of TH=8 rows x TW=32 cols).  The generator is an MFMA GEMM with the
-// 16 output channels of one (branch, tap) as M, 16 pixels as N and the input
-// channels as K (v_mfma_f32_16x16x32_{bf16,f16}; fp32 runs as three bf16
-// products).  The y operand of each wave's 4 pixel blocks stays in registers
-// for all 3*K*K (branch, tap) products; the generated taps stay in the MFMA
-// result registers and are multiplied against the x halo tile held in LDS
-// (channel-innermost, swizzled), so no dynamic kernel ever reaches HBM.
+// One workgroup = (image n, 16-channel block, 16 x 32 pixel tile), 8 waves;
+// wave w owns tile rows 2w and 2w+1, i.e. four 16-pixel blocks.  The
+// generator is an MFMA GEMM per (branch, tap): M = the 16 channels, N = 16
+// pixels, K = the input channels (v_mfma_f32_16x16x32_{bf16,f16}; fp32 runs
+// as three bf16 products).  Operands:
+//   * y (B): each wave loads its four pixel blocks once and keeps them in
+//     registers for all 3*K*K products;
+//   * W (A): the 16 x C slice of one (branch, tap) is converted once per
+//     workgroup (fp32: split into bf16 hi/lo) into LDS in fragment order,
+//     double-buffered one tap ahead, and read by all 8 waves;
+//   * x: the halo tile (16+2R) x (32+2R) of the 16 channels sits in LDS as 4
+//     planes of 4-channel pixels, so the shifted read of one lane's 4 output
+//     channels is one ds_read_b128 (fp32) / ds_read_b64 (2-byte) whose
+//     address moves by a uniform offset per tap.
+// The generated taps never leave the MFMA result registers.  The identity
+// part of the concat is written from the registers that stage the halo tile.
+// Every global access is a raw buffer access; lanes outside the image or the
+// channel range use an offset past the resource's end (read as zero, write
+// dropped) instead of a branch.
 
 #include "gen_common.h"
+#include <type_traits>
 
 namespace ddpm {
 
-constexpr int kGenThreads = 256;
-constexpr int kGenRPW = 2;                 // tile rows per wave
-constexpr int kGenCPW = 2;                 // 16-pixel column blocks per wave
-constexpr int kGenTH = 4 * kGenRPW;        // tile rows
-constexpr int kGenTW = 16 * kGenCPW;       // tile cols
-constexpr int kGenNB = kGenRPW * kGenCPW;  // pixel blocks per wave
+constexpr int kGfWaves = 8;
+constexpr int kGfThreads = 64 * kGfWaves;
+constexpr int kGfTH = 2 * kGfWaves;  // tile rows, two per wave
+constexpr int kGfTW = 32;            // tile columns, two 16-pixel blocks
+constexpr int kGfMaxLds = 160 * 1024;
 
-// LDS swizzle of the 4-channel groups inside one pixel (conflict-free reads
-// of 4 consecutive channels by 16 consecutive pixels).
-template <typename T>
-__device__ __forceinline__ int gen_swz(int pix) {
-  return sizeof(T) == 4 ? ((pix >> 1) & 3) : ((pix >> 2) & 3);
+struct FwdGeom {
+  int N, C, H, W;
+  int d0, d1, d2;
+  int R;        // halo radius
+  int cblocks;  // ceil(C/16)
+  int tiles_w, tiles;
+  int LH, LW;   // halo tile rows / columns
+  int npix;     // LH * LW
+  int plane;    // bytes of one 4-channel plane of the halo tile (256-byte multiple)
+};
+
+// Raw element bits through a buffer resource (no conversion).
+template <int E>
+__device__ __forceinline__ uint32_t gf_load_raw(BufRes r, uint32_t off) {
+  if constexpr (E == 4)
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  else
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+template <int E>
+__device__ __forceinline__ void gf_store_raw(BufRes r, uint32_t off, uint32_t v) {
+  if constexpr (E == 4)
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
+  else
+    __builtin_amdgcn_raw_buffer_store_b16((unsigned short)v, r, off, 0, 0);
 }
 
-// Loads 8 consecutive weights W[o][k0 .. k0+7] as fp32 (zero past C or for
-// rows beyond C output channels).
-template <typename T>
-__device__ __forceinline__ void load_w8(const T* __restrict__ wt, int64_t o, bool row_ok, int k0,
-                                        int C, bool wvec, float (&v)[8]) {
-  const T* __restrict__ p = wt + o * C + k0;
-  if (row_ok && wvec && k0 + 8 <= C) {
-    if constexpr (sizeof(T) == 4) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[e] = a[e];
-        v[4 + e] = b[e];
-      }
-    } else {
-      typedef T T8 __attribute__((ext_vector_type(8)));
-      const T8 a = *reinterpret_cast<const T8*>(p);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = to_f(a[e]);
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = (row_ok && k0 + e < C) ? to_f(p[e]) : 0.f;
-  }
-}
-
-template <typename T, int KS, int KSTEPS>
-__global__ __launch_bounds__(kGenThreads) void gen_fwd_kernel(const T* __restrict__ x,
-                                                                const T* __restrict__ y,
-                                                                const T* __restrict__ wt,
-                                                                const T* __restrict__ bias,
-                                                                T* __restrict__ out, GenGeom g) {
+// amdgpu_waves_per_eu(4): 128 registers, so two 8-wave workgroups share a CU.
+template <typename T, int KS, int NK>
+__global__ __launch_bounds__(kGfThreads) __attribute__((amdgpu_waves_per_eu(4))) void gen_fwd_kernel(
+    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ wt,
+    const T* __restrict__ bias, T* __restrict__ out, FwdGeom g) {
   typedef Mma<T> M;
   typedef typename M::V V;
-  typedef T T4 __attribute__((ext_vector_type(4)));
+  constexpr int P = M::P;
   constexpr int KK = KS * KS;
+  constexpr int NBT = 3 * KK;         // (branch, tap) steps
   constexpr int r = KS / 2;
+  constexpr int E = (int)sizeof(T);
+  constexpr int XB = 4 * E;           // bytes of one 4-channel pixel entry
+  constexpr int AU = NK * P * 64;     // 16-byte units of one weight slice
+  typedef uint32_t XQ __attribute__((ext_vector_type(E)));  // one 4-channel entry
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const int npix = g.LH * g.LW;
-  T4* __restrict__ xs = reinterpret_cast<T4*>(smem);                    // [npix][4 groups]
-  float* __restrict__ bs = reinterpret_cast<float*>(smem + (size_t)npix * 4 * sizeof(T4));  // [3][KK][16]
+  unsigned char* __restrict__ xs = smem;                                   // [4][plane]
+  unsigned char* __restrict__ abuf = smem + 4 * g.plane;                   // [2][AU] x 16 B
+  float* __restrict__ bs = reinterpret_cast<float*>(abuf + 2 * AU * 16);  // [NBT][16]
 
   // Block -> (n, tile, channel block), channel block fastest.
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
@@ -88,127 +96,187 @@ __global__ __launch_bounds__(kGenThreads) void gen_fwd_kernel(const T* __restric
   const int tile = nt % g.tiles;
   const int n = nt / g.tiles;
   const int ty = tile / g.tiles_w, tx = tile - ty * g.tiles_w;
-  const int h0 = ty * kGenTH, w0 = tx * kGenTW;
-  const int C = g.C;
-  const int64_t HW = (int64_t)g.H * g.W;
+  const int h0 = ty * kGfTH, w0 = tx * kGfTW;
+  const int C = g.C, H = g.H, W = g.W, R = g.R, LW = g.LW;
+  const int64_t HW = (int64_t)H * W;
+  const uint32_t HWE = (uint32_t)HW * (uint32_t)E;  // bytes of one channel plane
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int col16 = lane & 15, quad = lane >> 4;
   const int c0 = cb * 16;
+  const int nch = C - c0 < 16 ? C - c0 : 16;
 
-  // ---- stage x tile (+halo, zero padded) for this channel block; copy the
-  //      interior to the identity channels of the output.
-  for (int grp = 0; grp < 4; ++grp) {
-    for (int pix = tid; pix < npix; pix += kGenThreads) {
-      const int i = pix / g.LW, j = pix - i * g.LW;
-      const int gh = h0 - g.R + i, gw = w0 - g.R + j;
-      const bool in_img = (unsigned)gh < (unsigned)g.H && (unsigned)gw < (unsigned)g.W;
-      const bool interior = i >= g.R && i < g.R + kGenTH && j >= g.R && j < g.R + kGenTW;
-      T4 v;
+  // ---- weight slices: thread -> (row m, input channels i, i+1); the slice
+  //      of step bt is loaded during step bt-2 and written to LDS in step bt-1.
+  //      Wave (kk, q) = (wave/4, wave%4), lane (m, e/2) = (lane%16, lane/16):
+  //      the 64 lanes of a wave write 64 different LDS banks.
+  const int wm = lane & 15, wi = (wave >> 2) * 32 + 8 * (wave & 3) + 2 * (lane >> 4);
+  const bool wlive = (wave >> 2) < NK;
+  const BufRes wres = make_buf(wt, (uint32_t)(3 * C * KK * C * E));
+  uint32_t wraw[2];
+  auto wload = [&](int bt) {
+    const int b = bt / KK, t = bt - b * KK;
+    const int c = c0 + wm;
+    const uint32_t row = (uint32_t)(((b * C + c) * KK + t) * C);
+    wraw[0] = gf_load_raw<E>(wres, (c < C && wi < C) ? (row + wi) * E : kOob);
+    wraw[1] = gf_load_raw<E>(wres, (c < C && wi + 1 < C) ? (row + wi + 1) * E : kOob);
+  };
+  auto wput = [&](int buf) {
+    if (!wlive) return;
+    // unit (kk, part, lane = m + 16*q) holds W[m][kk*32 + 8*q + e], e = 0..7
+    uint32_t* __restrict__ dst = reinterpret_cast<uint32_t*>(abuf + buf * AU * 16) +
+                                 ((wi >> 5) * P * 64 + wm + 16 * ((wi & 31) >> 3)) * 4 +
+                                 ((wi & 7) >> 1);
+    if constexpr (E == 4) {
+      uint32_t hi, lo;
+      split_bf16x2(__uint_as_float(wraw[0]), __uint_as_float(wraw[1]), hi, lo);
+      dst[0] = hi;
+      dst[64 * 4] = lo;
+    } else {
+      dst[0] = wraw[0] | (wraw[1] << 16);
+    }
+  };
+  wload(0);
+
+  // ---- halo tile of x (zero outside the image) -> LDS planes; interior
+  //      pixels also go to the identity channels of the output.  Two pixels
+  //      per thread and batch: 32 loads in flight before any LDS write.
+  {
+    const BufRes xres = make_buf(x + ((int64_t)n * C + c0) * HW, (uint32_t)nch * HWE);
+    const BufRes ores = make_buf(out + ((int64_t)n * 4 * C + c0) * HW, (uint32_t)nch * HWE);
+    for (int p0 = tid; p0 < g.npix; p0 += 2 * kGfThreads) {
+      uint32_t lo[2], so[2];
+      int pix[2];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int ch = c0 + 4 * grp + e;
-        T val = (T)0.f;
-        if (in_img && ch < C) {
-          const int64_t off = ((int64_t)n * C + ch) * HW + (int64_t)gh * g.W + gw;
-          val = x[off];
-          if (interior) out[((int64_t)n * 4 * C + ch) * HW + (int64_t)gh * g.W + gw] = val;
-        }
-        v[e] = val;
+      for (int s = 0; s < 2; ++s) {
+        pix[s] = p0 + s * kGfThreads;
+        const int i = pix[s] / LW, j = pix[s] - i * LW;
+        const int gh = h0 - R + i, gw = w0 - R + j;
+        const bool in =
+            pix[s] < g.npix && (unsigned)gh < (unsigned)H && (unsigned)gw < (unsigned)W;
+        const bool inner = i >= R && i < R + kGfTH && j >= R && j < R + kGfTW;
+        lo[s] = in ? (uint32_t)(gh * W + gw) * (uint32_t)E : kOob;
+        so[s] = (in && inner) ? lo[s] : kOob;
       }
-      xs[pix * 4 + (grp ^ gen_swz<T>(pix))] = v;
+      uint32_t v[2][16];
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int ch = 0; ch < 16; ++ch) v[s][ch] = gf_load_raw<E>(xres, lo[s] + ch * HWE);
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int ch = 0; ch < 16; ++ch) gf_store_raw<E>(ores, so[s] + ch * HWE, v[s][ch]);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (pix[s] >= g.npix) continue;
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp) {
+          XQ q;
+          if constexpr (E == 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[e] = v[s][4 * grp + e];
+          } else {
+            q[0] = v[s][4 * grp] | (v[s][4 * grp + 1] << 16);
+            q[1] = v[s][4 * grp + 2] | (v[s][4 * grp + 3] << 16);
+          }
+          *reinterpret_cast<XQ*>(xs + grp * g.plane + pix[s] * XB) = q;
+        }
+      }
     }
   }
-  // ---- bias rows of this channel block, [branch][tap][16]
-  for (int idx = tid; idx < 3 * KK * 16; idx += kGenThreads) {
+
+  // ---- bias rows of this channel block, [bt][16]
+  for (int idx = tid; idx < NBT * 16; idx += kGfThreads) {
     const int m = idx & 15, bt = idx >> 4;
     const int b = bt / KK, t = bt - b * KK;
-    const int ch = c0 + m;
-    bs[idx] = ch < C ? to_f(bias[(int64_t)(b * C + ch) * KK + t]) : 0.f;
+    bs[idx] = m < nch ? to_f(bias[(int64_t)(b * C + c0 + m) * KK + t]) : 0.f;
   }
+  wput(0);
+  if (NBT > 1) wload(1);
 
-  // ---- y operand (unshifted pixels) for this wave's pixel blocks
-  V bfrag[kGenNB][KSTEPS][M::P];
+  // ---- y operand (unshifted pixels) of this wave's four blocks; per block
+  //      the LDS address of this lane's x entry at zero shift and the byte
+  //      offset of its pixel in a channel plane (kOob outside the image)
+  V bfr[4][NK][P];
+  uint32_t pbase[4], obase[4];
+  {
+    const BufRes yres = make_buf(y + (int64_t)n * C * HW, (uint32_t)C * HWE);
 #pragma unroll
-  for (int blk = 0; blk < kGenNB; ++blk) {
-    const int gh = h0 + wave * kGenRPW + blk / kGenCPW;
-    const int gw = w0 + (blk % kGenCPW) * 16 + col16;
-    const bool ok = gh < g.H && gw < g.W;
-    const T* __restrict__ yp = y + (int64_t)n * C * HW + (int64_t)gh * g.W + gw;
+    for (int blk = 0; blk < 4; ++blk) {
+      const int lrow = 2 * wave + (blk >> 1), lcol = 16 * (blk & 1) + col16;
+      const int gh = h0 + lrow, gw = w0 + lcol;
+      const uint32_t po = (gh < H && gw < W) ? (uint32_t)(gh * W + gw) * (uint32_t)E : kOob;
+      obase[blk] = po;
+      pbase[blk] = (uint32_t)(quad * g.plane + ((lrow + R) * LW + lcol + R) * XB);
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) {
-      float v[8];
+      for (int kk = 0; kk < NK; ++kk) {
+        float v[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int i = 32 * kk + 8 * quad + e;
-        v[e] = (ok && i < C) ? to_f(yp[(int64_t)i * HW]) : 0.f;
+        for (int e = 0; e < 8; ++e) {
+          const int i = 32 * kk + 8 * quad + e;
+          v[e] = buf_load1<T>(yres, i < C ? po + (uint32_t)i * HWE : kOob);
+        }
+        M::pack(v, bfr[blk][kk]);
       }
-      M::pack(v, bfrag[blk][kk]);
     }
   }
   __syncthreads();
 
-  const int crow = c0 + col16;  // channel of this lane's A-fragment row
-  const bool crow_ok = crow < C;
-  const bool wvec = g.wvec != 0;
-
-  // Flattened (branch, tap) loop; the weight rows of step bt+1 are fetched
-  // while step bt runs its MFMAs and epilogue.
-  float wnext[KSTEPS][8];
-#pragma unroll
-  for (int kk = 0; kk < KSTEPS; ++kk)
-    load_w8<T>(wt, (int64_t)crow * KK, crow_ok, 32 * kk + 8 * quad, C, wvec, wnext[kk]);
-  f32x4 acc[kGenNB];
+  f32x4 acc[4];
 #pragma unroll 1
-  for (int bt = 0; bt < 3 * KK; ++bt) {
+  for (int bt = 0; bt < NBT; ++bt) {
     const int b = bt / KK, t = bt - b * KK;
+    if (bt + 1 < NBT) {
+      wput((bt + 1) & 1);
+      if (bt + 2 < NBT) wload(bt + 2);
+    }
+    const unsigned char* __restrict__ ab = abuf + (bt & 1) * AU * 16;
+    V afr[NK][P];
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk)
+#pragma unroll
+      for (int pp = 0; pp < P; ++pp)
+        afr[kk][pp] = __builtin_bit_cast(
+            V, *reinterpret_cast<const u32x4*>(ab + ((kk * P + pp) * 64 + lane) * 16));
+    const f32x4 binit = *reinterpret_cast<const f32x4*>(bs + bt * 16 + 4 * quad);
     const int ki = t / KS, kj = t - ki * KS;
     const int d = dil_of(b, g.d0, g.d1, g.d2);
+    const int shift = ((ki - r) * d * LW + (kj - r) * d) * XB;
     if (t == 0) {
 #pragma unroll
-      for (int blk = 0; blk < kGenNB; ++blk) acc[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int blk = 0; blk < 4; ++blk) acc[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    V afrag[KSTEPS][M::P];
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) M::pack(wnext[kk], afrag[kk]);
-    if (bt + 1 < 3 * KK) {
-      const int b1 = (bt + 1) / KK, t1 = (bt + 1) - b1 * KK;
-      const int64_t o1 = (int64_t)(b1 * C + crow) * KK + t1;
-#pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk)
-        load_w8<T>(wt, o1, crow_ok, 32 * kk + 8 * quad, C, wvec, wnext[kk]);
-    }
-    const f32x4 binit = *reinterpret_cast<const f32x4*>(bs + bt * 16 + 4 * quad);
-    const int dh = (ki - r) * d, dw = (kj - r) * d;
-#pragma unroll
-    for (int blk = 0; blk < kGenNB; ++blk) {
+    for (int blk = 0; blk < 4; ++blk) {
       f32x4 dacc = binit;
 #pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk) dacc = M::mac(afrag[kk], bfrag[blk][kk], dacc);
-      const int lrow = wave * kGenRPW + blk / kGenCPW + g.R + dh;
-      const int lcol = (blk % kGenCPW) * 16 + col16 + g.R + dw;
-      const int pix = lrow * g.LW + lcol;
-      const T4 xv = xs[pix * 4 + (quad ^ gen_swz<T>(pix))];
+      for (int kk = 0; kk < NK; ++kk) dacc = M::mac(afr[kk], bfr[blk][kk], dacc);
+      const XQ xq = *reinterpret_cast<const XQ*>(xs + pbase[blk] + shift);
+      float xv[4];
+      if constexpr (E == 4) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[blk][e] = fmaf(quant<T>(dacc[e]), to_f(xv[e]), acc[blk][e]);
+        for (int e = 0; e < 4; ++e) xv[e] = __uint_as_float(xq[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xv[e] = to_f(__builtin_bit_cast(T, (unsigned short)(xq[e >> 1] >> (16 * (e & 1)))));
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[blk][e] = fmaf(quant<T>(dacc[e]), xv[e], acc[blk][e]);
     }
     if (t == KK - 1) {
-      // ---- store branch b
+      // ---- branch b: channels c0 + 4*quad + e of output block b+1
+      const BufRes bres =
+          make_buf(out + ((int64_t)n * 4 * C + (int64_t)(b + 1) * C + c0) * HW, (uint32_t)nch * HWE);
 #pragma unroll
-      for (int blk = 0; blk < kGenNB; ++blk) {
-        const int gh = h0 + wave * kGenRPW + blk / kGenCPW;
-        const int gw = w0 + (blk % kGenCPW) * 16 + col16;
-        if (gh < g.H && gw < g.W) {
-          T* __restrict__ op = out + ((int64_t)n * 4 * C + (int64_t)(b + 1) * C) * HW +
-                               (int64_t)gh * g.W + gw;
+      for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int ch = c0 + 4 * quad + e;
-            if (ch < C) op[(int64_t)ch * HW] = from_f<T>(acc[blk][e]);
-          }
-        }
-      }
+        for (int e = 0; e < 4; ++e)
+          buf_store1<T>(bres, obase[blk] + (uint32_t)(4 * quad + e) * HWE, acc[blk][e]);
     }
+    __syncthreads();
   }
 }
 
@@ -228,15 +296,43 @@ int with_type(int dt, F&& f) {
   }
 }
 
+// Forward tiling and LDS bytes; kUnsupported when the halo tile does not fit.
+int fwd_geom(FwdGeom& f, const GenGeom& g, int esz, size_t& lds) {
+  f.N = g.N;
+  f.C = g.C;
+  f.H = g.H;
+  f.W = g.W;
+  f.d0 = g.d0;
+  f.d1 = g.d1;
+  f.d2 = g.d2;
+  f.R = g.R;
+  f.cblocks = g.cblocks;
+  f.tiles_w = (g.W + kGfTW - 1) / kGfTW;
+  f.tiles = f.tiles_w * ((g.H + kGfTH - 1) / kGfTH);
+  f.LH = kGfTH + 2 * g.R;
+  f.LW = kGfTW + 2 * g.R;
+  f.npix = f.LH * f.LW;
+  // planes start on 256-byte boundaries: the four quads of a wave then read
+  // their 4-channel entries with the fewest LDS bank conflicts (measured)
+  f.plane = (f.npix * 4 * esz + 255) / 256 * 256;
+  const int nk = (g.C + 31) / 32;
+  const int parts = esz == 4 ? 2 : 1;
+  lds = (size_t)4 * f.plane + (size_t)2 * nk * parts * 64 * 16 + (size_t)3 * g.K * g.K * 16 * 4;
+  if (lds > (size_t)kGfMaxLds) return kUnsupported;
+  if ((int64_t)f.tiles * g.cblocks * g.N > 0x7fffffffLL) return kUnsupported;
+  return kOk;
+}
+
 }  // namespace
 
-// Shared with gen_bwd.hip.
+// Shared with the backward entry points.
 int gen_make_geom(GenGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int k, int d0, int d1,
                   int d2) {
   if (n < 0 || c < 0 || h < 0 || w < 0) return kBadArgument;
   if (k < 1 || (k % 2) == 0 || d0 < 1 || d1 < 1 || d2 < 1) return kBadArgument;
   if (k > 3 || c > 64) return kUnsupported;
   if (h > (1 << 20) || w > (1 << 20) || h * w > ((int64_t)1 << 31)) return kUnsupported;
+  if (k == 1) d0 = d1 = d2 = 1;  // a 1x1 tap has no neighbour to dilate
   g.N = (int)n;
   g.C = (int)c;
   g.H = (int)h;
@@ -249,15 +345,6 @@ int gen_make_geom(GenGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int k,
   dmax = dmax > d2 ? dmax : d2;
   g.R = (k / 2) * dmax;
   g.cblocks = (int)((c + 15) / 16);
-  g.tiles_w = (int)((w + kGenTW - 1) / kGenTW);
-  g.tiles = g.tiles_w * (int)((h + kGenTH - 1) / kGenTH);
-  g.LH = kGenTH + 2 * g.R;
-  g.LW = kGenTW + 2 * g.R;
-  g.wvec = 0;
-  // fp32 halo tile + bias rows must fit the 64 KB a workgroup may allocate
-  if ((size_t)g.LH * g.LW * 16 * sizeof(float) + 3 * k * k * 16 * sizeof(float) > 64 * 1024)
-    return kUnsupported;
-  if ((int64_t)g.tiles * g.cblocks * n > 0x7fffffffLL) return kUnsupported;
   return kOk;
 }
 
@@ -269,33 +356,35 @@ extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, co
                             void* out, int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size,
                             int d0, int d1, int d2, int dtype, hipStream_t stream) {
   if (dtype < kF32 || dtype > kF16) return kBadArgument;
-  GenGeom g;
-  int st = gen_make_geom(g, n, c, h, w, kernel_size, d0, d1, d2);
+  GenGeom gg;
+  int st = gen_make_geom(gg, n, c, h, w, kernel_size, d0, d1, d2);
   if (st != kOk) return st;
   if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
   if (!x || !y || !weight || !bias || !out) return kBadArgument;
-  g.wvec = ((uintptr_t)weight % 16 == 0) && (c % 8 == 0);
+  const int esz = dtype == kF32 ? 4 : 2;
+  // 32-bit buffer offsets inside one image's [C][H][W] planes
+  if (c * h * w * esz > 0x7fffffffLL) return kUnsupported;
+  FwdGeom g;
+  size_t lds = 0;
+  st = fwd_geom(g, gg, esz, lds);
+  if (st != kOk) return st;
+  const int nk = (int)((c + 31) / 32);
   return with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
-    const size_t lds = (size_t)g.LH * g.LW * 16 * sizeof(T) + 3 * kernel_size * kernel_size * 16 * 4;
-    const dim3 grid((unsigned)((int64_t)g.N * g.tiles * g.cblocks));
-    const dim3 block(kGenThreads);
-    const int ksteps = (int)((c + 31) / 32);
-    if (kernel_size == 1) {
-      if (ksteps == 1)
-        hipLaunchKernelGGL((gen_fwd_kernel<T, 1, 1>), grid, block, lds, stream, (const T*)x,
-                           (const T*)y, (const T*)weight, (const T*)bias, (T*)out, g);
-      else
-        hipLaunchKernelGGL((gen_fwd_kernel<T, 1, 2>), grid, block, lds, stream, (const T*)x,
-                           (const T*)y, (const T*)weight, (const T*)bias, (T*)out, g);
-    } else {
-      if (ksteps == 1)
-        hipLaunchKernelGGL((gen_fwd_kernel<T, 3, 1>), grid, block, lds, stream, (const T*)x,
-                           (const T*)y, (const T*)weight, (const T*)bias, (T*)out, g);
-      else
-        hipLaunchKernelGGL((gen_fwd_kernel<T, 3, 2>), grid, block, lds, stream, (const T*)x,
-                           (const T*)y, (const T*)weight, (const T*)bias, (T*)out, g);
-    }
-    return (int)hipGetLastError();
+    auto launch = [&](auto kern) {
+      if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)lds);
+        if (e != hipSuccess) return (int)e;
+      }
+      hipLaunchKernelGGL(kern, dim3((unsigned)((int64_t)g.N * g.tiles * g.cblocks)),
+                         dim3(kGfThreads), lds, stream, (const T*)x, (const T*)y,
+                         (const T*)weight, (const T*)bias, (T*)out, g);
+      return (int)hipGetLastError();
+    };
+    if (kernel_size == 1)
+      return nk == 1 ? launch(gen_fwd_kernel<T, 1, 1>) : launch(gen_fwd_kernel<T, 1, 2>);
+    return nk == 1 ? launch(gen_fwd_kernel<T, 3, 1>) : launch(gen_fwd_kernel<T, 3, 2>);
   });
 }

@@ -128,6 +128,41 @@ def test_generator_matches_oracle(shape, K, dtype):
         assert_close(a, e, atol * scale, rtol, f"gen {name}")
 
 
+@pytest.mark.parametrize(
+    "K,dil,fused",
+    [
+        (3, (2, 7, 8), True),    # largest dilation the fused kernels stage
+        (1, (1, 12, 20), True),  # a 1x1 tap ignores the dilation
+        (3, (1, 3, 9), False),   # beyond the fused halo: materialized route
+    ],
+)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_generator_dilation_sets(K, dil, fused, dtype):
+    shape = (1, 40, 37, 45)
+    n, c, h, w = shape
+    say(f"generator dilations={dil} K={K} dtype={dtype}")
+    assert ops.generator_supported(c, K, dil) == fused
+    x = randn(shape, 34, dtype)
+    y = randn(shape, 35, dtype)
+    wt, b = default_generator_params(c, K, 36, dtype)
+    g = randn((n, 4 * c, h, w), 37, dtype)
+    xd, yd = x.to(DEV).requires_grad_(), y.to(DEV).requires_grad_()
+    wd, bd = wt.to(DEV).requires_grad_(), b.to(DEV).requires_grad_()
+    out = ops.fused_generator_dynamic_cat(xd, yd, wd, bd, K, dil)
+    out.backward(g.to(DEV))
+    x64, y64, w64, b64, g64 = (v.double() for v in (x, y, wt, b, g))
+    kern = ref.generated_kernels(y64, w64, b64, K)
+    if dtype != torch.float32:
+        kern = kern.to(dtype).double()
+    atol, rtol = TOL["gen_fwd"][dtype]
+    assert_close(out, ref.dynamic_cat(x64, kern, K, dil), atol, rtol, "gen out")
+    dx, dy, dw, db = ref.generator_dynamic_cat_backward(x64, y64, w64, b64, g64, K, dil)
+    atol, rtol = TOL["gen_bwd"][dtype]
+    for name, a, e in (("dx", xd.grad, dx), ("dy", yd.grad, dy), ("dw", wd.grad, dw), ("db", bd.grad, db)):
+        scale = max(1.0, e.abs().max().item())
+        assert_close(a, e, atol * scale, rtol, f"gen {name}")
+
+
 def test_generator_inference_has_no_autograd_graph():
     x = randn((1, 8, 9, 16), 40).to(DEV)
     y = randn((1, 8, 9, 16), 41).to(DEV)

@@ -37,6 +37,10 @@ def test_host_only_queries():
     assert lib.ddpm_gen_supported(64, 3, 5) == 1
     assert lib.ddpm_gen_supported(65, 3, 5) == 0
     assert lib.ddpm_gen_supported(64, 5, 5) == 0
+    # the backward kernels stage a column halo of 8 pixels; 1x1 taps ignore dilation
+    assert lib.ddpm_gen_supported(64, 3, 8) == 1
+    assert lib.ddpm_gen_supported(64, 3, 9) == 0
+    assert lib.ddpm_gen_supported(64, 1, 50) == 1
     # 16 splits x 27 (branch, tap) x 64 x (64 + 1) fp32 partials at 256x256
     assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 64, 256, 256, 3) == 16 * 27 * 64 * 65 * 4
     assert lib.ddpm_gen_bwd_w_workspace_bytes(2, 24, 15, 17, 3) == 0  # direct write
