@@ -43,6 +43,13 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--quick", action="store_true", help="skip the secondary measurements")
+    p.add_argument(
+        "--kernel",
+        help="comma-separated C-ABI entry points (or 'copy') to run alone at the headline "
+        "shape, for rocprofv3 counter runs; no timing line is printed",
+    )
+    p.add_argument("--dtype", choices=("f32", "bf16"), default="f32", help="with --kernel")
+    p.add_argument("--reps", type=int, default=3, help="launches per entry point with --kernel")
     return p.parse_args()
 
 
@@ -70,6 +77,11 @@ def train_step(module, x, y):
     x.grad = None
     y.grad = None
     module(x, y).square().mean().backward()
+
+
+def progress(msg):
+    """One line per finished measurement on stderr (stdout carries only the JSON line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def time_loop(fn, steps, warmup):
@@ -225,7 +237,8 @@ def cpu_baseline(budget_s=20.0):
 
     from oracle.unfold_ref import UnfoldDDPM
 
-    threads = os.cpu_count() or 1
+    # the host's CPU share: OMP_NUM_THREADS when the environment sets it
+    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or os.cpu_count() or 1
     torch.set_num_threads(threads)
     torch.manual_seed(21)
     model = UnfoldDDPM(C, K).train()
@@ -265,6 +278,68 @@ def cpu_baseline(budget_s=20.0):
     }
 
 
+# --------------------------------------------------------------------------- kernel mode
+COPY_BYTES = 2**30  # 'copy': a plain 1 GiB device copy (4x the MALL; reads and writes this many bytes)
+
+
+def kernel_mode(args):
+    """Launches the named entry points `reps` times each at B1 C64 K3 256x256
+    (dilations 1/3/5) on seeded inputs, and 'copy' as a plain device copy of
+    COPY_BYTES, so that rocprofv3 --pmc can read each kernel's HBM counters
+    (FETCH_SIZE / WRITE_SIZE) and the copy calibrates them."""
+    import ctypes
+
+    import torch
+
+    from dynamicconvolutionoperator_amd import _lib
+
+    lib = _lib.load()
+    dt = {"f32": torch.float32, "bf16": torch.bfloat16}[args.dtype]
+    code = 0 if dt == torch.float32 else 1
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    g = torch.Generator(device="cuda").manual_seed(1)
+    rnd = lambda *shape: torch.randn(*shape, device="cuda", generator=g).to(dt)  # noqa: E731
+    x, y = rnd(B, C, H, W), rnd(B, C, H, W)
+    go = rnd(B, 4 * C, H, W)
+    wt, bs = rnd(3 * C * K * K, C) * 0.1, rnd(3 * C * K * K) * 0.1
+    kern = rnd(B, 3, C, K * K, H, W)
+    out = torch.empty(B, 4 * C, H, W, device="cuda", dtype=dt)
+    dx, dy, dk = torch.empty_like(x), torch.empty_like(y), torch.empty_like(kern)
+    dw, db = torch.empty_like(wt), torch.empty_like(bs)
+    wsb = max(int(lib.ddpm_gen_bwd_w_workspace_bytes(B, C, H, W, K)),
+              int(lib.ddpm_gen_bwd_y_workspace_bytes(C, K)),
+              int(lib.ddpm_gen_bwd_x_workspace_bytes(B, C, H, W, K)), 1)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    shp = (B, C, H, W, K, *DIL)
+    calls = {
+        "ddpm_gen_fwd": lambda: lib.ddpm_gen_fwd(ptr(x), ptr(y), ptr(wt), ptr(bs), ptr(out), *shp, code, s),
+        "ddpm_gen_bwd_x": lambda: lib.ddpm_gen_bwd_x(ptr(y), ptr(wt), ptr(bs), ptr(go), ptr(dx), ptr(ws), wsb,
+                                                     *shp, code, s),
+        "ddpm_gen_bwd_y": lambda: lib.ddpm_gen_bwd_y(ptr(x), ptr(wt), ptr(go), ptr(dy), ptr(ws), wsb, *shp,
+                                                     code, s),
+        "ddpm_gen_bwd_w": lambda: lib.ddpm_gen_bwd_w(ptr(x), ptr(y), ptr(go), ptr(dw), ptr(db), ptr(ws), wsb,
+                                                     *shp, code, s),
+        "ddpm_filter_fwd": lambda: lib.ddpm_filter_fwd(ptr(x), ptr(kern), ptr(out), *shp, code, code, s),
+        "ddpm_filter_bwd_x": lambda: lib.ddpm_filter_bwd_x(ptr(go), ptr(kern), ptr(dx), *shp, code, code, s),
+        "ddpm_filter_bwd_k": lambda: lib.ddpm_filter_bwd_k(ptr(x), ptr(go), ptr(dk), *shp, code, code, s),
+        "copy": lambda: (dst.copy_(src), 0)[1],
+    }
+    names = args.kernel.split(",")
+    for name in names:
+        if name not in calls:
+            raise SystemExit(f"unknown --kernel {name}; choose from {', '.join(calls)}")
+    for name in names:
+        for _ in range(args.reps):
+            rc = calls[name]()
+            if rc:
+                raise SystemExit(f"{name} failed with status {rc}")
+        torch.cuda.synchronize()
+        print(f"ran {name} x{args.reps} ({args.dtype})", flush=True)
+
+
 # --------------------------------------------------------------------------- main
 def main():
     args = parse_args()
@@ -283,6 +358,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+    if args.kernel:
+        kernel_mode(args)
+        return
     lib = _lib.load()
     entries = [n for n in _lib.SIGNATURES if n.startswith(("ddpm_gen_fwd", "ddpm_gen_bwd_x", "ddpm_gen_bwd_y", "ddpm_gen_bwd_w", "ddpm_filter_"))]
     entries = [n for n in entries if not n.endswith("_workspace_bytes")]
@@ -332,6 +410,7 @@ def main():
     }
     del module, x, y
     torch.cuda.empty_cache()
+    progress(f"fp32 training step {train_ms:.3f} ms")
 
     extra = {"kernels_fp32_train": kernels}
     if not args.quick:
@@ -350,10 +429,12 @@ def main():
         del module, x, y
         torch.cuda.empty_cache()
 
+        progress("bf16 training and inference done")
         # ---- dynamic filter bandwidth (materialized path)
         extra["filter_fwd_fp32"] = filter_bandwidth(torch.float32)
         extra["filter_fwd_bf16"] = filter_bandwidth(torch.bfloat16)
 
+        progress("filter bandwidth done")
         # ---- peak temporary memory and Unfold-route time (GPU)
         for name, dtype in (("fp32", torch.float32), ("bf16", torch.bfloat16)):
             module = make_module(dtype)
@@ -377,6 +458,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
+        progress("CPU baseline (about 20 s)")
         cpu = cpu_baseline()
 
     result = {
