@@ -109,7 +109,8 @@ __global__ __launch_bounds__(256) void gen_pack_w_kernel(const T* __restrict__ w
   for (int part = 0; part < P; ++part) dst[unit + part * 64] = __builtin_bit_cast(u32x4, o[part]);
 }
 
-template <typename T, int KS, int MB>
+// CF: C == MB*16, every channel row of the last 16-channel block exists.
+template <typename T, int KS, int MB, bool CF>
 __global__ __launch_bounds__(kXtThreads) void gen_bwd_x_kernel(const uint16_t* __restrict__ yt,
                                                                const uint32_t* __restrict__ pk,
                                                                const T* __restrict__ bias,
@@ -174,62 +175,100 @@ __global__ __launch_bounds__(kXtThreads) void gen_bwd_x_kernel(const uint16_t* _
         acc[blk][mb][e] = (ok && ch < C) ? to_f(go[(int64_t)ch * HW + (int64_t)h * W + w]) : 0.f;
       }
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
   const BufRes yres = make_buf(yt + (int64_t)n * HW * P * g.cp, (uint32_t)(HW * P * g.cp * 2));
   const BufRes gres = make_buf(go + (int64_t)C * HW, (uint32_t)(3 * C * HW * E));
-#pragma unroll 1
-  for (int bt = 0; bt < 3 * KK; ++bt) {
-    const int buf = bt & 1;
-    if (bt + 1 < 3 * KK) stage_a(bt + 1, buf ^ 1);
+  constexpr int CPc = NK * 32;                       // channels per pixel of the transposed y
+  const uint32_t HWE = (uint32_t)HW * (uint32_t)E;   // bytes of one channel plane
+
+  // Operands of one step (one 16-pixel block at one (branch, tap)): the B
+  // fragments (8 consecutive channels of y at the source pixel) and the branch
+  // gradient at the source pixel, channels mb*16 + 4*quad + e.  The next
+  // step's set is loaded while the current one is consumed.
+  struct Ops {
+    V bf[NK][P];
+    float gv[MB][4];
+  };
+  auto load_ops = [&](int bt, int blk, Ops& o) {
     const int b = bt / KK, t = bt - b * KK;
     const int ki = t / KS, kj = t - ki * KS;
     const int d = dil_of(b, g.d0, g.d1, g.d2);
     const int sh = h - (ki - r) * d;
-    const uint32_t* __restrict__ ab = abuf + buf * AU * 4;
+    const int sw = wb + 16 * blk - (kj - r) * d;
+    const bool ok = (unsigned)sh < (unsigned)H && (unsigned)sw < (unsigned)W;
+    const uint32_t sp = (uint32_t)(sh * W + sw);
+    // y: one offset per lane (kOob outside the image), the (kk, part) slice
+    // as the instruction's immediate offset (read as zero past the end too)
+    const uint32_t yoff = ok ? (sp * (uint32_t)(P * CPc) + 8 * quad) * 2u : kOob;
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      const int sw = wb + 16 * blk - (kj - r) * d;
-      const bool ok = (unsigned)sh < (unsigned)H && (unsigned)sw < (unsigned)W;
-      const int64_t sp = (int64_t)sh * W + sw;
-      // B fragments: 8 consecutive channels at the source pixel
-      V bfr[NK][P];
+    for (int kk = 0; kk < NK; ++kk)
 #pragma unroll
-      for (int kk = 0; kk < NK; ++kk)
+      for (int pp = 0; pp < P; ++pp)
+        o.bf[kk][pp] = __builtin_bit_cast(
+            V, __builtin_amdgcn_raw_buffer_load_b128(yres, yoff + (pp * CPc + kk * 32) * 2, 0, 0));
+    const uint32_t goff = ((uint32_t)(b * C) * (uint32_t)HW + sp) * (uint32_t)E;
+    if constexpr (CF) {
+      // lane part of the channel in the offset, the uniform part (mb*16 + e)
+      // planes in soffset: a masked lane's kOob stays past the end either way
+      const uint32_t gq = ok ? goff + (uint32_t)(4 * quad) * HWE : kOob;
 #pragma unroll
-        for (int pp = 0; pp < P; ++pp) {
-          const uint32_t off =
-              ok ? (uint32_t)((sp * P + pp) * g.cp + kk * 32 + 8 * quad) * 2u : kOob;
-          bfr[kk][pp] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(yres, off, 0, 0));
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t so = (uint32_t)(mb * 16 + e) * HWE;
+          if constexpr (E == 4)
+            o.gv[mb][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(gres, gq, so, 0));
+          else
+            o.gv[mb][e] = to_f(__builtin_bit_cast(
+                T, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(gres, gq, so, 0)));
         }
-      // branch gradient at the source pixel, channels mb*16 + 4*quad + e
-      float gv[MB][4];
+    } else {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int ch = mb * 16 + 4 * quad + e;
-          const uint32_t off =
-              (ok && ch < C) ? (uint32_t)(((int64_t)b * C + ch) * HW + sp) * (uint32_t)E : kOob;
-          gv[mb][e] = buf_load1<T>(gres, off);
+          o.gv[mb][e] = buf_load1<T>(gres, (ok && ch < C) ? goff + (uint32_t)ch * HWE : kOob);
         }
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        f32x4 dacc = *reinterpret_cast<const f32x4*>(bs + bt * (MB * 16) + mb * 16 + 4 * quad);
-#pragma unroll
-        for (int kk = 0; kk < NK; ++kk) {
-          V afr[P];
-#pragma unroll
-          for (int pp = 0; pp < P; ++pp)
-            afr[pp] = __builtin_bit_cast(
-                V, *reinterpret_cast<const u32x4*>(ab + 4 * (((mb * NK + kk) * P + pp) * 64 + lane)));
-          dacc = M::mac(afr, bfr[kk], dacc);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[blk][mb][e] = fmaf(quant<T>(dacc[e]), gv[mb][e], acc[blk][mb][e]);
-      }
     }
+  };
+  // Generator at the source pixels of one step (A fragments of the tap are in
+  // registers), rounded like the forward and weighted by the branch gradient.
+  auto step = [&](const V (&afr)[MB][NK][P], const float* __restrict__ bsl, const Ops& o,
+                  f32x4 (&ac)[MB]) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      f32x4 dacc = *reinterpret_cast<const f32x4*>(bsl + mb * 16 + 4 * quad);
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) dacc = M::mac(afr[mb][kk], o.bf[kk], dacc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ac[mb][e] = fmaf(quant<T>(dacc[e]), o.gv[mb][e], ac[mb][e]);
+    }
+  };
+
+  Ops o0, o1;
+  load_ops(0, 0, o0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+#pragma unroll 1
+  for (int bt = 0; bt < 3 * KK; ++bt) {
+    const int buf = bt & 1;
+    if (bt + 1 < 3 * KK) stage_a(bt + 1, buf ^ 1);
+    load_ops(bt, 1, o1);
+    const uint32_t* __restrict__ ab = abuf + buf * AU * 4;
+    V afr[MB][NK][P];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk)
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp)
+          afr[mb][kk][pp] = __builtin_bit_cast(
+              V, *reinterpret_cast<const u32x4*>(ab + 4 * (((mb * NK + kk) * P + pp) * 64 + lane)));
+    const float* __restrict__ bsl = bs + bt * (MB * 16);
+    step(afr, bsl, o0, acc[0]);
+    if (bt + 1 < 3 * KK) load_ops(bt + 1, 0, o0);
+    step(afr, bsl, o1, acc[1]);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
@@ -355,9 +394,15 @@ extern "C" int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bia
         if (e != 0) return e;
         constexpr int AU = MB * NK * Mma<T>::P * 64;
         const size_t lds = (size_t)2 * AU * 16 + (size_t)3 * KS * KS * MB * 16 * sizeof(float);
-        hipLaunchKernelGGL((gen_bwd_x_kernel<T, KS, MB>), dim3((unsigned)((int64_t)g.N * g.tiles)),
-                           dim3(kXtThreads), lds, stream, (const uint16_t*)yt, (const uint32_t*)pk,
-                           (const T*)bias, (const T*)grad_out, (T*)grad_x, g);
+        const dim3 grid((unsigned)((int64_t)g.N * g.tiles));
+        if (c == MB * 16)
+          hipLaunchKernelGGL((gen_bwd_x_kernel<T, KS, MB, true>), grid, dim3(kXtThreads), lds,
+                             stream, (const uint16_t*)yt, (const uint32_t*)pk, (const T*)bias,
+                             (const T*)grad_out, (T*)grad_x, g);
+        else
+          hipLaunchKernelGGL((gen_bwd_x_kernel<T, KS, MB, false>), grid, dim3(kXtThreads), lds,
+                             stream, (const uint16_t*)yt, (const uint32_t*)pk, (const T*)bias,
+                             (const T*)grad_out, (T*)grad_x, g);
         return (int)hipGetLastError();
       };
       if (kernel_size == 1) return launch(std::integral_constant<int, 1>());
