@@ -10,8 +10,10 @@
 // q() rounds the generated tap to the input dtype (bf16/f16), as the
 // reference does before consuming it (_triton_kernels.py:332-335).
 //
-// One workgroup = (image n, 16-channel block, 16 x 32 pixel tile), 8 waves;
-// wave w owns tile rows 2w and 2w+1, i.e. four 16-pixel blocks.  The
+// One workgroup = (image n, 16-channel block, 16 x 16*CB pixel tile), 8
+// waves; wave w owns tile rows 2w and 2w+1, i.e. 2*CB 16-pixel blocks (CB = 4:
+// eight independent MFMA chains per wave and one weight read per 8 blocks;
+// CB = 2 for halos too large for the 64-column tile).  The
 // generator is an MFMA GEMM per (branch, tap): M = the 16 channels, N = 16
 // pixels, K = the input channels (v_mfma_f32_16x16x32_{bf16,f16}; fp32 runs
 // as three bf16 products).  Operands:
@@ -38,7 +40,6 @@ namespace ddpm {
 constexpr int kGfWaves = 8;
 constexpr int kGfThreads = 64 * kGfWaves;
 constexpr int kGfTH = 2 * kGfWaves;  // tile rows, two per wave
-constexpr int kGfTW = 32;            // tile columns, two 16-pixel blocks
 constexpr int kGfMaxLds = 160 * 1024;
 
 struct FwdGeom {
@@ -47,6 +48,7 @@ struct FwdGeom {
   int R;        // halo radius
   int cblocks;  // ceil(C/16)
   int tiles_w, tiles;
+  int TW;       // tile columns (16 * CB)
   int LH, LW;   // halo tile rows / columns
   int npix;     // LH * LW
   int plane;    // bytes of one 4-channel plane of the halo tile (256-byte multiple)
@@ -68,9 +70,10 @@ __device__ __forceinline__ void gf_store_raw(BufRes r, uint32_t off, uint32_t v)
     __builtin_amdgcn_raw_buffer_store_b16((unsigned short)v, r, off, 0, 0);
 }
 
-// amdgpu_waves_per_eu(4): 128 registers, so two 8-wave workgroups share a CU.
-template <typename T, int KS, int NK>
-__global__ __launch_bounds__(kGfThreads) __attribute__((amdgpu_waves_per_eu(4))) void gen_fwd_kernel(
+// CB = 4: 256 registers per lane (one 8-wave workgroup per CU, whose 133 KB
+// halo tile fills the LDS anyway); CB = 2: 128 registers, two workgroups per CU.
+template <typename T, int KS, int NK, int CB>
+__global__ __launch_bounds__(kGfThreads) __attribute__((amdgpu_waves_per_eu(CB == 4 ? 2 : 4))) void gen_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ wt,
     const T* __restrict__ bias, T* __restrict__ out, FwdGeom g) {
   typedef Mma<T> M;
@@ -83,6 +86,8 @@ __global__ __launch_bounds__(kGfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   constexpr int XB = 4 * E;           // bytes of one 4-channel pixel entry
   constexpr int AU = NK * P * 64;     // 16-byte units of one weight slice
   typedef uint32_t XQ __attribute__((ext_vector_type(E)));  // one 4-channel entry
+  constexpr int TW = 16 * CB;         // tile columns
+  constexpr int NBW = 2 * CB;         // 16-pixel blocks per wave
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   unsigned char* __restrict__ xs = smem;                                   // [4][plane]
@@ -96,7 +101,7 @@ __global__ __launch_bounds__(kGfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   const int tile = nt % g.tiles;
   const int n = nt / g.tiles;
   const int ty = tile / g.tiles_w, tx = tile - ty * g.tiles_w;
-  const int h0 = ty * kGfTH, w0 = tx * kGfTW;
+  const int h0 = ty * kGfTH, w0 = tx * TW;
   const int C = g.C, H = g.H, W = g.W, R = g.R, LW = g.LW;
   const int64_t HW = (int64_t)H * W;
   const uint32_t HWE = (uint32_t)HW * (uint32_t)E;  // bytes of one channel plane
@@ -155,7 +160,7 @@ __global__ __launch_bounds__(kGfThreads) __attribute__((amdgpu_waves_per_eu(4)))
         const int gh = h0 - R + i, gw = w0 - R + j;
         const bool in =
             pix[s] < g.npix && (unsigned)gh < (unsigned)H && (unsigned)gw < (unsigned)W;
-        const bool inner = i >= R && i < R + kGfTH && j >= R && j < R + kGfTW;
+        const bool inner = i >= R && i < R + kGfTH && j >= R && j < R + TW;
         lo[s] = in ? (uint32_t)(gh * W + gw) * (uint32_t)E : kOob;
         so[s] = (in && inner) ? lo[s] : kOob;
       }
@@ -196,19 +201,20 @@ __global__ __launch_bounds__(kGfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   wput(0);
   if (NBT > 1) wload(1);
 
-  // ---- y operand (unshifted pixels) of this wave's four blocks; per block
-  //      the LDS address of this lane's x entry at zero shift and the byte
-  //      offset of its pixel in a channel plane (kOob outside the image)
-  V bfr[4][NK][P];
-  uint32_t pbase[4], obase[4];
+  // ---- y operand (unshifted pixels) of this wave's blocks; per block the
+  //      LDS address of this lane's x entry at zero shift
+  V bfr[NBW][NK][P];
+  uint32_t pbase[NBW];
+  auto pix_off = [&](int blk) {  // byte offset of this lane's pixel in a plane
+    const int gh = h0 + 2 * wave + blk / CB, gw = w0 + 16 * (blk % CB) + col16;
+    return (gh < H && gw < W) ? (uint32_t)(gh * W + gw) * (uint32_t)E : kOob;
+  };
   {
     const BufRes yres = make_buf(y + (int64_t)n * C * HW, (uint32_t)C * HWE);
 #pragma unroll
-    for (int blk = 0; blk < 4; ++blk) {
-      const int lrow = 2 * wave + (blk >> 1), lcol = 16 * (blk & 1) + col16;
-      const int gh = h0 + lrow, gw = w0 + lcol;
-      const uint32_t po = (gh < H && gw < W) ? (uint32_t)(gh * W + gw) * (uint32_t)E : kOob;
-      obase[blk] = po;
+    for (int blk = 0; blk < NBW; ++blk) {
+      const int lrow = 2 * wave + blk / CB, lcol = 16 * (blk % CB) + col16;
+      const uint32_t po = pix_off(blk);
       pbase[blk] = (uint32_t)(quad * g.plane + ((lrow + R) * LW + lcol + R) * XB);
 #pragma unroll
       for (int kk = 0; kk < NK; ++kk) {
@@ -224,7 +230,7 @@ __global__ __launch_bounds__(kGfThreads) __attribute__((amdgpu_waves_per_eu(4)))
   }
   __syncthreads();
 
-  f32x4 acc[4];
+  f32x4 acc[NBW];
 #pragma unroll 1
   for (int bt = 0; bt < NBT; ++bt) {
     const int b = bt / KK, t = bt - b * KK;
@@ -232,6 +238,9 @@ __global__ __launch_bounds__(kGfThreads) __attribute__((amdgpu_waves_per_eu(4)))
       wput((bt + 1) & 1);
       if (bt + 2 < NBT) wload(bt + 2);
     }
+    const int ki = t / KS, kj = t - ki * KS;
+    const int d = dil_of(b, g.d0, g.d1, g.d2);
+    const int shift = ((ki - r) * d * LW + (kj - r) * d) * XB;
     const unsigned char* __restrict__ ab = abuf + (bt & 1) * AU * 16;
     V afr[NK][P];
 #pragma unroll
@@ -241,18 +250,20 @@ __global__ __launch_bounds__(kGfThreads) __attribute__((amdgpu_waves_per_eu(4)))
         afr[kk][pp] = __builtin_bit_cast(
             V, *reinterpret_cast<const u32x4*>(ab + ((kk * P + pp) * 64 + lane) * 16));
     const f32x4 binit = *reinterpret_cast<const f32x4*>(bs + bt * 16 + 4 * quad);
-    const int ki = t / KS, kj = t - ki * KS;
-    const int d = dil_of(b, g.d0, g.d1, g.d2);
-    const int shift = ((ki - r) * d * LW + (kj - r) * d) * XB;
     if (t == 0) {
 #pragma unroll
-      for (int blk = 0; blk < 4; ++blk) acc[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int blk = 0; blk < NBW; ++blk) acc[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    // NBW independent accumulation chains
+    f32x4 dacc[NBW];
 #pragma unroll
-    for (int blk = 0; blk < 4; ++blk) {
-      f32x4 dacc = binit;
+    for (int blk = 0; blk < NBW; ++blk) dacc[blk] = binit;
 #pragma unroll
-      for (int kk = 0; kk < NK; ++kk) dacc = M::mac(afr[kk], bfr[blk][kk], dacc);
+    for (int kk = 0; kk < NK; ++kk)
+#pragma unroll
+      for (int blk = 0; blk < NBW; ++blk) dacc[blk] = M::mac(afr[kk], bfr[blk][kk], dacc[blk]);
+#pragma unroll
+    for (int blk = 0; blk < NBW; ++blk) {
       const XQ xq = *reinterpret_cast<const XQ*>(xs + pbase[blk] + shift);
       float xv[4];
       if constexpr (E == 4) {
@@ -264,17 +275,19 @@ __global__ __launch_bounds__(kGfThreads) __attribute__((amdgpu_waves_per_eu(4)))
           xv[e] = to_f(__builtin_bit_cast(T, (unsigned short)(xq[e >> 1] >> (16 * (e & 1)))));
       }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[blk][e] = fmaf(quant<T>(dacc[e]), xv[e], acc[blk][e]);
+      for (int e = 0; e < 4; ++e) acc[blk][e] = fmaf(quant<T>(dacc[blk][e]), xv[e], acc[blk][e]);
     }
     if (t == KK - 1) {
       // ---- branch b: channels c0 + 4*quad + e of output block b+1
       const BufRes bres =
           make_buf(out + ((int64_t)n * 4 * C + (int64_t)(b + 1) * C + c0) * HW, (uint32_t)nch * HWE);
 #pragma unroll
-      for (int blk = 0; blk < 4; ++blk)
+      for (int blk = 0; blk < NBW; ++blk) {
+        const uint32_t po = pix_off(blk);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          buf_store1<T>(bres, obase[blk] + (uint32_t)(4 * quad + e) * HWE, acc[blk][e]);
+          buf_store1<T>(bres, po + (uint32_t)(4 * quad + e) * HWE, acc[blk][e]);
+      }
     }
     __syncthreads();
   }
@@ -296,8 +309,9 @@ int with_type(int dt, F&& f) {
   }
 }
 
-// Forward tiling and LDS bytes; kUnsupported when the halo tile does not fit.
-int fwd_geom(FwdGeom& f, const GenGeom& g, int esz, size_t& lds) {
+// Forward tiling and LDS bytes for a tile of 16 x 16*cb pixels;
+// kUnsupported when the halo tile does not fit.
+int fwd_geom(FwdGeom& f, const GenGeom& g, int esz, int cb, size_t& lds) {
   f.N = g.N;
   f.C = g.C;
   f.H = g.H;
@@ -307,10 +321,11 @@ int fwd_geom(FwdGeom& f, const GenGeom& g, int esz, size_t& lds) {
   f.d2 = g.d2;
   f.R = g.R;
   f.cblocks = g.cblocks;
-  f.tiles_w = (g.W + kGfTW - 1) / kGfTW;
+  f.TW = 16 * cb;
+  f.tiles_w = (g.W + f.TW - 1) / f.TW;
   f.tiles = f.tiles_w * ((g.H + kGfTH - 1) / kGfTH);
   f.LH = kGfTH + 2 * g.R;
-  f.LW = kGfTW + 2 * g.R;
+  f.LW = f.TW + 2 * g.R;
   f.npix = f.LH * f.LW;
   // planes start on 256-byte boundaries: the four quads of a wave then read
   // their 4-channel entries with the fewest LDS bank conflicts (measured)
@@ -364,9 +379,15 @@ extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, co
   const int esz = dtype == kF32 ? 4 : 2;
   // 32-bit buffer offsets inside one image's [C][H][W] planes
   if (c * h * w * esz > 0x7fffffffLL) return kUnsupported;
+  // 64-column tiles when their halo tile fits the LDS, else 32 columns
   FwdGeom g;
   size_t lds = 0;
-  st = fwd_geom(g, gg, esz, lds);
+  int cb = 4;
+  st = fwd_geom(g, gg, esz, cb, lds);
+  if (st == kUnsupported) {
+    cb = 2;
+    st = fwd_geom(g, gg, esz, cb, lds);
+  }
   if (st != kOk) return st;
   const int nk = (int)((c + 31) / 32);
   return with_type(dtype, [&](auto tag) {
@@ -383,8 +404,13 @@ extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, co
                          (const T*)weight, (const T*)bias, (T*)out, g);
       return (int)hipGetLastError();
     };
-    if (kernel_size == 1)
-      return nk == 1 ? launch(gen_fwd_kernel<T, 1, 1>) : launch(gen_fwd_kernel<T, 1, 2>);
-    return nk == 1 ? launch(gen_fwd_kernel<T, 3, 1>) : launch(gen_fwd_kernel<T, 3, 2>);
+    auto pick = [&](auto ks) {
+      constexpr int KS = decltype(ks)::value;
+      if (cb == 4)
+        return nk == 1 ? launch(gen_fwd_kernel<T, KS, 1, 4>) : launch(gen_fwd_kernel<T, KS, 2, 4>);
+      return nk == 1 ? launch(gen_fwd_kernel<T, KS, 1, 2>) : launch(gen_fwd_kernel<T, KS, 2, 2>);
+    };
+    if (kernel_size == 1) return pick(std::integral_constant<int, 1>());
+    return pick(std::integral_constant<int, 3>());
   });
 }
