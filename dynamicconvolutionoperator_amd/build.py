@@ -45,6 +45,15 @@ def _compile(src: str) -> str:
     return obj
 
 
+def _undefined_library_symbols(path: str) -> list[str]:
+    """Undefined dynamic symbols of `path` in this library's namespace (needs nm)."""
+    nm = shutil.which("nm")
+    if nm is None:
+        return []
+    res = subprocess.run([nm, "-D", "--undefined-only", path], capture_output=True, text=True)
+    return [ln.split()[-1] for ln in res.stdout.splitlines() if "ddpm" in ln]
+
+
 def build(verbose: bool = False) -> str:
     """Compile every csrc/*.hip for gfx950 and link libddpm_hip.so (always rebuilds)."""
     os.makedirs(OBJ_DIR, exist_ok=True)
@@ -57,6 +66,12 @@ def build(verbose: bool = False) -> str:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc link failed:\n{res.stderr}")
+    # a kernel whose host stub the compiler failed to emit shows up only as an
+    # undefined symbol at load time: refuse to install such a library
+    undefined = _undefined_library_symbols(tmp)
+    if undefined:
+        os.remove(tmp)
+        raise RuntimeError("libddpm_hip.so references undefined library symbols:\n  " + "\n  ".join(undefined))
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH}")

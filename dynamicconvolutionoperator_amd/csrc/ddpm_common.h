@@ -94,6 +94,10 @@ struct Mma<float> {
     o[0] = __builtin_bit_cast(V, (u32x4){hi[0], hi[1], hi[2], hi[3]});
     o[1] = __builtin_bit_cast(V, (u32x4){lo[0], lo[1], lo[2], lo[3]});
   }
+  // one product of single parts (for operands exact in bf16)
+  static __device__ __forceinline__ f32x4 mac1(V a, V b, f32x4 acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+  }
   static __device__ __forceinline__ f32x4 mac(const V (&a)[2], const V (&b)[2], f32x4 acc) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[0], acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[1], acc, 0, 0, 0);
@@ -113,8 +117,11 @@ struct Mma<bf16> {
     for (int e = 0; e < 4; ++e) p[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
     o[0] = __builtin_bit_cast(V, p);
   }
+  static __device__ __forceinline__ f32x4 mac1(V a, V b, f32x4 acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+  }
   static __device__ __forceinline__ f32x4 mac(const V (&a)[1], const V (&b)[1], f32x4 acc) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], acc, 0, 0, 0);
+    return mac1(a[0], b[0], acc);
   }
 };
 
@@ -127,8 +134,11 @@ struct Mma<f16> {
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[0][e] = (f16)v[e];
   }
+  static __device__ __forceinline__ f32x4 mac1(V a, V b, f32x4 acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+  }
   static __device__ __forceinline__ f32x4 mac(const V (&a)[1], const V (&b)[1], f32x4 acc) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], b[0], acc, 0, 0, 0);
+    return mac1(a[0], b[0], acc);
   }
 };
 

@@ -13,15 +13,18 @@
 // them write fp32 partials that a second kernel sums in a fixed order
 // (deterministic, no atomics).  A workgroup walks its rows in steps of one
 // row segment of 128 columns.  Everything a step reads -- the K rows
-// {h-d, h, h+d} of x (128 + 16 columns, 16 channels), the y row (all C
-// channels) and the branch-gradient row (16 channels) -- is copied
+// {h-d, h, h+d} of x (128 + 16 columns, 16 channels), the y rows (all C
+// channels) and the branch-gradient rows (16 channels) -- is copied
 // global -> LDS by buffer loads that write LDS directly (no registers; reads
 // outside the image return zero), one step ahead into a second buffer.
 // Wave (segment sg, tap half th) owns 32 tokens of the step and half of the
-// K*K taps; it accumulates its taps x 16 c x C i with
-// v_mfma_f32_16x16x32_{bf16,f16} (M = c, N = i, K = tokens; fp32 operands
-// run as three bf16 products).  Two waves share each SIMD, so one wave's VALU
-// work (forming and splitting dK) overlaps the other's MFMAs.
+// K*K taps.  It forms dK for its taps on the fly -- one multiply per element,
+// plus the bf16 hi/lo split for fp32, is all its VALU work -- and
+// accumulates taps x 16 c x C i with v_mfma_f32_16x16x32_{bf16,f16} (M = c,
+// N = i, K = tokens; fp32 operands run as three bf16 products).  db is one
+// more MFMA per tap and part against a column of ones.  For fp32, y is split
+// into bf16 hi/lo planes once per call by a small kernel, so every B fragment
+// is a plain 16-byte LDS read.
 
 #include "gen_common.h"
 #include <type_traits>
@@ -45,8 +48,8 @@ struct WGradGeom {
   int rows_per_split;  // image rows (n, h) per split
   int rows;            // N * H
   int direct;          // one split: write grad_weight / grad_bias directly
-  int dma;             // rows start on dword boundaries: LDS-direct dword copies
-  int x4;              // W % 8 == 0 and 16-byte aligned y / grad_out: 16-byte copies
+  int xdma;            // x rows start on dword boundaries: LDS-direct dword copies
+  int x4;              // y and gradient rows 16-byte aligned (W % 8 == 0): 16-byte copies
 };
 
 // Tap halves per kernel size: the K = 3 taps are split over two waves.
@@ -56,27 +59,33 @@ struct WgTaps {
   static constexpr int kPer = (KS * KS + kHalves - 1) / kHalves;
 };
 
-// One LDS staging buffer (dwords; elements of T packed):
-//   x rows [KS*16][kXSD]   pitch 2 (mod 32) dwords; read element-wise
-//   y rows [MB*16][kYC]    16-byte chunks, chunk k of row i stored at
-//   g rows [16][kYC]       position k ^ (i & 15): the 16-byte B-fragment
-//                          reads of 16 rows at one k hit distinct banks
+// One LDS staging buffer (dwords):
+//   x rows [KS*16][kXSD]      T elements; odd pitch, so the 64 lanes' reads of
+//                             one element fall at most two to a bank
+//   y rows [P][MB*16][kYD]    2-byte elements (the bf16 hi / lo planes of an
+//                             fp32 y, or y itself): 16 chunks of 16 bytes,
+//                             chunk k of row i stored at position k ^ (i & 15)
+//   g rows [16][kGD]          T elements, chunks swizzled the same way
+// The 16-byte fragment reads of 16 rows at one chunk index hit 16 distinct
+// bank groups.
 template <typename T, int KS, int MB>
 struct WgLds {
-  static constexpr int kPerD = 4 / (int)sizeof(T);             // elements per dword
-  static constexpr int kPerC = 4 * kPerD;                      // elements per 16-byte chunk
-  static constexpr int kXD = kWgLW / kPerD;                    // dwords per staged x row
-  static constexpr int kXI = (kXD + 63) / 64;                  // 64-dword copies per x row
-  static constexpr int kXSD = kXD + ((2 - kXD % 32) + 32) % 32;
-  static constexpr int kYC = kWgTW / kPerC;                    // chunks per y / g row (32 / 16)
-  static constexpr int kYD = 4 * kYC;                          // dwords per y / g row
-  static constexpr int kRPI = 64 / kYC;                        // y / g rows per 1 KB copy
+  static constexpr int P = Mma<T>::P;
+  static constexpr int kPerD = 4 / (int)sizeof(T);                  // elements per dword
+  static constexpr int kXD = kWgLW / kPerD;                         // dwords per staged x row
+  static constexpr int kXI = (kXD + 63) / 64;                       // 64-dword copies per x row
+  static constexpr int kXSD = kXD + (sizeof(T) == 4 ? 1 : 3);
+  static constexpr int kYC = kWgTW / 8;                             // chunks per y row (16)
+  static constexpr int kYD = 4 * kYC;
+  static constexpr int kGC = kWgTW * (int)sizeof(T) / 16;           // chunks per g row
+  static constexpr int kGD = 4 * kGC;
   static constexpr int kXRows = KS * 16;
-  static constexpr int kYRows = MB * 16;
+  static constexpr int kYRows = P * MB * 16;
   static constexpr int kYOff = kXRows * kXSD;
   static constexpr int kGOff = kYOff + kYRows * kYD;
-  static constexpr int kBuf = kGOff + 16 * kYD;
-  static_assert(kYC >= 16, "the chunk swizzle needs 16 chunks per row");
+  static constexpr int kBuf = kGOff + 16 * kGD;
+  static_assert(kXSD % 2 == 1, "odd x-row pitch");
+  static_assert(kYC == 16 && kGC >= 16, "the chunk swizzle needs 16 chunks per row");
 };
 
 template <typename T>
@@ -85,28 +94,6 @@ __device__ __forceinline__ float lds_elem(const uint32_t* __restrict__ base, int
     return __uint_as_float(base[idx]);
   } else {
     return to_f(reinterpret_cast<const T*>(base)[idx]);
-  }
-}
-
-// 8 consecutive elements of an LDS row as fp32: for fp32 the two 16-byte
-// chunks at dwords p0 and p1, for 2-byte types the chunk at p0.
-template <typename T>
-__device__ __forceinline__ void lds_chunks8(const uint32_t* __restrict__ row, int p0, int p1,
-                                            float (&v)[8]) {
-  if constexpr (sizeof(T) == 4) {
-    const u32x4 a = *reinterpret_cast<const u32x4*>(row + p0);
-    const u32x4 b = *reinterpret_cast<const u32x4*>(row + p1);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[e] = __uint_as_float(a[e]);
-      v[4 + e] = __uint_as_float(b[e]);
-    }
-  } else {
-    typedef T T8 __attribute__((ext_vector_type(8)));
-    const T8 t = __builtin_bit_cast(T8, *reinterpret_cast<const u32x4*>(row + p0));
-    (void)p1;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = to_f(t[e]);
   }
 }
 
@@ -126,21 +113,52 @@ struct WgPos {
   }
 };
 
+// fp32 y -> bf16 hi / lo planes ys[n][part][c][hw] (hi = top 16 bits of the
+// fp32 pattern, lo = the remainder rounded to nearest even), 4 per thread.
+__global__ __launch_bounds__(256) void gen_ysplit_kernel(const float* __restrict__ y,
+                                                         uint16_t* __restrict__ ys, int64_t chw,
+                                                         int64_t total) {
+  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i0 >= total) return;
+#pragma unroll
+  for (int e = 0; e < 4; e += 2) {
+    const int64_t i = i0 + e;
+    if (i >= total) break;
+    const bool two = i + 1 < total;
+    uint32_t h2, l2;
+    split_bf16x2(y[i], two ? y[i + 1] : 0.f, h2, l2);
+    const int64_t n = i / chw;
+    uint16_t* __restrict__ hi = ys + n * chw + i;  // = ys + n*2*chw + (i - n*chw)
+    hi[0] = (uint16_t)h2;
+    hi[chw] = (uint16_t)l2;
+    if (two) {
+      const int64_t n1 = (i + 1) / chw;
+      uint16_t* __restrict__ hi1 = ys + n1 * chw + i + 1;
+      hi1[0] = (uint16_t)(h2 >> 16);
+      hi1[chw] = (uint16_t)(l2 >> 16);
+    }
+  }
+}
+
+// yb: y itself (2-byte types) or its bf16 hi / lo planes [n][2][C][H*W] (fp32).
 template <typename T, int KS, int MB>
 __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kHalves) void gen_bwd_w_partial_kernel(
-    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ gout,
+    const T* __restrict__ x, const uint16_t* __restrict__ yb, const T* __restrict__ gout,
     float* __restrict__ pw, float* __restrict__ pb, T* __restrict__ dw_out, T* __restrict__ db_out,
     WGradGeom g) {
   typedef Mma<T> M;
   typedef typename M::V V;
+  typedef typename M::E ME;
   typedef WgLds<T, KS, MB> L;
   constexpr int KK = KS * KS;
   constexpr int r = KS / 2;
+  constexpr int P = M::P;
   constexpr int NH = WgTaps<KS>::kHalves;
   constexpr int TPH = WgTaps<KS>::kPer;
   constexpr int NW = kWgSegs * NH;
   constexpr int NT = 64 * NW;
   constexpr int E = (int)sizeof(T);
+  constexpr int PC = 16 / E;  // T elements per 16-byte chunk
   extern __shared__ __attribute__((aligned(16))) uint32_t wsm[];
 
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
@@ -153,7 +171,6 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kHalves) void gen_bwd_w_
   const int C = g.C, H = g.H, W = g.W;
   const int64_t HW = (int64_t)H * W;
   const int64_t CHW = (int64_t)C * HW;
-  const uint32_t plane_bytes = (uint32_t)(CHW * E);
   const uint32_t row_bytes = (uint32_t)(W * E);
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -167,10 +184,47 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kHalves) void gen_bwd_w_
   const int steps = row_end > row_beg ? (row_end - row_beg) * g.col_blocks : 0;
   const T* __restrict__ gbase = gout + (int64_t)(b + 1) * C * HW;
 
+  // Step-invariant parts of this wave's copies, computed once:
+  //   x rows: the lane's byte offset at column 0 of the staged row (may be
+  //     negative: columns left of the image read zero);
+  //   y / gradient rows (16-byte copies): the lane's byte offset within one
+  //     image's planes at row 0, column 0 (kOob for channels >= C) and the
+  //     column of its chunk.
+  constexpr int YRPC = 64 / L::kYC;  // y rows per 1 KB copy
+  constexpr int GRPC = 64 / L::kGC;  // gradient rows per 1 KB copy
+  constexpr int NY = L::kYRows / YRPC, NG = 16 / GRPC;
+  constexpr int NJ = (NY + NG + NW - 1) / NW;
+  int xlo[L::kXI];
+#pragma unroll
+  for (int part = 0; part < L::kXI; ++part) {
+    const int po = 64 * part < L::kXD - 64 ? 64 * part : L::kXD - 64;
+    xlo[part] = ((po + lane) * L::kPerD - kWgPad) * E;
+  }
+  uint32_t cpo[NJ];
+  int cpc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int ii = wave + NW * j;
+    cpo[j] = kOob;
+    cpc[j] = 0;
+    if (ii < NY) {
+      const int row = ii * YRPC + lane / L::kYC, pos = lane % L::kYC;
+      const int part = row / (MB * 16), i = row - part * (MB * 16);
+      cpc[j] = (pos ^ (i & 15)) * 8;
+      if (i < C) cpo[j] = ((uint32_t)(part * C + i) * (uint32_t)HW + (uint32_t)cpc[j]) * 2u;
+    } else if (ii < NY + NG) {
+      const int row = (ii - NY) * GRPC + lane / L::kGC, pos = lane % L::kGC;
+      cpc[j] = (pos ^ (row & 15)) * PC;
+      const int ch = cb * 16 + row;
+      if (ch < C) cpo[j] = ((uint32_t)ch * (uint32_t)HW + (uint32_t)cpc[j]) * (uint32_t)E;
+    }
+  }
+
   // ---- operands of step `p` -> LDS buffer `buf`
   auto stage = [&](const WgPos& p, int buf) {
     uint32_t* __restrict__ dstb = wsm + buf * L::kBuf;
-    if (g.dma) {
+    const uint32_t rowel = (uint32_t)(p.h * W);
+    if (g.xdma) {
       // x rows: copies of 64 dwords (lane l moves dword l) from a resource
       // spanning one image row, so columns outside the image read zero
 #pragma unroll
@@ -188,95 +242,89 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kHalves) void gen_bwd_w_
           const int po = 64 * part < L::kXD - 64 ? 64 * part : L::kXD - 64;
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
               res, (__attribute__((address_space(3))) void*)(dstb + pr * L::kXSD + po), 4,
-              (uint32_t)(p.w0 - kWgPad + (po + lane) * L::kPerD) * (uint32_t)E, 0, 0, 0);
+              (uint32_t)(xlo[part] + p.w0 * E), 0, 0, 0);
         }
       }
-    }
-    // y and branch-gradient rows in the swizzled chunk layout; channels
-    // >= C read past the end of the resource (zero)
-    const BufRes yres = make_buf(y + (int64_t)p.n * CHW, plane_bytes);
-    const BufRes gres = make_buf(gbase + (int64_t)p.n * 4 * CHW, plane_bytes);
-    const uint32_t rowel = (uint32_t)(p.h * W);
-    if (g.x4) {
-      // 1 KB copies: lane l moves chunk l, i.e. row i0 + l / kYC, position l % kYC
-      const int ri = lane / L::kYC, pos = lane % L::kYC;
-      constexpr int NY = L::kYRows / L::kRPI, NG = 16 / L::kRPI;
-#pragma unroll
-      for (int j = 0; j < (NY + NG + NW - 1) / NW; ++j) {
-        const int ii = wave + NW * j;
-        if ((NY + NG) % NW != 0 && ii >= NY + NG) break;
-        const bool isy = ii < NY;
-        const int row = (isy ? ii : ii - NY) * L::kRPI + ri;  // y row i or g row c
-        const int w = p.w0 + (pos ^ (row & 15)) * L::kPerC;
-        const int ch = isy ? row : cb * 16 + row;
-        const uint32_t off = w < W ? ((uint32_t)ch * (uint32_t)HW + rowel + (uint32_t)w) * E : kOob;
-        const int ldsd = (isy ? L::kYOff : L::kGOff) + (ii - (isy ? 0 : NY)) * 256;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(isy ? yres : gres,
-                                                 (__attribute__((address_space(3))) void*)(dstb + ldsd),
-                                                 16, off, 0, 0, 0);
-      }
-    } else if (g.dma) {
-      // dword copies: lane l moves dword l of a 64-dword piece of one row
-      constexpr int PPR = L::kYD / 64 > 0 ? L::kYD / 64 : 1;  // pieces per row
-      constexpr int NY = L::kYRows * PPR, NG = 16 * PPR;
-#pragma unroll
-      for (int j = 0; j < (NY + NG + NW - 1) / NW; ++j) {
-        const int ii = wave + NW * j;
-        if ((NY + NG) % NW != 0 && ii >= NY + NG) break;
-        const bool isy = ii < NY;
-        const int k2 = isy ? ii : ii - NY;
-        const int row = k2 / PPR, piece = k2 - row * PPR;
-        const int dw = 64 * piece + lane;  // dword within the row
-        const int kc = ((dw >> 2) ^ (row & 15)), wi = dw & 3;
-        const int w = p.w0 + kc * L::kPerC + wi * L::kPerD;
-        const int ch = isy ? row : cb * 16 + row;
-        const uint32_t off = w < W ? ((uint32_t)ch * (uint32_t)HW + rowel + (uint32_t)w) * E : kOob;
-        const int ldsd = (isy ? L::kYOff : L::kGOff) + row * L::kYD + 64 * piece;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(isy ? yres : gres,
-                                                 (__attribute__((address_space(3))) void*)(dstb + ldsd),
-                                                 4, off, 0, 0, 0);
-      }
-    }
-    if (!g.dma) {
-      // element-wise copy through registers (2-byte types with odd W)
+    } else {
+      // element-wise through registers (2-byte x with odd W or unaligned x)
       T* __restrict__ dst = reinterpret_cast<T*>(dstb);
-      constexpr int PX = L::kXRows * kWgLW, PY = L::kYRows * kWgTW, PG = 16 * kWgTW;
-      const BufRes xres = make_buf(x + (int64_t)p.n * CHW, plane_bytes);
-      for (int idx = tid; idx < PX + PY + PG; idx += NT) {
-        uint32_t off = kOob;
-        int li;
-        BufRes res;
-        if (idx < PX) {
-          const int pr = idx / kWgLW, j = idx - pr * kWgLW;
-          const int rr = pr >> 4, c = pr & 15;
-          const int ch = cb * 16 + c, hh = p.h + (rr - r) * d, gw = p.w0 - kWgPad + j;
-          if (ch < C && (unsigned)hh < (unsigned)H && (unsigned)gw < (unsigned)W)
-            off = (uint32_t)(((int64_t)ch * H + hh) * W + gw) * E;
-          li = pr * L::kXSD * L::kPerD + j;
-          res = xres;
+      const BufRes xres = make_buf(x + (int64_t)p.n * CHW, (uint32_t)(CHW * E));
+      for (int idx = tid; idx < L::kXRows * kWgLW; idx += NT) {
+        const int pr = idx / kWgLW, j = idx - pr * kWgLW;
+        const int rr = pr >> 4, c = pr & 15;
+        const int ch = cb * 16 + c, hh = p.h + (rr - r) * d, gw = p.w0 - kWgPad + j;
+        const bool ok = ch < C && (unsigned)hh < (unsigned)H && (unsigned)gw < (unsigned)W;
+        const uint32_t off = ok ? (uint32_t)(((int64_t)ch * H + hh) * W + gw) * E : kOob;
+        dst[pr * L::kXSD * L::kPerD + j] = from_f<T>(buf_load1<T>(xres, off));
+      }
+    }
+    // y rows (P parts x MB*16 channels) and branch-gradient rows (16
+    // channels) in the swizzled chunk layout; channels >= C read zero
+    const BufRes yres = make_buf(yb + (int64_t)p.n * P * CHW, (uint32_t)(P * CHW * 2));
+    const BufRes gres = make_buf(gbase + (int64_t)p.n * 4 * CHW, (uint32_t)(CHW * E));
+    if (g.x4) {
+      // 1 KB copies: lane l moves one 16-byte chunk
+      const uint32_t ystep = (rowel + (uint32_t)p.w0) * 2u, gstep = (rowel + (uint32_t)p.w0) * E;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int ii = wave + NW * j;
+        if ((NY + NG) % NW != 0 && ii >= NY + NG) break;
+        const bool colok = p.w0 + cpc[j] < W;
+        if (ii < NY) {
+          const uint32_t off = colok ? cpo[j] + ystep : kOob;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              yres, (__attribute__((address_space(3))) void*)(dstb + L::kYOff + ii * 256), 16, off,
+              0, 0, 0);
         } else {
-          const bool isy = idx < PX + PY;
-          const int k2 = idx - PX - (isy ? 0 : PY);
-          const int row = k2 / kWgTW, j = k2 - row * kWgTW, gw = p.w0 + j;
-          const int ch = isy ? row : cb * 16 + row;
-          if (ch < C && gw < W) off = ((uint32_t)ch * (uint32_t)HW + rowel + (uint32_t)gw) * E;
-          const int kc = (j / L::kPerC) ^ (row & 15), wi = j % L::kPerC;
-          li = ((isy ? L::kYOff : L::kGOff) + row * L::kYD) * L::kPerD + kc * L::kPerC + wi;
-          res = isy ? yres : gres;
+          const uint32_t off = colok ? cpo[j] + gstep : kOob;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              gres, (__attribute__((address_space(3))) void*)(dstb + L::kGOff + (ii - NY) * 256), 16,
+              off, 0, 0, 0);
         }
-        dst[li] = from_f<T>(buf_load1<T>(res, off));
+      }
+    } else {
+      // element-wise through registers
+      uint16_t* __restrict__ dy = reinterpret_cast<uint16_t*>(dstb + L::kYOff);
+      T* __restrict__ dg = reinterpret_cast<T*>(dstb + L::kGOff);
+      constexpr int PY = L::kYRows * kWgTW, PG = 16 * kWgTW;
+      for (int idx = tid; idx < PY + PG; idx += NT) {
+        if (idx < PY) {
+          const int row = idx / kWgTW, j = idx - row * kWgTW;
+          const int part = row / (MB * 16), i = row - part * (MB * 16);
+          const int w = p.w0 + j;
+          const uint32_t off =
+              (i < C && w < W) ? ((uint32_t)(part * C + i) * (uint32_t)HW + rowel + (uint32_t)w) * 2u
+                               : kOob;
+          const int kc = (j >> 3) ^ (i & 15);
+          dy[row * L::kYD * 2 + kc * 8 + (j & 7)] =
+              (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(yres, off, 0, 0);
+        } else {
+          const int k2 = idx - PY;
+          const int row = k2 / kWgTW, j = k2 - row * kWgTW;
+          const int ch = cb * 16 + row, w = p.w0 + j;
+          const uint32_t off =
+              (ch < C && w < W) ? ((uint32_t)ch * (uint32_t)HW + rowel + (uint32_t)w) * E : kOob;
+          const int kc = (j / PC) ^ (row & 15);
+          dg[row * L::kGD * L::kPerD + kc * PC + (j % PC)] = from_f<T>(buf_load1<T>(gres, off));
+        }
       }
     }
   };
 
-  f32x4 acc[TPH][MB];
+  // B fragment of the bias column: B[k][n] = (n == 0) for every k
+  V ones;
+  {
+    const ME one = col16 == 0 ? (ME)1.0f : (ME)0.0f;
 #pragma unroll
-  for (int tt = 0; tt < TPH; ++tt)
+    for (int e = 0; e < 8; ++e) ones[e] = one;
+  }
+  f32x4 acc[TPH][MB], accb[TPH];
+#pragma unroll
+  for (int tt = 0; tt < TPH; ++tt) {
+    accb[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ib = 0; ib < MB; ++ib) acc[tt][ib] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float bacc[TPH];
-#pragma unroll
-  for (int tt = 0; tt < TPH; ++tt) bacc[tt] = 0.f;
+  }
 
   WgPos nxt;
   nxt.n = row_beg / H;
@@ -290,6 +338,15 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kHalves) void gen_bwd_w_
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   const int wl = 32 * sg + 8 * quad;  // this lane's first token within the step
+  const int ky = (wl >> 3) ^ col16;   // its chunk position in rows with (row & 15) = col16
+  // element index (from the buffer start) of the lane's first x value per tap
+  int xel[TPH];
+#pragma unroll
+  for (int tt = 0; tt < TPH; ++tt) {
+    const int t = th * TPH + tt;
+    const int ki = t / KS, kj = t - ki * KS;
+    xel[tt] = (ki * 16 + col16) * L::kXSD * L::kPerD + kWgPad + wl + (kj - r) * d;
+  }
   for (int s = 0; s < steps; ++s) {
     const int buf = s & 1;
     if (s + 1 < steps) {
@@ -297,34 +354,47 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kHalves) void gen_bwd_w_
       nxt.advance(g);
     }
     const uint32_t* __restrict__ bb = wsm + buf * L::kBuf;
-    // this lane's 8 tokens wl .. wl+7 sit in chunk(s) wl / kPerC (+1 for fp32)
-    const int k0 = wl / L::kPerC;
-    const int p0 = 4 * (k0 ^ col16), p1 = 4 * ((k0 + 1) ^ col16);
-    V bfr[MB][M::P];
+    V bfr[MB][P];
 #pragma unroll
-    for (int ib = 0; ib < MB; ++ib) {
-      float yv[8];
-      lds_chunks8<T>(bb + L::kYOff + (ib * 16 + col16) * L::kYD, p0, p1, yv);
-      M::pack(yv, bfr[ib]);
-    }
+    for (int ib = 0; ib < MB; ++ib)
+#pragma unroll
+      for (int pp = 0; pp < P; ++pp)
+        bfr[ib][pp] = __builtin_bit_cast(
+            V, *reinterpret_cast<const u32x4*>(bb + L::kYOff + ((pp * MB + ib) * 16 + col16) * L::kYD +
+                                               4 * ky));
+    // branch gradient of channel col16 at the lane's 8 tokens
     float gv[8];
-    lds_chunks8<T>(bb + L::kGOff + col16 * L::kYD, p0, p1, gv);
+    {
+      const uint32_t* __restrict__ gr = bb + L::kGOff + col16 * L::kGD;
+      if constexpr (E == 4) {
+        const int kg = wl >> 2;
+        const u32x4 a0 = *reinterpret_cast<const u32x4*>(gr + 4 * (kg ^ col16));
+        const u32x4 a1 = *reinterpret_cast<const u32x4*>(gr + 4 * ((kg + 1) ^ col16));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          gv[e] = __uint_as_float(a0[e]);
+          gv[4 + e] = __uint_as_float(a1[e]);
+        }
+      } else {
+        typedef T T8 __attribute__((ext_vector_type(8)));
+        const T8 t8 = __builtin_bit_cast(T8, *reinterpret_cast<const u32x4*>(gr + 4 * ky));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gv[e] = to_f(t8[e]);
+      }
+    }
 #pragma unroll
     for (int tt = 0; tt < TPH; ++tt) {
       const int t = th * TPH + tt;  // wave-uniform
       if (KK % NH != 0 && t >= KK) break;
-      const int ki = t / KS, kj = t - ki * KS;
-      const uint32_t* __restrict__ xr = bb + (ki * 16 + col16) * L::kXSD;
-      const int xo = kWgPad + wl + (kj - r) * d;
       float dk[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dk[e] = gv[e] * lds_elem<T>(xr, xo + e);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) bacc[tt] += quant<T>(dk[e]);
-      V afr[M::P];
+      for (int e = 0; e < 8; ++e) dk[e] = gv[e] * lds_elem<T>(bb, xel[tt] + e);
+      V afr[P];
       M::pack(dk, afr);
 #pragma unroll
       for (int ib = 0; ib < MB; ++ib) acc[tt][ib] = M::mac(afr, bfr[ib], acc[tt][ib]);
+#pragma unroll
+      for (int pp = 0; pp < P; ++pp) accb[tt] = M::mac1(afr[pp], ones, accb[tt]);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -334,11 +404,15 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kHalves) void gen_bwd_w_
   constexpr int NO = MB * 16;
   constexpr int RS = NO + 1;
   float* __restrict__ red = reinterpret_cast<float*>(wsm);  // [KK][16 c][RS]
-  float* __restrict__ rb = red + KK * 16 * RS;              // [KK][segs*4][16]
+  float* __restrict__ rb = red + KK * 16 * RS;              // [KK][segs][16 c]
+  if (col16 == 0) {
 #pragma unroll
-  for (int tt = 0; tt < TPH; ++tt) {
-    const int t = th * TPH + tt;
-    if (t < KK) rb[(t * kWgSegs * 4 + sg * 4 + quad) * 16 + col16] = bacc[tt];
+    for (int tt = 0; tt < TPH; ++tt) {
+      const int t = th * TPH + tt;
+      if (t < KK)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rb[(t * kWgSegs + sg) * 16 + 4 * quad + e] = accb[tt][e];
+    }
   }
   for (int w = 0; w < kWgSegs; ++w) {
     if (sg == w) {
@@ -374,7 +448,7 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kHalves) void gen_bwd_w_
     const int ch = cb * 16 + c;
     if (ch >= C) continue;
     float v = 0.f;
-    for (int j = 0; j < kWgSegs * 4; ++j) v += rb[(t * kWgSegs * 4 + j) * 16 + c];
+    for (int j = 0; j < kWgSegs; ++j) v += rb[(t * kWgSegs + j) * 16 + c];
     if (g.direct)
       db_out[(int64_t)(b * C + ch) * KK + t] = from_f<T>(v);
     else
@@ -464,9 +538,17 @@ void wgrad_geom(WGradGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int d0
   g.rows_per_split = (int)((g.rows + splits - 1) / splits);
   g.splits = (int)((g.rows + g.rows_per_split - 1) / g.rows_per_split);
   g.direct = g.splits == 1;
-  g.dma = 0;
+  g.xdma = 0;
   g.x4 = 0;
 }
+
+// Workspace: the fp32 split partials (none with one split), then, for fp32,
+// y's bf16 hi / lo planes (256-byte aligned).
+int64_t wg_partial_bytes(const WGradGeom& g, int64_t c, int k) {
+  if (g.direct) return 0;
+  return (int64_t)g.splits * 3 * k * k * c * (c + 1) * (int64_t)sizeof(float);
+}
+int64_t wg_align(int64_t v) { return (v + 255) / 256 * 256; }
 
 }  // namespace
 }  // namespace ddpm
@@ -479,9 +561,8 @@ extern "C" int64_t ddpm_gen_bwd_w_workspace_bytes(int64_t n, int64_t c, int64_t 
   if (n * h > 0x7fffffffLL) return 0;
   WGradGeom g;
   wgrad_geom(g, n, c, h, w, 1, 1, 1);
-  if (g.direct) return 0;
-  const int64_t kk = (int64_t)kernel_size * kernel_size;
-  return (int64_t)g.splits * 3 * kk * c * (c + 1) * (int64_t)sizeof(float);
+  // the query takes no dtype: it covers fp32, whose y planes come on top
+  return wg_align(wg_partial_bytes(g, c, kernel_size)) + n * 2 * c * h * w * 2;
 }
 
 extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out,
@@ -497,22 +578,30 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
   if (!x || !y || !grad_out || !grad_weight || !grad_bias) return kBadArgument;
   if (gg.d0 > kWgMaxDil || gg.d1 > kWgMaxDil || gg.d2 > kWgMaxDil) return kUnsupported;
   if (n * h > 0x7fffffffLL / 4) return kUnsupported;
-  // 32-bit buffer offsets inside one image's [C][H][W] planes
-  if (((c + 15) / 16) * 16 * h * w * (dtype == kF32 ? 4 : 2) > 0x7fffffffLL) return kUnsupported;
+  const int esz = dtype == kF32 ? 4 : 2;
+  // 32-bit buffer offsets inside one image's planes (fp32 y: two 2-byte planes)
+  if (((c + 15) / 16) * 16 * h * w * 4 > 0x7fffffffLL) return kUnsupported;
   WGradGeom g;
   wgrad_geom(g, n, c, h, w, gg.d0, gg.d1, gg.d2);
-  const int64_t need = ddpm_gen_bwd_w_workspace_bytes(n, c, h, w, kernel_size);
+  const int64_t pbytes = wg_partial_bytes(g, c, kernel_size);
+  const int64_t need = dtype == kF32 ? wg_align(pbytes) + n * 2 * c * h * w * 2 : pbytes;
   if (need > 0 && (!workspace || workspace_bytes < need)) return kWorkspaceTooSmall;
-  const size_t esz = dtype == kF32 ? 4 : 2;
-  // LDS-direct dword copies need every row to start on a dword boundary
-  g.dma = (esz == 4) || ((w % 2 == 0) && ((uintptr_t)x % 4 == 0) && ((uintptr_t)y % 4 == 0) &&
-                         ((uintptr_t)grad_out % 4 == 0));
-  g.x4 = (w % 8 == 0) && ((uintptr_t)y % 16 == 0) && ((uintptr_t)grad_out % 16 == 0);
+  uint16_t* ys = dtype == kF32 ? (uint16_t*)((char*)workspace + wg_align(pbytes)) : nullptr;
+  const uint16_t* ysrc = dtype == kF32 ? ys : (const uint16_t*)y;
+  // LDS-direct dword copies of x rows need every row to start on a dword boundary
+  g.xdma = (esz == 4) || ((w % 2 == 0) && ((uintptr_t)x % 4 == 0));
+  g.x4 = (w % 8 == 0) && ((uintptr_t)ysrc % 16 == 0) && ((uintptr_t)grad_out % 16 == 0);
   const int mb = (int)((c + 15) / 16);
   const int kk = kernel_size * kernel_size;
-  float* pw = (float*)workspace;
-  float* pb = pw ? pw + (int64_t)g.splits * 3 * kk * c * c : nullptr;
-  if (g.direct) pw = pb = nullptr;
+  float* pw = g.direct ? nullptr : (float*)workspace;
+  float* pb = g.direct ? nullptr : pw + (int64_t)g.splits * 3 * kk * c * c;
+  if (dtype == kF32) {
+    const int64_t total = n * c * h * w;
+    hipLaunchKernelGGL(gen_ysplit_kernel, dim3((unsigned)((total + 1023) / 1024)), dim3(256), 0,
+                       stream, (const float*)y, ys, c * h * w, total);
+    const int e = (int)hipGetLastError();
+    if (e != 0) return e;
+  }
   return wg_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
     auto launch = [&](auto ks, auto mbc) {
@@ -521,7 +610,7 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
       constexpr int KKc = KS * KS;
       typedef WgLds<T, KS, MB> L;
       const size_t stage = (size_t)2 * L::kBuf * 4;
-      const size_t red = (size_t)(KKc * 16 * (MB * 16 + 1) + KKc * kWgSegs * 4 * 16) * sizeof(float);
+      const size_t red = (size_t)(KKc * 16 * (MB * 16 + 1) + KKc * kWgSegs * 16) * sizeof(float);
       const size_t lds = stage > red ? stage : red;
       const dim3 grid((unsigned)(g.splits * 3 * g.cblocks));
       if (lds > 64 * 1024) {
@@ -533,7 +622,7 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
       }
       hipLaunchKernelGGL((gen_bwd_w_partial_kernel<T, KS, MB>), grid,
                          dim3(64 * kWgSegs * WgTaps<KS>::kHalves), lds, stream, (const T*)x,
-                         (const T*)y, (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g);
+                         ysrc, (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g);
       int e = (int)hipGetLastError();
       if (e != 0 || g.direct) return e;
       const int64_t total = (int64_t)3 * KKc * c * c + (int64_t)3 * KKc * c;

@@ -41,9 +41,12 @@ def test_host_only_queries():
     assert lib.ddpm_gen_supported(64, 3, 8) == 1
     assert lib.ddpm_gen_supported(64, 3, 9) == 0
     assert lib.ddpm_gen_supported(64, 1, 50) == 1
-    # 16 splits x 27 (branch, tap) x 64 x (64 + 1) fp32 partials at 256x256
-    assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 64, 256, 256, 3) == 16 * 27 * 64 * 65 * 4
-    assert lib.ddpm_gen_bwd_w_workspace_bytes(2, 24, 15, 17, 3) == 0  # direct write
+    # 16 splits x 27 (branch, tap) x 64 x (64 + 1) fp32 partials at 256x256, then
+    # the bf16 hi / lo planes of an fp32 y (2 x 2 bytes per element)
+    ysplit = lambda n, c, h, w: n * c * h * w * 4  # noqa: E731
+    assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 64, 256, 256, 3) == 16 * 27 * 64 * 65 * 4 + ysplit(1, 64, 256, 256)
+    # one split writes the gradients directly: only the y planes remain
+    assert lib.ddpm_gen_bwd_w_workspace_bytes(2, 24, 15, 17, 3) == ysplit(2, 24, 15, 17)
 
 
 def test_entry_points_validate_arguments_before_touching_the_device():
