@@ -101,9 +101,10 @@ def time_loop(fn, steps, warmup):
 class LaunchTimer:
     """Brackets every call of the named C-ABI entry points with HIP events.
 
-    The library launches on torch's current stream, which is where
-    torch.cuda.Event records, so each (start, end) pair spans exactly that
-    entry point's kernels on their own stream.
+    Every entry point takes the stream it launches on as its last argument
+    (the current stream, or a side stream for two of the backward entry
+    points); the events are recorded on that stream, so each (start, end)
+    pair spans exactly that entry point's kernels on their own stream.
     """
 
     def __init__(self, lib, names):
@@ -112,21 +113,37 @@ class LaunchTimer:
         self.torch = torch
         self.records = {n: [] for n in names}
         self.active = False
+        self.streams = {}
         for name in names:
             real = getattr(lib, name)
 
             def wrapper(*args, _real=real, _name=name):
                 if not self.active:
                     return _real(*args)
+                stream = self._stream(args[-1])
                 start = torch.cuda.Event(enable_timing=True)
                 end = torch.cuda.Event(enable_timing=True)
-                start.record()
+                start.record(stream)
                 rc = _real(*args)
-                end.record()
+                end.record(stream)
                 self.records[_name].append((start, end))
                 return rc
 
             setattr(lib, name, wrapper)
+
+    def _stream(self, handle):
+        """torch stream object for a raw hipStream_t argument."""
+        ptr = handle.value if hasattr(handle, "value") else handle
+        ptr = int(ptr or 0)
+        stream = self.streams.get(ptr)
+        if stream is None:
+            current = self.torch.cuda.current_stream()
+            if ptr == current.cuda_stream:
+                stream = current
+            else:
+                stream = self.torch.cuda.ExternalStream(ptr)
+            self.streams[ptr] = stream
+        return stream
 
     def mean_ms(self):
         out = {}
