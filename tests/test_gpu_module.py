@@ -55,7 +55,7 @@ def check_training(channels, h, w, kernel_size, dtype, fused, n=2, seed=456):
 
 
 @pytest.mark.parametrize("kernel_size", [1, 3, 5])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("fused", [True, False])
 def test_training_matches_oracle_nonaligned(kernel_size, dtype, fused):
     say(f"module training K={kernel_size} dtype={dtype} fused={fused}")
@@ -88,6 +88,21 @@ def test_autocast_bf16_uses_materialized_route():
     with torch.no_grad():
         expected = ref(x.double(), y.double())
     assert_close(out, expected, 5e-2, 5e-2, "autocast out")
+
+
+def test_autocast_fp16_uses_materialized_route():
+    """fp16 autocast: the generator conv runs in fp16, the HIP filter takes fp32 x
+    with fp16 kernels and returns fp16, as the reference's mixed path does."""
+    ref, cand = make_models(8, 3, torch.float32)
+    torch.manual_seed(8)
+    x = torch.randn(1, 8, 12, 16)
+    y = torch.randn_like(x)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16):
+        out = cand(x.to(DEV), y.to(DEV))
+    assert out.dtype == torch.float16
+    with torch.no_grad():
+        expected = ref(x.double(), y.double())
+    assert_close(out, expected, 1e-2, 1e-2, "autocast fp16 out")
 
 
 def test_module_runs_native_library():

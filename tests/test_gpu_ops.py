@@ -59,7 +59,7 @@ def test_kat_generator_exact(kat_cases):
 # ---------------------------------------------------------------- materialized filter
 @pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("K", [1, 3, 5])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_filter_matches_oracle(shape, K, dtype):
     n, c, h, w = shape
     say(f"filter shape={shape} K={K} dtype={dtype}")
@@ -100,7 +100,7 @@ def test_filter_mixed_dtypes_autocast_layout():
 # ---------------------------------------------------------------- fused generator
 @pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("K", [1, 3])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_generator_matches_oracle(shape, K, dtype):
     n, c, h, w = shape
     say(f"generator shape={shape} K={K} dtype={dtype}")
