@@ -268,9 +268,11 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_kernel(const TK* 
   const int64_t HW = (int64_t)g.H * g.W;
   const int K = KS > 0 ? KS : g.K;
   const int KK = K * K, r = K / 2;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int lpr = 1 << g.lpr_log2;  // lanes per row; lane pixels are lpr apart
-  const int trow = wave * (64 >> g.lpr_log2) + (lane >> g.lpr_log2);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  // U == 4 tiles are 64 lanes wide (one image row per wave): the row is
+  // wave-uniform, so per-row buffer resources stay in scalar registers
+  const int lpr = U == 4 ? 64 : 1 << g.lpr_log2;  // lanes per row; lane pixels are lpr apart
+  const int trow = U == 4 ? wave : wave * (64 >> g.lpr_log2) + (lane >> g.lpr_log2);
   const int cl = lane & (lpr - 1);
   const int gh = h0 + trow;
   const bool row_active = gh < g.H && trow < g.TH;
@@ -282,8 +284,10 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_kernel(const TK* 
   const int lplane = g.LH * g.RS;
 
   // kernel values at the gathered source pixels, requested before the
-  // branch-gradient tiles are staged (one image row of a tap's plane per
-  // resource: columns outside it read zero)
+  // branch-gradient tiles are staged.  U == 4: one resource per source row
+  // (columns past its end read zero, columns left of it are masked);
+  // otherwise one per tap plane, with source pixels outside the image masked
+  // by offset.  Both keep the resource wave-uniform.
   constexpr int NT = KS > 0 ? 3 * KS * KS : 1;
   float kvs[KS > 0 ? NT : 1][U];
   auto load_k = [&](int b, int ki, int kj, float (&kv)[U]) {
@@ -292,10 +296,25 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_kernel(const TK* 
     const int sh = gh - dh;
     const bool sh_ok = row_active && (unsigned)sh < (unsigned)g.H;
     const TK* kt = kp + b * bstride + (int64_t)(ki * K + kj) * HW;
-    const BufRes res = make_buf(sh_ok ? kt + (int64_t)sh * g.W : kt, sh_ok ? (uint32_t)(g.W * sizeof(TK)) : 0u);
+    if constexpr (U == 4) {
+      const BufRes res = make_buf(sh_ok ? kt + (int64_t)sh * g.W : kt,
+                                  sh_ok ? (uint32_t)(g.W * sizeof(TK)) : 0u);
+      const int col0 = w0 + cl - dw;
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      kv[u] = buf_load1<TK>(res, (uint32_t)(w0 + cl + lpr * u - dw) * (uint32_t)sizeof(TK));
+      for (int u = 0; u < U; ++u) {
+        const int col = col0 + 64 * u;
+        kv[u] = buf_load1<TK>(res, col >= 0 ? (uint32_t)col * (uint32_t)sizeof(TK) : kOob);
+      }
+    } else {
+      const BufRes res = make_buf(kt, (uint32_t)(HW * (int64_t)sizeof(TK)));
+      const int rowel = sh * g.W;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int col = w0 + cl + lpr * u - dw;
+        const bool ok = sh_ok && (unsigned)col < (unsigned)g.W;
+        kv[u] = buf_load1<TK>(res, ok ? (uint32_t)(rowel + col) * (uint32_t)sizeof(TK) : kOob);
+      }
+    }
   };
   if constexpr (KS > 0) {
 #pragma unroll
