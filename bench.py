@@ -325,7 +325,7 @@ def kernel_mode(args):
     dw, db = torch.empty_like(wt), torch.empty_like(bs)
     wsb = max(int(lib.ddpm_gen_bwd_w_workspace_bytes(B, C, H, W, K)),
               int(lib.ddpm_gen_bwd_y_workspace_bytes(C, K)),
-              int(lib.ddpm_gen_bwd_x_workspace_bytes(B, C, H, W, K)), 1)
+              int(lib.ddpm_gen_bwd_x_workspace_bytes(B, C, H, W, K, *DIL)), 1)
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)

@@ -31,7 +31,7 @@ SIGNATURES: dict[str, tuple[list, type]] = {
     "ddpm_filter_bwd_x": (_FILTER_ARGS, _I),
     "ddpm_filter_bwd_k": (_FILTER_ARGS, _I),
     "ddpm_gen_fwd": ([_P, _P, _P, _P, _P, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
-    "ddpm_gen_bwd_x_workspace_bytes": ([_L, _L, _L, _L, _I], _L),
+    "ddpm_gen_bwd_x_workspace_bytes": ([_L, _L, _L, _L, _I, _I, _I, _I], _L),
     "ddpm_gen_bwd_x": ([_P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
     "ddpm_gen_bwd_y_workspace_bytes": ([_L, _I], _L),
     "ddpm_gen_bwd_y": ([_P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),

@@ -114,29 +114,35 @@ struct WgPos {
 };
 
 // fp32 y -> bf16 hi / lo planes ys[n][part][c][hw] (hi = top 16 bits of the
-// fp32 pattern, lo = the remainder rounded to nearest even), 4 per thread.
+// fp32 pattern, lo = the remainder rounded to nearest even).  Each thread
+// splits 8 consecutive elements: two 16-byte loads, two 16-byte stores when
+// one image's planes hold a multiple of 8 elements, element-wise otherwise.
 __global__ __launch_bounds__(256) void gen_ysplit_kernel(const float* __restrict__ y,
                                                          uint16_t* __restrict__ ys, int64_t chw,
                                                          int64_t total) {
-  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
   if (i0 >= total) return;
-#pragma unroll
-  for (int e = 0; e < 4; e += 2) {
-    const int64_t i = i0 + e;
-    if (i >= total) break;
-    const bool two = i + 1 < total;
+  if (chw % 8 == 0) {
+    // 8 elements of one image (i0 and chw are multiples of 8)
+    const int64_t n = i0 / chw;
+    const f32x4 a = *reinterpret_cast<const f32x4*>(y + i0);
+    const f32x4 c = *reinterpret_cast<const f32x4*>(y + i0 + 4);
+    uint32_t hi[4], lo[4];
+    split_bf16x2(a[0], a[1], hi[0], lo[0]);
+    split_bf16x2(a[2], a[3], hi[1], lo[1]);
+    split_bf16x2(c[0], c[1], hi[2], lo[2]);
+    split_bf16x2(c[2], c[3], hi[3], lo[3]);
+    uint16_t* __restrict__ h = ys + n * chw + i0;  // = ys + n*2*chw + (i0 - n*chw)
+    *reinterpret_cast<u32x4*>(h) = (u32x4){hi[0], hi[1], hi[2], hi[3]};
+    *reinterpret_cast<u32x4*>(h + chw) = (u32x4){lo[0], lo[1], lo[2], lo[3]};
+    return;
+  }
+  for (int64_t i = i0; i < total && i < i0 + 8; ++i) {
     uint32_t h2, l2;
-    split_bf16x2(y[i], two ? y[i + 1] : 0.f, h2, l2);
-    const int64_t n = i / chw;
-    uint16_t* __restrict__ hi = ys + n * chw + i;  // = ys + n*2*chw + (i - n*chw)
-    hi[0] = (uint16_t)h2;
-    hi[chw] = (uint16_t)l2;
-    if (two) {
-      const int64_t n1 = (i + 1) / chw;
-      uint16_t* __restrict__ hi1 = ys + n1 * chw + i + 1;
-      hi1[0] = (uint16_t)(h2 >> 16);
-      hi1[chw] = (uint16_t)(l2 >> 16);
-    }
+    split_bf16x2(y[i], 0.f, h2, l2);
+    uint16_t* __restrict__ h = ys + (i / chw) * chw + i;
+    h[0] = (uint16_t)h2;
+    h[chw] = (uint16_t)l2;
   }
 }
 
@@ -597,7 +603,7 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
   float* pb = g.direct ? nullptr : pw + (int64_t)g.splits * 3 * kk * c * c;
   if (dtype == kF32) {
     const int64_t total = n * c * h * w;
-    hipLaunchKernelGGL(gen_ysplit_kernel, dim3((unsigned)((total + 1023) / 1024)), dim3(256), 0,
+    hipLaunchKernelGGL(gen_ysplit_kernel, dim3((unsigned)((total + 2047) / 2048)), dim3(256), 0,
                        stream, (const float*)y, ys, c * h * w, total);
     const int e = (int)hipGetLastError();
     if (e != 0) return e;

@@ -1,0 +1,396 @@
+// Generator tile: the workgroup body shared by the fused forward and by the
+// fused backward with respect to x.
+//
+// One workgroup = (image n, 16-channel block, 16 x 16*CB pixel tile), 8
+// waves; wave w owns tile rows 2w and 2w+1, i.e. 2*CB 16-pixel blocks (CB = 4:
+// eight independent MFMA chains per wave and one weight read per 8 blocks;
+// CB = 2 for halos too large for the 64-column tile).  The generator is an
+// MFMA GEMM per (branch, tap): M = the 16 channels, N = 16 pixels, K = the
+// input channels (v_mfma_f32_16x16x32_{bf16,f16}; fp32 runs as three bf16
+// products).  Operands:
+//   * y (B): each wave loads its pixel blocks once and keeps them in
+//     registers for all 3*K*K products;
+//   * W (A): the 16 x C slice of one (branch, tap) is converted once per
+//     workgroup (fp32: split into bf16 hi/lo) into LDS in fragment order,
+//     double-buffered one tap ahead, and read by all 8 waves.
+// The LDS also holds a halo tile (16+2R) x (16*CB+2R) of the 16 channels as 4
+// planes of 4-channel pixels, addressed per tap by a uniform shift:
+//   * forward: x, zero outside the image; a lane's 4 output channels at the
+//     shifted pixel are one ds_read_b128 (fp32) / ds_read_b64 (2-byte);
+//     out_b[c, p] = sum_tap q(gen[(b,c,tap), p]) * x[c, p + off] stays in
+//     registers until the branch's last tap;
+//   * backward (BX): an fp32 accumulator, zero at the start; every tap adds
+//     q(gen[(b,c,tap), p]) * gO_b[c, p] at p + off (one ds_read_b128 +
+//     ds_write_b128 per lane and block).  A tap's shift is one-to-one, and
+//     taps are separated by the workgroup barrier, so each accumulator entry
+//     is updated by one lane at a time in the fixed tap order.  The tile, halo
+//     included, is then written to a per-workgroup partial that a second
+//     kernel sums over the (at most 2 x 2) workgroups covering each pixel.
+// Every global access is a raw buffer access; lanes outside the image or the
+// channel range use an offset past the resource's end (read as zero, write
+// dropped) instead of a branch.
+#pragma once
+
+#include "gen_common.h"
+
+namespace ddpm {
+
+constexpr int kGtWaves = 8;
+constexpr int kGtThreads = 64 * kGtWaves;
+constexpr int kGtTH = 2 * kGtWaves;  // tile rows, two per wave
+constexpr int kGtMaxLds = 160 * 1024;
+
+struct TileGeom {
+  int N, C, H, W;
+  int d0, d1, d2;
+  int R;        // halo radius
+  int cblocks;  // ceil(C/16)
+  int tiles_w, tiles;
+  int TW;       // tile columns (16 * CB)
+  int LH, LW;   // halo tile rows / columns
+  int npix;     // LH * LW
+  int plane;    // bytes of one 4-channel plane of the halo tile (256-byte multiple)
+  int pad;      // BX partial rows: halo column j is stored at position j + pad ...
+  int LWp;      // ... of a row of LWp (multiple of 4) positions; see gen_tile_body
+};
+
+// Tiling and LDS bytes for a tile of 16 x 16*cb pixels whose LDS tile holds
+// `entry` bytes per 4-channel pixel and whose weight slices have `parts`
+// parts; kUnsupported when it does not fit the LDS.
+inline int tile_geom(TileGeom& f, const GenGeom& g, int entry, int parts, int cb, size_t& lds) {
+  f.N = g.N;
+  f.C = g.C;
+  f.H = g.H;
+  f.W = g.W;
+  f.d0 = g.d0;
+  f.d1 = g.d1;
+  f.d2 = g.d2;
+  f.R = g.R;
+  f.cblocks = g.cblocks;
+  f.TW = 16 * cb;
+  f.tiles_w = (g.W + f.TW - 1) / f.TW;
+  f.tiles = f.tiles_w * ((g.H + kGtTH - 1) / kGtTH);
+  f.LH = kGtTH + 2 * g.R;
+  f.LW = f.TW + 2 * g.R;
+  f.npix = f.LH * f.LW;
+  f.pad = (4 - g.R % 4) % 4;
+  f.LWp = (f.LW + f.pad + 3) / 4 * 4;
+  // planes start on 256-byte boundaries: the four quads of a wave then read
+  // their 4-channel entries with the fewest LDS bank conflicts (measured)
+  f.plane = (f.npix * entry + 255) / 256 * 256;
+  const int nk = (g.C + 31) / 32;
+  lds = (size_t)4 * f.plane + (size_t)2 * nk * parts * 64 * 16 + (size_t)3 * g.K * g.K * 16 * 4;
+  if (lds > (size_t)kGtMaxLds) return kUnsupported;
+  if ((int64_t)f.tiles * g.cblocks * g.N > 0x7fffffffLL) return kUnsupported;
+  return kOk;
+}
+
+// Raw element bits through a buffer resource (no conversion).
+template <int E>
+__device__ __forceinline__ uint32_t gf_load_raw(BufRes r, uint32_t off) {
+  if constexpr (E == 4)
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  else
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+template <int E>
+__device__ __forceinline__ void gf_store_raw(BufRes r, uint32_t off, uint32_t v) {
+  if constexpr (E == 4)
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
+  else
+    __builtin_amdgcn_raw_buffer_store_b16((unsigned short)v, r, off, 0, 0);
+}
+
+// a: x (forward) or grad_cat (BX); out: the concat (forward); part: the
+// per-workgroup partials (BX), [N][tiles][cblocks][16][LH][LWp] fp32, halo
+// column j at position j + pad and zero at the positions no column maps to:
+// a tile column c (c % 4 == 0) then sits at a 16-byte aligned position in its
+// own partial (c + R + pad) and in its left / right neighbour's (c + R + pad
+// -/+ TW), and the 4-column groups that a neighbour's halo only partly covers
+// read zeros for the rest.
+template <typename T, int KS, int NK, int CB, bool BX>
+__device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* __restrict__ y,
+                                              const T* __restrict__ wt, const T* __restrict__ bias,
+                                              T* __restrict__ out, float* __restrict__ part,
+                                              const TileGeom& g) {
+  typedef Mma<T> M;
+  typedef typename M::V V;
+  constexpr int P = M::P;
+  constexpr int KK = KS * KS;
+  constexpr int NBT = 3 * KK;         // (branch, tap) steps
+  constexpr int r = KS / 2;
+  constexpr int E = (int)sizeof(T);
+  constexpr int XB = BX ? 16 : 4 * E;  // bytes of one 4-channel entry of the LDS tile
+  constexpr int AU = NK * P * 64;     // 16-byte units of one weight slice
+  typedef uint32_t XQ __attribute__((ext_vector_type(E)));  // one 4-channel x entry
+  constexpr int TW = 16 * CB;         // tile columns
+  constexpr int NBW = 2 * CB;         // 16-pixel blocks per wave
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  unsigned char* __restrict__ xs = smem;                                   // [4][plane]
+  unsigned char* __restrict__ abuf = smem + 4 * g.plane;                   // [2][AU] x 16 B
+  float* __restrict__ bs = reinterpret_cast<float*>(abuf + 2 * AU * 16);  // [NBT][16]
+
+  // Block -> (n, tile, channel block), channel block fastest.
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int cb = bid % g.cblocks;
+  const int nt = bid / g.cblocks;
+  const int tile = nt % g.tiles;
+  const int n = nt / g.tiles;
+  const int ty = tile / g.tiles_w, tx = tile - ty * g.tiles_w;
+  const int h0 = ty * kGtTH, w0 = tx * TW;
+  const int C = g.C, H = g.H, W = g.W, R = g.R, LW = g.LW;
+  const int64_t HW = (int64_t)H * W;
+  const uint32_t HWE = (uint32_t)HW * (uint32_t)E;  // bytes of one channel plane
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int col16 = lane & 15, quad = lane >> 4;
+  const int c0 = cb * 16;
+  const int nch = C - c0 < 16 ? C - c0 : 16;
+
+  // ---- weight slices: thread -> (row m, input channels i, i+1); the slice
+  //      of step bt is loaded during step bt-2 and written to LDS in step bt-1.
+  //      Wave (kk, q) = (wave/4, wave%4), lane (m, e/2) = (lane%16, lane/16):
+  //      the 64 lanes of a wave write 64 different LDS banks.
+  const int wm = lane & 15, wi = (wave >> 2) * 32 + 8 * (wave & 3) + 2 * (lane >> 4);
+  const bool wlive = (wave >> 2) < NK;
+  const BufRes wres = make_buf(wt, (uint32_t)(3 * C * KK * C * E));
+  uint32_t wraw[2];
+  auto wload = [&](int bt) {
+    const int b = bt / KK, t = bt - b * KK;
+    const int c = c0 + wm;
+    const uint32_t row = (uint32_t)(((b * C + c) * KK + t) * C);
+    wraw[0] = gf_load_raw<E>(wres, (c < C && wi < C) ? (row + wi) * E : kOob);
+    wraw[1] = gf_load_raw<E>(wres, (c < C && wi + 1 < C) ? (row + wi + 1) * E : kOob);
+  };
+  auto wput = [&](int buf) {
+    if (!wlive) return;
+    // unit (kk, part, lane = m + 16*q) holds W[m][kk*32 + 8*q + e], e = 0..7
+    uint32_t* __restrict__ dst = reinterpret_cast<uint32_t*>(abuf + buf * AU * 16) +
+                                 ((wi >> 5) * P * 64 + wm + 16 * ((wi & 31) >> 3)) * 4 +
+                                 ((wi & 7) >> 1);
+    if constexpr (E == 4) {
+      uint32_t hi, lo;
+      split_bf16x2(__uint_as_float(wraw[0]), __uint_as_float(wraw[1]), hi, lo);
+      dst[0] = hi;
+      dst[64 * 4] = lo;
+    } else {
+      dst[0] = wraw[0] | (wraw[1] << 16);
+    }
+  };
+  wload(0);
+
+  if constexpr (BX) {
+    // ---- accumulator tile = 0
+    for (int i = tid; i < g.plane / 4; i += kGtThreads)
+      reinterpret_cast<f32x4*>(xs)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  } else {
+    // ---- halo tile of x (zero outside the image) -> LDS planes; interior
+    //      pixels also go to the identity channels of the output.  Two pixels
+    //      per thread and batch: 32 loads in flight before any LDS write.
+    const BufRes xres = make_buf(a + ((int64_t)n * C + c0) * HW, (uint32_t)nch * HWE);
+    const BufRes ores = make_buf(out + ((int64_t)n * 4 * C + c0) * HW, (uint32_t)nch * HWE);
+    for (int p0 = tid; p0 < g.npix; p0 += 2 * kGtThreads) {
+      uint32_t lo[2], so[2];
+      int pix[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        pix[s] = p0 + s * kGtThreads;
+        const int i = pix[s] / LW, j = pix[s] - i * LW;
+        const int gh = h0 - R + i, gw = w0 - R + j;
+        const bool in =
+            pix[s] < g.npix && (unsigned)gh < (unsigned)H && (unsigned)gw < (unsigned)W;
+        const bool inner = i >= R && i < R + kGtTH && j >= R && j < R + TW;
+        lo[s] = in ? (uint32_t)(gh * W + gw) * (uint32_t)E : kOob;
+        so[s] = (in && inner) ? lo[s] : kOob;
+      }
+      uint32_t v[2][16];
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int ch = 0; ch < 16; ++ch) v[s][ch] = gf_load_raw<E>(xres, lo[s] + ch * HWE);
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int ch = 0; ch < 16; ++ch) gf_store_raw<E>(ores, so[s] + ch * HWE, v[s][ch]);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (pix[s] >= g.npix) continue;
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp) {
+          XQ q;
+          if constexpr (E == 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[e] = v[s][4 * grp + e];
+          } else {
+            q[0] = v[s][4 * grp] | (v[s][4 * grp + 1] << 16);
+            q[1] = v[s][4 * grp + 2] | (v[s][4 * grp + 3] << 16);
+          }
+          *reinterpret_cast<XQ*>(xs + grp * g.plane + pix[s] * XB) = q;
+        }
+      }
+    }
+  }
+
+  // ---- bias rows of this channel block, [bt][16]
+  for (int idx = tid; idx < NBT * 16; idx += kGtThreads) {
+    const int m = idx & 15, bt = idx >> 4;
+    const int b = bt / KK, t = bt - b * KK;
+    bs[idx] = m < nch ? to_f(bias[(int64_t)(b * C + c0 + m) * KK + t]) : 0.f;
+  }
+  wput(0);
+  if (NBT > 1) wload(1);
+
+  // ---- y operand (unshifted pixels) of this wave's blocks; per block the
+  //      LDS address of this lane's tile entry at zero shift
+  V bfr[NBW][NK][P];
+  uint32_t pbase[NBW];
+  auto pix_off = [&](int blk) {  // byte offset of this lane's pixel in a plane
+    const int gh = h0 + 2 * wave + blk / CB, gw = w0 + 16 * (blk % CB) + col16;
+    return (gh < H && gw < W) ? (uint32_t)(gh * W + gw) * (uint32_t)E : kOob;
+  };
+  {
+    const BufRes yres = make_buf(y + (int64_t)n * C * HW, (uint32_t)C * HWE);
+#pragma unroll
+    for (int blk = 0; blk < NBW; ++blk) {
+      const int lrow = 2 * wave + blk / CB, lcol = 16 * (blk % CB) + col16;
+      const uint32_t po = pix_off(blk);
+      pbase[blk] = (uint32_t)(quad * g.plane + ((lrow + R) * LW + lcol + R) * XB);
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int i = 32 * kk + 8 * quad + e;
+          v[e] = buf_load1<T>(yres, i < C ? po + (uint32_t)i * HWE : kOob);
+        }
+        M::pack(v, bfr[blk][kk]);
+      }
+    }
+  }
+  __syncthreads();
+
+  f32x4 acc[NBW];   // forward: branch output of this lane's 4 channels per block
+  float go[NBW][4];  // BX: the branch gradient gO_b at this lane's pixel and 4 channels
+#pragma unroll 1
+  for (int bt = 0; bt < NBT; ++bt) {
+    const int b = bt / KK, t = bt - b * KK;
+    if (bt + 1 < NBT) {
+      wput((bt + 1) & 1);
+      if (bt + 2 < NBT) wload(bt + 2);
+    }
+    if constexpr (BX) {
+      if (t == 0) {
+        const BufRes gres = make_buf(a + ((int64_t)n * 4 * C + (int64_t)(b + 1) * C + c0) * HW,
+                                     (uint32_t)nch * HWE);
+#pragma unroll
+        for (int blk = 0; blk < NBW; ++blk) {
+          const uint32_t po = pix_off(blk);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            go[blk][e] = buf_load1<T>(gres, po + (uint32_t)(4 * quad + e) * HWE);
+        }
+      }
+    }
+    const int ki = t / KS, kj = t - ki * KS;
+    const int d = dil_of(b, g.d0, g.d1, g.d2);
+    const int shift = ((ki - r) * d * LW + (kj - r) * d) * XB;
+    const unsigned char* __restrict__ ab = abuf + (bt & 1) * AU * 16;
+    V afr[NK][P];
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk)
+#pragma unroll
+      for (int pp = 0; pp < P; ++pp)
+        afr[kk][pp] = __builtin_bit_cast(
+            V, *reinterpret_cast<const u32x4*>(ab + ((kk * P + pp) * 64 + lane) * 16));
+    const f32x4 binit = *reinterpret_cast<const f32x4*>(bs + bt * 16 + 4 * quad);
+    if constexpr (!BX) {
+      if (t == 0) {
+#pragma unroll
+        for (int blk = 0; blk < NBW; ++blk) acc[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    // NBW independent accumulation chains
+    f32x4 dacc[NBW];
+#pragma unroll
+    for (int blk = 0; blk < NBW; ++blk) dacc[blk] = binit;
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk)
+#pragma unroll
+      for (int blk = 0; blk < NBW; ++blk) dacc[blk] = M::mac(afr[kk], bfr[blk][kk], dacc[blk]);
+    if constexpr (BX) {
+#pragma unroll
+      for (int blk = 0; blk < NBW; ++blk) {
+        f32x4* __restrict__ pa = reinterpret_cast<f32x4*>(xs + pbase[blk] + shift);
+        f32x4 s = *pa;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[e] = fmaf(quant<T>(dacc[blk][e]), go[blk][e], s[e]);
+        *pa = s;
+      }
+    } else {
+#pragma unroll
+      for (int blk = 0; blk < NBW; ++blk) {
+        const XQ xq = *reinterpret_cast<const XQ*>(xs + pbase[blk] + shift);
+        float xv[4];
+        if constexpr (E == 4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xv[e] = __uint_as_float(xq[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            xv[e] = to_f(__builtin_bit_cast(T, (unsigned short)(xq[e >> 1] >> (16 * (e & 1)))));
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[blk][e] = fmaf(quant<T>(dacc[blk][e]), xv[e], acc[blk][e]);
+      }
+      if (t == KK - 1) {
+        // ---- branch b: channels c0 + 4*quad + e of output block b+1
+        const BufRes bres = make_buf(out + ((int64_t)n * 4 * C + (int64_t)(b + 1) * C + c0) * HW,
+                                     (uint32_t)nch * HWE);
+#pragma unroll
+        for (int blk = 0; blk < NBW; ++blk) {
+          const uint32_t po = pix_off(blk);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            buf_store1<T>(bres, po + (uint32_t)(4 * quad + e) * HWE, acc[blk][e]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  if constexpr (BX) {
+    // ---- the accumulator tile -> this workgroup's partial, rows inside the
+    //      image only; a task = (4-channel plane, row, 4 positions): four LDS
+    //      entries in, one 16-byte store per channel out.  The loop's last
+    //      barrier ordered every update before these reads.
+    const int64_t wg = ((int64_t)n * g.tiles + tile) * g.cblocks + cb;
+    const int LHp = g.LH * g.LWp;
+    const BufRes pres = make_buf(part + wg * 16 * LHp, (uint32_t)(nch * LHp * 4));
+    const int gpr = g.LWp / 4;
+    const int tasks = 4 * g.LH * gpr;
+    for (int task = tid; task < tasks; task += kGtThreads) {
+      const int k = task % gpr, rest = task / gpr;
+      const int i = rest % g.LH, grp = rest / g.LH;
+      const bool rowin = (unsigned)(h0 - R + i) < (unsigned)H;
+      f32x4 v[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int j = 4 * k + m - g.pad;
+        v[m] = (j >= 0 && j < LW)
+                   ? *reinterpret_cast<const f32x4*>(xs + grp * g.plane + (i * LW + j) * 16)
+                   : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      const uint32_t off = rowin ? (uint32_t)(i * g.LWp + 4 * k) * 4u : kOob;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f32x4 o = {v[0][e], v[1][e], v[2][e], v[3][e]};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), pres,
+                                               off + (uint32_t)((4 * grp + e) * LHp * 4), 0, 0);
+      }
+    }
+  }
+}
+
+}  // namespace ddpm

@@ -200,7 +200,7 @@ class _GeneratorDynamicCat(torch.autograd.Function):
         with torch.cuda.device(x.device):
             if ctx.needs_input_grad[0]:
                 grad_x = torch.empty_like(x)
-                wsx_bytes = int(lib.ddpm_gen_bwd_x_workspace_bytes(n, c, h, w, k))
+                wsx_bytes = int(lib.ddpm_gen_bwd_x_workspace_bytes(n, c, h, w, k, *dil))
                 wsx = torch.empty(wsx_bytes, dtype=torch.uint8, device=x.device)
                 _lib.check(
                     lib.ddpm_gen_bwd_x(_ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),

@@ -84,12 +84,16 @@ int ddpm_gen_fwd(const void* x, const void* y, const void* weight, const void* b
                  int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size, int d0, int d1,
                  int d2, int dtype, hipStream_t stream);
 
-/* Bytes of workspace ddpm_gen_bwd_x needs: its packed weight and a
- * channel-innermost (bf16 hi/lo for fp32) copy of y; valid for every dtype.
+/* Bytes of workspace ddpm_gen_bwd_x needs: the fp32 partial sums of its
+ * tiles, halo of radius (kernel_size/2)*max(d) included (about 1.9x the
+ * fp32 size of x at dilations (1,3,5)); valid for every dtype, 0 for an
+ * unsupported or empty shape.
  * Part of the launch set-up of _GeneratorDynamicCat.backward (_triton_kernels.py:944-961). */
-int64_t ddpm_gen_bwd_x_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size);
+int64_t ddpm_gen_bwd_x_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size,
+                                       int d0, int d1, int d2);
 
-/* grad_x of the fused op, recomputing the generator at the gathered pixels.
+/* grad_x of the fused op, recomputing the generator once per pixel and
+ * scattering its products to the shifted pixels (deterministic order).
  * `workspace` (at least ddpm_gen_bwd_x_workspace_bytes) is overwritten.
  * Replaces _generator_dynamic_cat_bwd_x (_triton_kernels.py:430-531, launched at :944-961). */
 int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bias, const void* grad_out,

@@ -132,13 +132,15 @@ def test_generator_matches_oracle(shape, K, dtype):
     "K,dil,fused",
     [
         (3, (2, 7, 8), True),    # largest dilation the fused kernels stage
+        (3, (1, 2, 6), True),    # halo radius 6 (partial rows shifted by 2)
+        (3, (4, 1, 1), True),    # halo radius 4 (no shift)
         (1, (1, 12, 20), True),  # a 1x1 tap ignores the dilation
         (3, (1, 3, 9), False),   # beyond the fused halo: materialized route
     ],
 )
+@pytest.mark.parametrize("shape", [(1, 40, 37, 45), (1, 24, 36, 72)])  # W % 4 != 0 / == 0
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_generator_dilation_sets(K, dil, fused, dtype):
-    shape = (1, 40, 37, 45)
+def test_generator_dilation_sets(K, dil, fused, shape, dtype):
     n, c, h, w = shape
     say(f"generator dilations={dil} K={K} dtype={dtype}")
     assert ops.generator_supported(c, K, dil) == fused

@@ -47,6 +47,13 @@ def test_host_only_queries():
     assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 64, 256, 256, 3) == 16 * 27 * 64 * 65 * 4 + ysplit(1, 64, 256, 256)
     # one split writes the gradients directly: only the y planes remain
     assert lib.ddpm_gen_bwd_w_workspace_bytes(2, 24, 15, 17, 3) == ysplit(2, 24, 15, 17)
+    # dX partials: 16x64 tiles (4 x 16 of them) x 4 channel blocks x 16 channels x
+    # the 16+2R rows of the halo tile, R = 5, each padded from 64+2R = 74 columns
+    # (shifted by 3 so that tile columns sit 16-byte aligned) to 80 ...
+    assert lib.ddpm_gen_bwd_x_workspace_bytes(1, 64, 256, 256, 3, 1, 3, 5) == 64 * 4 * 16 * 26 * 80 * 4
+    # ... and 16x32 tiles when the R = 8 accumulator tile does not fit the LDS
+    assert lib.ddpm_gen_bwd_x_workspace_bytes(1, 64, 256, 256, 3, 1, 3, 8) == 128 * 4 * 16 * 32 * 48 * 4
+    assert lib.ddpm_gen_bwd_x_workspace_bytes(1, 64, 256, 256, 5, 1, 3, 5) == 0  # unsupported
 
 
 def test_entry_points_validate_arguments_before_touching_the_device():
