@@ -9,10 +9,11 @@
 //   db[(b,c,t)]    = sum_p dK[(b,c,t), p]
 //
 // Work decomposition (CDNA4): one workgroup per (token split, branch b,
-// 16-channel block of c).  Splits are ranges of image rows; at most 16 of
-// them write fp32 partials that a second kernel sums in a fixed order
-// (deterministic, no atomics).  A workgroup walks its rows in steps of one
-// row segment of 128 columns.  Everything a step reads -- the K rows
+// 16-channel block of c).  Splits are equal ranges of steps -- one step is
+// one row segment of 128 columns -- as many as give every one of the 256 CUs
+// of an MI355X one workgroup (21 splits x 3 branches x 4 channel blocks at
+// C = 64); they write fp32 partials that a second kernel sums in a fixed
+// order (deterministic, no atomics).  Everything a step reads -- the K rows
 // {h-d, h, h+d} of x (128 + 16 columns, 16 channels), the y rows (all C
 // channels) and the branch-gradient rows (16 channels) -- is copied
 // global -> LDS by buffer loads that write LDS directly (no registers; reads
@@ -36,8 +37,8 @@ constexpr int kWgTW = 32 * kWgSegs;          // columns per step
 constexpr int kWgPad = 8;                    // staged column halo (>= dilation), even
 constexpr int kWgLW = kWgTW + 2 * kWgPad;    // staged x columns
 constexpr int kWgMaxDil = kWgPad;
-constexpr int kWgMaxSplits = 16;
-constexpr int kWgTokensPerSplit = 1024;      // split target below the cap
+constexpr int kWgCUs = 256;                  // workgroup slots the split count fills (one per CU)
+constexpr int kWgMinSteps = 4;               // steps per split at least
 
 struct WGradGeom {
   int N, C, H, W;
@@ -45,8 +46,8 @@ struct WGradGeom {
   int cblocks;         // ceil(C / 16)
   int col_blocks;      // ceil(W / kWgTW)
   int splits;
-  int rows_per_split;  // image rows (n, h) per split
-  int rows;            // N * H
+  int steps;           // N * H * col_blocks
+  int steps_per_split;
   int direct;          // one split: write grad_weight / grad_bias directly
   int xdma;            // x rows start on dword boundaries: LDS-direct dword copies
   int x4;              // y and gradient rows 16-byte aligned (W % 8 == 0): 16-byte copies
@@ -184,10 +185,10 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kHalves) void gen_bwd_w_
   const int col16 = lane & 15, quad = lane >> 4;
   const int sg = wave % kWgSegs, th = wave / kWgSegs;
 
-  const int row_beg = split * g.rows_per_split;
-  int row_end = row_beg + g.rows_per_split;
-  if (row_end > g.rows) row_end = g.rows;
-  const int steps = row_end > row_beg ? (row_end - row_beg) * g.col_blocks : 0;
+  const int step_beg = split * g.steps_per_split;
+  int step_end = step_beg + g.steps_per_split;
+  if (step_end > g.steps) step_end = g.steps;
+  const int steps = step_end > step_beg ? step_end - step_beg : 0;
   const T* __restrict__ gbase = gout + (int64_t)(b + 1) * C * HW;
 
   // Step-invariant parts of this wave's copies, computed once:
@@ -333,10 +334,13 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kHalves) void gen_bwd_w_
   }
 
   WgPos nxt;
-  nxt.n = row_beg / H;
-  nxt.h = row_beg - nxt.n * H;
-  nxt.w0 = 0;
-  nxt.cbk = 0;
+  {
+    const int row = step_beg / g.col_blocks;
+    nxt.cbk = step_beg - row * g.col_blocks;
+    nxt.w0 = nxt.cbk * kWgTW;
+    nxt.n = row / H;
+    nxt.h = row - nxt.n * H;
+  }
   if (steps > 0) {
     stage(nxt, 0);
     nxt.advance(g);
@@ -474,6 +478,7 @@ __global__ __launch_bounds__(256) void gen_bwd_w_reduce_kernel(const float* __re
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx < per) {
     float v = 0.f;
+#pragma unroll 8
     for (int s = 0; s < splits; ++s) v += pw[s * per + idx];
     // idx = (bt*C + c)*C + i  ->  row o = (b*C + c)*KK + t
     const int64_t i = idx % C;
@@ -484,6 +489,7 @@ __global__ __launch_bounds__(256) void gen_bwd_w_reduce_kernel(const float* __re
   } else if (idx < per + perb) {
     const int64_t j = idx - per;
     float v = 0.f;
+#pragma unroll 8
     for (int s = 0; s < splits; ++s) v += pb[s * perb + j];
     const int64_t c = j % C, bt = j / C;
     const int64_t b = bt / KK, t = bt % KK;
@@ -523,8 +529,9 @@ int wg_with_mb(int mb, F&& f) {
   }
 }
 
-// Splits: about kWgTokensPerSplit tokens each, at most 16 and at most one per
-// image row; one split means grad_weight / grad_bias are written directly.
+// Splits: enough to give each of kWgCUs CUs one workgroup (3 * cblocks
+// workgroups per split), at least kWgMinSteps steps each; one split means
+// grad_weight / grad_bias are written directly.
 void wgrad_geom(WGradGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int d0, int d1, int d2) {
   g.N = (int)n;
   g.C = (int)c;
@@ -535,14 +542,13 @@ void wgrad_geom(WGradGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int d0
   g.d2 = d2;
   g.cblocks = (int)((c + 15) / 16);
   g.col_blocks = (int)((w + kWgTW - 1) / kWgTW);
-  g.rows = (int)(n * h);
-  const int64_t tokens = n * h * w;
-  int64_t splits = (tokens + kWgTokensPerSplit - 1) / kWgTokensPerSplit;
-  if (splits > kWgMaxSplits) splits = kWgMaxSplits;
-  if (splits > g.rows) splits = g.rows;
+  const int64_t steps = n * h * g.col_blocks;
+  int64_t splits = kWgCUs / (3 * g.cblocks);
+  if (splits > (steps + kWgMinSteps - 1) / kWgMinSteps) splits = (steps + kWgMinSteps - 1) / kWgMinSteps;
   if (splits < 1) splits = 1;
-  g.rows_per_split = (int)((g.rows + splits - 1) / splits);
-  g.splits = (int)((g.rows + g.rows_per_split - 1) / g.rows_per_split);
+  g.steps = (int)steps;
+  g.steps_per_split = (int)((steps + splits - 1) / splits);
+  g.splits = (int)((steps + g.steps_per_split - 1) / g.steps_per_split);
   g.direct = g.splits == 1;
   g.xdma = 0;
   g.x4 = 0;
@@ -564,7 +570,7 @@ using namespace ddpm;
 extern "C" int64_t ddpm_gen_bwd_w_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w,
                                                   int kernel_size) {
   if (n <= 0 || c <= 0 || h <= 0 || w <= 0 || kernel_size < 1) return 0;
-  if (n * h > 0x7fffffffLL) return 0;
+  if (n * h * ((w + kWgTW - 1) / kWgTW) > 0x7fffffffLL) return 0;
   WGradGeom g;
   wgrad_geom(g, n, c, h, w, 1, 1, 1);
   // the query takes no dtype: it covers fp32, whose y planes come on top
@@ -583,7 +589,7 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
   if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
   if (!x || !y || !grad_out || !grad_weight || !grad_bias) return kBadArgument;
   if (gg.d0 > kWgMaxDil || gg.d1 > kWgMaxDil || gg.d2 > kWgMaxDil) return kUnsupported;
-  if (n * h > 0x7fffffffLL / 4) return kUnsupported;
+  if (n * h * ((w + kWgTW - 1) / kWgTW) > 0x7fffffffLL) return kUnsupported;
   const int esz = dtype == kF32 ? 4 : 2;
   // 32-bit buffer offsets inside one image's planes (fp32 y: two 2-byte planes)
   if (((c + 15) / 16) * 16 * h * w * 4 > 0x7fffffffLL) return kUnsupported;

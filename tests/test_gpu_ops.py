@@ -177,10 +177,16 @@ def test_generator_inference_has_no_autograd_graph():
     assert torch.equal(out, out2)
 
 
-def test_generator_split_weight_gradient_matches_direct():
-    """Shapes above 2048 tokens use split fp32 partials; compare to the oracle."""
-    shape = (2, 32, 40, 64)  # 5120 tokens -> 3 splits
+@pytest.mark.parametrize(
+    "shape",
+    [
+        (2, 32, 40, 64),  # 80 steps (row segments of 128 columns) -> 20 splits of fp32 partials
+        (1, 24, 4, 17),   # 4 steps -> one split writes the gradients directly
+    ],
+)
+def test_generator_weight_gradient_splits(shape):
     n, c, h, w = shape
+    say(f"weight gradient shape={shape}")
     x = randn(shape, 50)
     y = randn(shape, 51)
     wt, b = default_generator_params(c, 3, 52, torch.float32)

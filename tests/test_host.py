@@ -41,12 +41,15 @@ def test_host_only_queries():
     assert lib.ddpm_gen_supported(64, 3, 8) == 1
     assert lib.ddpm_gen_supported(64, 3, 9) == 0
     assert lib.ddpm_gen_supported(64, 1, 50) == 1
-    # 16 splits x 27 (branch, tap) x 64 x (64 + 1) fp32 partials at 256x256, then
-    # the bf16 hi / lo planes of an fp32 y (2 x 2 bytes per element)
+    # 21 splits (x 3 branches x 4 channel blocks = 252 workgroups for 256 CUs) x
+    # 27 (branch, tap) x 64 x (64 + 1) fp32 partials at 256x256, then the bf16
+    # hi / lo planes of an fp32 y (2 x 2 bytes per element)
     ysplit = lambda n, c, h, w: n * c * h * w * 4  # noqa: E731
-    assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 64, 256, 256, 3) == 16 * 27 * 64 * 65 * 4 + ysplit(1, 64, 256, 256)
-    # one split writes the gradients directly: only the y planes remain
-    assert lib.ddpm_gen_bwd_w_workspace_bytes(2, 24, 15, 17, 3) == ysplit(2, 24, 15, 17)
+    assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 64, 256, 256, 3) == 21 * 27 * 64 * 65 * 4 + ysplit(1, 64, 256, 256)
+    # 30 steps (image rows of 128 columns) at 4 per split: 8 splits
+    assert lib.ddpm_gen_bwd_w_workspace_bytes(2, 24, 15, 17, 3) == 8 * 27 * 24 * 25 * 4 + ysplit(2, 24, 15, 17)
+    # 4 steps or fewer: one split writes the gradients directly, only the y planes remain
+    assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 24, 4, 17, 3) == ysplit(1, 24, 4, 17)
     # dX partials: 16x64 tiles (4 x 16 of them) x 4 channel blocks x 16 channels x
     # the 16+2R rows of the halo tile, R = 5, each padded from 64+2R = 74 columns
     # (shifted by 3 so that tile columns sit 16-byte aligned) to 80 ...
