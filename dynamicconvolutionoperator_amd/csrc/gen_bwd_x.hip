@@ -153,8 +153,9 @@ extern "C" int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bia
   if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
   if (!y || !weight || !bias || !grad_out || !grad_x) return kBadArgument;
   const int esz = dtype == kF32 ? 4 : 2;
-  // 32-bit buffer offsets inside one image's [C][H][W] planes
-  if (c * h * w * esz > 0x7fffffffLL) return kUnsupported;
+  // 32-bit buffer offsets inside one image's [C][H][W] planes (and 16 planes
+  // past a channel block's first one)
+  if (c * h * w * esz > 0x7fffffffLL || 16 * h * w * esz > 0x7fffffffLL) return kUnsupported;
   // one reduce workgroup per 256 column groups of a row
   const int vec = w % 4 == 0 ? 4 : 1;
   const int64_t rsegs = ((w + vec - 1) / vec + 255) / 256;

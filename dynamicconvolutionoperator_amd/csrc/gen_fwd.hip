@@ -82,8 +82,9 @@ extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, co
   if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
   if (!x || !y || !weight || !bias || !out) return kBadArgument;
   const int esz = dtype == kF32 ? 4 : 2;
-  // 32-bit buffer offsets inside one image's [C][H][W] planes
-  if (c * h * w * esz > 0x7fffffffLL) return kUnsupported;
+  // 32-bit buffer offsets inside one image's [C][H][W] planes (and 16 planes
+  // past a channel block's first one)
+  if (c * h * w * esz > 0x7fffffffLL || 16 * h * w * esz > 0x7fffffffLL) return kUnsupported;
   // 64-column tiles when their halo tile fits the LDS, else 32 columns
   TileGeom g;
   size_t lds = 0;

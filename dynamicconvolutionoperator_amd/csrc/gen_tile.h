@@ -50,8 +50,9 @@ struct TileGeom {
   int LH, LW;   // halo tile rows / columns
   int npix;     // LH * LW
   int plane;    // bytes of one 4-channel plane of the halo tile (256-byte multiple)
-  int pad;      // BX partial rows: halo column j is stored at position j + pad ...
+  int pad;      // halo column j <-> position j + pad (R + pad = 0 mod 4) ...
   int LWp;      // ... of a row of LWp (multiple of 4) positions; see gen_tile_body
+  int vec;      // W % 4 == 0: 4-column groups at positions 4k are whole inside or outside the image
 };
 
 // Tiling and LDS bytes for a tile of 16 x 16*cb pixels whose LDS tile holds
@@ -75,6 +76,7 @@ inline int tile_geom(TileGeom& f, const GenGeom& g, int entry, int parts, int cb
   f.npix = f.LH * f.LW;
   f.pad = (4 - g.R % 4) % 4;
   f.LWp = (f.LW + f.pad + 3) / 4 * 4;
+  f.vec = g.W % 4 == 0;
   // planes start on 256-byte boundaries: the four quads of a wave then read
   // their 4-channel entries with the fewest LDS bank conflicts (measured)
   f.plane = (f.npix * entry + 255) / 256 * 256;
@@ -99,6 +101,32 @@ __device__ __forceinline__ void gf_store_raw(BufRes r, uint32_t off, uint32_t v)
     __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
   else
     __builtin_amdgcn_raw_buffer_store_b16((unsigned short)v, r, off, 0, 0);
+}
+
+// 4 consecutive elements at byte offset `off` (16-byte aligned for fp32,
+// 8-byte for 2-byte types) as raw bits, one element per dword, and the
+// matching store.
+template <int E>
+__device__ __forceinline__ void gf_load4_raw(BufRes r, uint32_t off, uint32_t (&v)[4]) {
+  if constexpr (E == 4) {
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) v[m] = a[m];
+  } else {
+    const auto a = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) v[m] = (a[m >> 1] >> (16 * (m & 1))) & 0xffffu;
+  }
+}
+template <int E>
+__device__ __forceinline__ void gf_store4_raw(BufRes r, uint32_t off, const uint32_t (&v)[4]) {
+  if constexpr (E == 4) {
+    __builtin_amdgcn_raw_buffer_store_b128((u32x4){v[0], v[1], v[2], v[3]}, r, off, 0, 0);
+  } else {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    __builtin_amdgcn_raw_buffer_store_b64((u32x2){v[0] | (v[1] << 16), v[2] | (v[3] << 16)}, r,
+                                          off, 0, 0);
+  }
 }
 
 // a: x (forward) or grad_cat (BX); out: the concat (forward); part: the
@@ -186,48 +214,85 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
     for (int i = tid; i < g.plane / 4; i += kGtThreads)
       reinterpret_cast<f32x4*>(xs)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   } else {
-    // ---- halo tile of x (zero outside the image) -> LDS planes; interior
-    //      pixels also go to the identity channels of the output.  Two pixels
-    //      per thread and batch: 32 loads in flight before any LDS write.
+    // ---- halo tile of x (zero outside the image) -> LDS planes; the tile's
+    //      own pixels also go to the identity channels of the output
     const BufRes xres = make_buf(a + ((int64_t)n * C + c0) * HW, (uint32_t)nch * HWE);
     const BufRes ores = make_buf(out + ((int64_t)n * 4 * C + c0) * HW, (uint32_t)nch * HWE);
-    for (int p0 = tid; p0 < g.npix; p0 += 2 * kGtThreads) {
-      uint32_t lo[2], so[2];
-      int pix[2];
+    if (g.vec) {
+      // a task = (4-channel plane, halo row, 4 image columns a multiple of 4
+      // apart from column 0): one 16-byte (8-byte) access per channel, the
+      // 4 x 4 block transposed in registers into four 4-channel entries
+      const int gpr = g.LWp / 4, cpos = R + g.pad;
+      const int tasks = 4 * g.LH * gpr;
+      for (int task = tid; task < tasks; task += kGtThreads) {
+        const int k = task % gpr, rest = task / gpr;
+        const int i = rest % g.LH, grp = rest / g.LH;
+        const int gh = h0 - R + i, gc = w0 - cpos + 4 * k;
+        const bool in = (unsigned)gh < (unsigned)H && (unsigned)gc < (unsigned)W;
+        const uint32_t off = in ? (uint32_t)(gh * W + gc) * (uint32_t)E : kOob;
+        uint32_t v[4][4];  // [channel][column]
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        pix[s] = p0 + s * kGtThreads;
-        const int i = pix[s] / LW, j = pix[s] - i * LW;
-        const int gh = h0 - R + i, gw = w0 - R + j;
-        const bool in =
-            pix[s] < g.npix && (unsigned)gh < (unsigned)H && (unsigned)gw < (unsigned)W;
-        const bool inner = i >= R && i < R + kGtTH && j >= R && j < R + TW;
-        lo[s] = in ? (uint32_t)(gh * W + gw) * (uint32_t)E : kOob;
-        so[s] = (in && inner) ? lo[s] : kOob;
-      }
-      uint32_t v[2][16];
+        for (int e = 0; e < 4; ++e) gf_load4_raw<E>(xres, off + (uint32_t)(4 * grp + e) * HWE, v[e]);
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int ch = 0; ch < 16; ++ch) v[s][ch] = gf_load_raw<E>(xres, lo[s] + ch * HWE);
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int ch = 0; ch < 16; ++ch) gf_store_raw<E>(ores, so[s] + ch * HWE, v[s][ch]);
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        if (pix[s] >= g.npix) continue;
-#pragma unroll
-        for (int grp = 0; grp < 4; ++grp) {
+        for (int m = 0; m < 4; ++m) {
+          const int j = 4 * k + m - g.pad;
+          if (j < 0 || j >= LW) continue;
           XQ q;
           if constexpr (E == 4) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) q[e] = v[s][4 * grp + e];
+            for (int e = 0; e < 4; ++e) q[e] = v[e][m];
           } else {
-            q[0] = v[s][4 * grp] | (v[s][4 * grp + 1] << 16);
-            q[1] = v[s][4 * grp + 2] | (v[s][4 * grp + 3] << 16);
+            q[0] = v[0][m] | (v[1][m] << 16);
+            q[1] = v[2][m] | (v[3][m] << 16);
           }
-          *reinterpret_cast<XQ*>(xs + grp * g.plane + pix[s] * XB) = q;
+          *reinterpret_cast<XQ*>(xs + grp * g.plane + (i * LW + j) * XB) = q;
+        }
+        if (i >= R && i < R + kGtTH && 4 * k >= cpos && 4 * k < cpos + TW) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) gf_store4_raw<E>(ores, off + (uint32_t)(4 * grp + e) * HWE, v[e]);
+        }
+      }
+    } else {
+      // element-wise: two pixels per thread and batch, 32 loads in flight
+      // before any LDS write
+      for (int p0 = tid; p0 < g.npix; p0 += 2 * kGtThreads) {
+        uint32_t lo[2], so[2];
+        int pix[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          pix[s] = p0 + s * kGtThreads;
+          const int i = pix[s] / LW, j = pix[s] - i * LW;
+          const int gh = h0 - R + i, gw = w0 - R + j;
+          const bool in =
+              pix[s] < g.npix && (unsigned)gh < (unsigned)H && (unsigned)gw < (unsigned)W;
+          const bool inner = i >= R && i < R + kGtTH && j >= R && j < R + TW;
+          lo[s] = in ? (uint32_t)(gh * W + gw) * (uint32_t)E : kOob;
+          so[s] = (in && inner) ? lo[s] : kOob;
+        }
+        uint32_t v[2][16];
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int ch = 0; ch < 16; ++ch) v[s][ch] = gf_load_raw<E>(xres, lo[s] + ch * HWE);
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int ch = 0; ch < 16; ++ch) gf_store_raw<E>(ores, so[s] + ch * HWE, v[s][ch]);
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          if (pix[s] >= g.npix) continue;
+#pragma unroll
+          for (int grp = 0; grp < 4; ++grp) {
+            XQ q;
+            if constexpr (E == 4) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) q[e] = v[s][4 * grp + e];
+            } else {
+              q[0] = v[s][4 * grp] | (v[s][4 * grp + 1] << 16);
+              q[1] = v[s][4 * grp + 2] | (v[s][4 * grp + 3] << 16);
+            }
+            *reinterpret_cast<XQ*>(xs + grp * g.plane + pix[s] * XB) = q;
+          }
         }
       }
     }
@@ -242,10 +307,8 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
   wput(0);
   if (NBT > 1) wload(1);
 
-  // ---- y operand (unshifted pixels) of this wave's blocks; per block the
-  //      LDS address of this lane's tile entry at zero shift
+  // ---- y operand (unshifted pixels) of this wave's blocks
   V bfr[NBW][NK][P];
-  uint32_t pbase[NBW];
   auto pix_off = [&](int blk) {  // byte offset of this lane's pixel in a plane
     const int gh = h0 + 2 * wave + blk / CB, gw = w0 + 16 * (blk % CB) + col16;
     return (gh < H && gw < W) ? (uint32_t)(gh * W + gw) * (uint32_t)E : kOob;
@@ -254,9 +317,7 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
     const BufRes yres = make_buf(y + (int64_t)n * C * HW, (uint32_t)C * HWE);
 #pragma unroll
     for (int blk = 0; blk < NBW; ++blk) {
-      const int lrow = 2 * wave + blk / CB, lcol = 16 * (blk % CB) + col16;
       const uint32_t po = pix_off(blk);
-      pbase[blk] = (uint32_t)(quad * g.plane + ((lrow + R) * LW + lcol + R) * XB);
 #pragma unroll
       for (int kk = 0; kk < NK; ++kk) {
         float v[8];
@@ -271,6 +332,31 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
   }
   __syncthreads();
 
+  // Addresses inside the loop are a lane part, kept in a few registers, plus
+  // a part uniform over the wave; the asm barriers below keep the compiler
+  // from hoisting their per-(block, channel) sums out of the loop, which
+  // would hold one register each.
+  //   LDS entry of this lane's pixel in block blk at zero shift:
+  //     lbase + ebase(blk)
+  const uint32_t lbase = (uint32_t)(quad * g.plane + col16 * XB);
+  auto ebase = [&](int blk) {
+    return (uint32_t)(((2 * wave + blk / CB + R) * LW + 16 * (blk % CB) + R) * XB);
+  };
+  //   global byte offset of channel 4*quad + e at this lane's pixel of block
+  //   blk within a channel block's planes: lofs[blk % CB] + row and channel
+  //   parts (kOob outside the image or the channel block)
+  uint32_t lofs[CB];
+#pragma unroll
+  for (int cp = 0; cp < CB; ++cp) {
+    const int gw = w0 + 16 * cp + col16;
+    lofs[cp] = (gw < W && 4 * quad < nch) ? (uint32_t)gw * E + (uint32_t)(4 * quad) * HWE : kOob;
+  }
+  const int emax = nch - 4 * quad;  // channels 4*quad + e with e < emax exist
+  auto goff = [&](const uint32_t (&lo)[CB], int blk, int e) {
+    const int gh = h0 + 2 * wave + blk / CB;
+    return (gh < H && e < emax) ? lo[blk % CB] + (uint32_t)(gh * W) * E + (uint32_t)e * HWE : kOob;
+  };
+
   f32x4 acc[NBW];   // forward: branch output of this lane's 4 channels per block
   float go[NBW][4];  // BX: the branch gradient gO_b at this lane's pixel and 4 channels
 #pragma unroll 1
@@ -284,18 +370,23 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
       if (t == 0) {
         const BufRes gres = make_buf(a + ((int64_t)n * 4 * C + (int64_t)(b + 1) * C + c0) * HW,
                                      (uint32_t)nch * HWE);
+        uint32_t lo[CB];
 #pragma unroll
-        for (int blk = 0; blk < NBW; ++blk) {
-          const uint32_t po = pix_off(blk);
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            go[blk][e] = buf_load1<T>(gres, po + (uint32_t)(4 * quad + e) * HWE);
+        for (int cp = 0; cp < CB; ++cp) {
+          lo[cp] = lofs[cp];
+          asm volatile("" : "+v"(lo[cp]));
         }
+#pragma unroll
+        for (int blk = 0; blk < NBW; ++blk)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) go[blk][e] = buf_load1<T>(gres, goff(lo, blk, e));
       }
     }
     const int ki = t / KS, kj = t - ki * KS;
     const int d = dil_of(b, g.d0, g.d1, g.d2);
     const int shift = ((ki - r) * d * LW + (kj - r) * d) * XB;
+    uint32_t lb = lbase;
+    asm volatile("" : "+v"(lb));
     const unsigned char* __restrict__ ab = abuf + (bt & 1) * AU * 16;
     V afr[NK][P];
 #pragma unroll
@@ -322,7 +413,7 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
     if constexpr (BX) {
 #pragma unroll
       for (int blk = 0; blk < NBW; ++blk) {
-        f32x4* __restrict__ pa = reinterpret_cast<f32x4*>(xs + pbase[blk] + shift);
+        f32x4* __restrict__ pa = reinterpret_cast<f32x4*>(xs + lb + ebase(blk) + shift);
         f32x4 s = *pa;
 #pragma unroll
         for (int e = 0; e < 4; ++e) s[e] = fmaf(quant<T>(dacc[blk][e]), go[blk][e], s[e]);
@@ -331,7 +422,7 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
     } else {
 #pragma unroll
       for (int blk = 0; blk < NBW; ++blk) {
-        const XQ xq = *reinterpret_cast<const XQ*>(xs + pbase[blk] + shift);
+        const XQ xq = *reinterpret_cast<const XQ*>(xs + lb + ebase(blk) + shift);
         float xv[4];
         if constexpr (E == 4) {
 #pragma unroll
@@ -348,13 +439,16 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
         // ---- branch b: channels c0 + 4*quad + e of output block b+1
         const BufRes bres = make_buf(out + ((int64_t)n * 4 * C + (int64_t)(b + 1) * C + c0) * HW,
                                      (uint32_t)nch * HWE);
+        uint32_t lo[CB];
 #pragma unroll
-        for (int blk = 0; blk < NBW; ++blk) {
-          const uint32_t po = pix_off(blk);
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            buf_store1<T>(bres, po + (uint32_t)(4 * quad + e) * HWE, acc[blk][e]);
+        for (int cp = 0; cp < CB; ++cp) {
+          lo[cp] = lofs[cp];
+          asm volatile("" : "+v"(lo[cp]));
         }
+#pragma unroll
+        for (int blk = 0; blk < NBW; ++blk)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) buf_store1<T>(bres, goff(lo, blk, e), acc[blk][e]);
       }
     }
     __syncthreads();
