@@ -468,8 +468,12 @@ int launch_ks(FilterOp op, const void* a, const void* b, void* o, const FilterGe
         return launch_kernel(filter_bwd_k_kernel<TX, TK, KS, 4>, g, lds1, stream, (const TX*)a, (const TK*)b, (TK*)o, g);
       return launch_kernel(filter_bwd_k_kernel<TX, TK, KS, 1>, g, lds1, stream, (const TX*)a, (const TK*)b, (TK*)o, g);
     case FilterOp::kBwdX:
-      if (vec == 4)
-        return launch_kernel(filter_bwd_x_kernel<TX, TK, KS, 4>, g, 3 * lds1, stream, (const TK*)a, (const TK*)b, (TX*)o, g);
+      // 4 pixels per lane only for K <= 3 (larger K would not keep the
+      // in-flight kernel values in registers)
+      if constexpr (KS >= 1 && KS <= 3) {
+        if (vec == 4)
+          return launch_kernel(filter_bwd_x_kernel<TX, TK, KS, 4>, g, 3 * lds1, stream, (const TK*)a, (const TK*)b, (TX*)o, g);
+      }
       return launch_kernel(filter_bwd_x_kernel<TX, TK, KS, 1>, g, 3 * lds1, stream, (const TK*)a, (const TK*)b, (TX*)o, g);
   }
   return kBadArgument;
