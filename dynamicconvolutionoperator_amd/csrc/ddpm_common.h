@@ -240,6 +240,20 @@ __device__ __forceinline__ void buf_load8(BufRes r, uint32_t off, float (&v)[8])
   }
 }
 
+// Workgroup barrier for loops whose waves exchange data through LDS only:
+// waits for this wave's LDS (and scalar) operations, then s_barrier.
+// __syncthreads() also waits for every outstanding global load and store
+// (vmcnt(0)), which would stall each step on stores and on loads that are
+// only consumed later; the compiler still waits for a global load before the
+// first use of its register.  The empty asm statements keep the compiler
+// from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // vmcnt(63) expcnt(7) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).
 // Remap the hardware block id so that each XCD receives one contiguous range of
 // logical block ids: neighbouring spatial tiles (which share halo rows) then

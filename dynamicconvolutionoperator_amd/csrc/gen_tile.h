@@ -451,7 +451,7 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
           for (int e = 0; e < 4; ++e) buf_store1<T>(bres, goff(lo, blk, e), acc[blk][e]);
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
 
   if constexpr (BX) {
