@@ -36,7 +36,7 @@ def _load_hip_ops():
     from . import _lib, ops
 
     _lib.load()
-    return ops.fused_dynamic_cat, ops.fused_generator_dynamic_cat, ops.generator_supported
+    return ops.fused_dynamic_cat, ops.fused_generator_dynamic_cat, ops.generator_supported, ops._generate
 
 
 def _check_inputs(x: torch.Tensor, y: torch.Tensor, channels: int) -> None:
@@ -122,12 +122,19 @@ class DDPM(nn.Module):
         return "fused" if can_fuse else "materialized"
 
     def _cuda_cat(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
-        fused_dynamic_cat, fused_generator_dynamic_cat, gen_supported = _load_hip_ops()
+        fused_dynamic_cat, fused_generator_dynamic_cat, gen_supported, generate = _load_hip_ops()
         if self._route(x, y, gen_supported) == "fused":
             return fused_generator_dynamic_cat(
                 x, y, self.generator.weight, self.generator.bias, self.kernel_size, self.dilations
             )
-        kernels = self.generator(y).reshape(
+        # the generator 1x1 convolution: the HIP MFMA kernel where it applies;
+        # under autocast the Conv2d runs in the autocast dtype, as the
+        # reference's does (the filter's output dtype follows the kernels')
+        if torch.is_autocast_enabled(y.device.type):
+            kernels = self.generator(y)
+        else:
+            kernels = generate(y, self.generator.weight, self.generator.bias, self.kernel_size)
+        kernels = kernels.reshape(
             x.shape[0], len(self.dilations), self.dim, self.kernel_size**2, x.shape[2], x.shape[3]
         )
         return fused_dynamic_cat(x, kernels, self.kernel_size, self.dilations)

@@ -236,9 +236,88 @@ class _GeneratorDynamicCat(torch.autograd.Function):
         return grad_x, grad_y, grad_w, grad_b, None, None
 
 
+# ---------------------------------------------------------------------------
+# Generator 1x1 convolution of the materialized route
+# ---------------------------------------------------------------------------
+GENERATOR_KERNELS_MAX_CHANNELS = 128  # ddpm_gen_kernels keeps y's K operand in registers
+
+
+def generator_kernels_supported(y, weight, bias) -> bool:
+    """Whether ``ddpm_gen_kernels`` computes this generator convolution: one
+    dtype for y, weight and bias, and at most 128 channels."""
+    return (
+        bias is not None
+        and y.dtype in _DTYPES
+        and y.dtype == weight.dtype == bias.dtype
+        and y.shape[1] <= GENERATOR_KERNELS_MAX_CHANNELS
+    )
+
+
+class _GeneratorKernels(torch.autograd.Function):
+    """``kernels = conv2d(y, weight, bias)`` for the 1x1 generator, as
+    ``[N, 3CK², H, W]`` in y's dtype (the reference's ``self.generator(y)``,
+    triton_impl.py:340-347).  Forward: one HIP MFMA kernel with the bias and
+    the output rounding fused.  Backward: the Conv2d gradients as batched
+    products -- dY = Wᵀ·dK, dW = Σ_n dK·yᵀ, db = Σ dK."""
+
+    @staticmethod
+    def forward(ctx, y, weight, bias, kernel_size):
+        k = _check_kernel_size(kernel_size)
+        y = y.contiguous()
+        n, c, h, w = y.shape
+        o = 3 * c * k * k
+        if tuple(weight.shape) not in ((o, c, 1, 1), (o, c)) or tuple(bias.shape) != (o,):
+            raise ValueError(
+                f"generator weight / bias must be [{o}, {c}, 1, 1] / [{o}], got "
+                f"{tuple(weight.shape)} / {tuple(bias.shape)}"
+            )
+        _require_device(y, weight, bias)
+        w2 = weight.reshape(o, c).contiguous()
+        b = bias.contiguous()
+        out = torch.empty((n, o, h, w), dtype=y.dtype, device=y.device)
+        lib = _lib.load()
+        with torch.cuda.device(y.device):
+            code = lib.ddpm_gen_kernels(_ptr(y), _ptr(w2), _ptr(b), _ptr(out), n, c, h, w, k, _dt(y),
+                                        _stream(y))
+        _lib.check(code, "ddpm_gen_kernels")
+        ctx.save_for_backward(y, w2)
+        ctx.weight_shape = tuple(weight.shape)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        y, w2 = ctx.saved_tensors
+        n, c, h, w = y.shape
+        o = w2.shape[0]
+        g = grad.to(y.dtype).contiguous().view(n, o, h * w)
+        grad_y = grad_w = grad_b = None
+        if ctx.needs_input_grad[0]:
+            grad_y = torch.matmul(w2.t().contiguous(), g).view(n, c, h, w)
+        if ctx.needs_input_grad[1]:
+            gw = torch.matmul(g, y.view(n, c, h * w).transpose(1, 2).contiguous())
+            gw = gw[0] if n == 1 else gw.float().sum(0).to(y.dtype)
+            grad_w = gw.reshape(ctx.weight_shape)
+        if ctx.needs_input_grad[2]:
+            grad_b = g.sum(dim=(0, 2))
+        return grad_y, grad_w, grad_b, None
+
+
+def generator_kernels(y, weight, bias, kernel_size):
+    """The 1x1 generator convolution ``[N, 3CK², H, W]`` of the materialized
+    route through ``ddpm_gen_kernels`` (shapes and dtypes of
+    :func:`generator_kernels_supported`)."""
+    return _GeneratorKernels.apply(y, weight, bias, kernel_size)
+
+
+def _generate(y, weight, bias, k):
+    if generator_kernels_supported(y, weight, bias):
+        return generator_kernels(y, weight, bias, k)
+    return torch.nn.functional.conv2d(y, weight, bias)
+
+
 def _materialized_generator_dynamic_cat(x, y, weight, bias, k, dil):
     n, c, h, w = x.shape
-    kernels = torch.nn.functional.conv2d(y, weight, bias).reshape(n, 3, c, k * k, h, w)
+    kernels = _generate(y, weight, bias, k).reshape(n, 3, c, k * k, h, w)
     return fused_dynamic_cat(x, kernels, k, dil)
 
 
@@ -259,4 +338,10 @@ def fused_generator_dynamic_cat(x, y, weight, bias, kernel_size, dilations):
     return _launch_generator_dynamic_cat(x, y, weight, bias, k, dil)
 
 
-__all__ = ["fused_dynamic_cat", "fused_generator_dynamic_cat", "generator_supported"]
+__all__ = [
+    "fused_dynamic_cat",
+    "fused_generator_dynamic_cat",
+    "generator_supported",
+    "generator_kernels",
+    "generator_kernels_supported",
+]

@@ -51,6 +51,17 @@ const char* ddpm_status_string(int code);
  * (ddpm_filter_*), with identical results. */
 int ddpm_gen_supported(int64_t c, int kernel_size, int max_dilation);
 
+/* The generator's 1x1 convolution on the materialized route:
+ * kernels[n][o][p] = sum_i weight[o][i] * y[n][i][p] + bias[o] for
+ * o < 3*c*k*k, rounded once to `dtype`, written in the [n][3][c][k*k][h][w]
+ * layout the ddpm_filter_* entry points read.  weight: [3*c*k*k][c] (the
+ * Conv2d weight without its trailing 1x1), bias: [3*c*k*k].  c <= 128
+ * (kUnsupported beyond); any kernel size.
+ * Replaces the cuDNN 1x1 convolution self.generator(y) of the reference's
+ * materialized path (triton_impl.py:340-347). */
+int ddpm_gen_kernels(const void* y, const void* weight, const void* bias, void* kernels, int64_t n,
+                     int64_t c, int64_t h, int64_t w, int kernel_size, int dtype, hipStream_t stream);
+
 /* ---- materialized dynamic filter ------------------------------------- */
 
 /* out = [x, d0, d1, d2] from materialized kernels; out has k_dtype, and the

@@ -165,6 +165,39 @@ def test_generator_dilation_sets(K, dil, fused, shape, dtype):
         assert_close(a, e, atol * scale, rtol, f"gen {name}")
 
 
+# ---------------------------------------------------------------- generator 1x1 conv (materialized route)
+@pytest.mark.parametrize(
+    "shape,K",
+    [
+        ((2, 24, 15, 17), 5),  # H*W % 4 != 0: element-wise stores
+        ((1, 20, 16, 16), 3),  # C % 8 != 0: element-wise weight loads
+        ((1, 64, 32, 32), 5),  # the K = 5 configuration's channel count
+        ((1, 128, 8, 12), 1),  # the largest C, four 32-channel K steps
+    ],
+)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_generator_kernels_match_oracle(shape, K, dtype):
+    n, c, h, w = shape
+    say(f"generator kernels shape={shape} K={K} dtype={dtype}")
+    y = randn(shape, 70, dtype)
+    wt, b = default_generator_params(c, K, 71, dtype)
+    g = randn((n, 3 * c * K * K, h, w), 72, dtype)
+    yd, wd, bd = (t.to(DEV).requires_grad_() for t in (y, wt, b))
+    assert ops.generator_kernels_supported(yd, wd, bd)
+    out = ops.generator_kernels(yd, wd, bd, K)
+    assert out.dtype == dtype and tuple(out.shape) == (n, 3 * c * K * K, h, w)
+    out.backward(g.to(DEV))
+    y64, w64, b64, g64 = (t.double().requires_grad_() for t in (y, wt, b, g))
+    e = ref.generated_kernels(y64, w64, b64, K).reshape(n, -1, h, w)
+    atol, rtol = TOL["gen_fwd"][dtype]
+    assert_close(out, e, atol, rtol, "generator kernels")
+    dy, dw, db = torch.autograd.grad(e, (y64, w64, b64), g64.detach())
+    atol, rtol = TOL["gen_bwd"][dtype]
+    for name, a, ex in (("dy", yd.grad, dy), ("dw", wd.grad, dw), ("db", bd.grad, db)):
+        scale = max(1.0, ex.abs().max().item())
+        assert_close(a, ex, atol * scale, rtol, f"generator kernels {name}")
+
+
 def test_generator_inference_has_no_autograd_graph():
     x = randn((1, 8, 9, 16), 40).to(DEV)
     y = randn((1, 8, 9, 16), 41).to(DEV)

@@ -68,8 +68,13 @@ def test_entry_points_validate_arguments_before_touching_the_device():
     assert lib.ddpm_filter_fwd(null, null, null, 1, 1, 4, 4, 3, 1, 3, 5, 0, 0, null) == 10001
     assert lib.ddpm_gen_fwd(null, null, null, null, null, 1, 65, 4, 4, 3, 1, 3, 5, 0, null) == 10002
     assert lib.ddpm_gen_bwd_w(null, null, null, null, null, null, 0, 1, 64, 256, 256, 3, 1, 3, 5, 0, null) != 0
+    # the generator 1x1 convolution: even kernel size, more than 128 channels
+    assert lib.ddpm_gen_kernels(null, null, null, null, 1, 64, 8, 8, 4, 1, null) == 10001
+    assert lib.ddpm_gen_kernels(null, null, null, null, 1, 129, 8, 8, 5, 1, null) == 10002
+    assert lib.ddpm_gen_kernels(null, null, null, null, 1, 64, 8, 8, 5, 1, null) == 10001
     # empty tensors are a no-op
     assert lib.ddpm_filter_fwd(null, null, null, 0, 4, 4, 4, 3, 1, 3, 5, 0, 0, null) == 0
+    assert lib.ddpm_gen_kernels(null, null, null, null, 0, 64, 8, 8, 5, 1, null) == 0
 
 
 class _FakeTensor:
