@@ -12,8 +12,12 @@
 // store stream.  MFMA GEMM with M = 16 pixels, N = 16 output rows o and K =
 // the input channels (v_mfma_f32_16x16x32_{bf16,f16}; fp32 runs as three
 // bf16 products, hi*hi + hi*lo + lo*hi): a lane's result is 4 consecutive
-// pixels of one output row, stored with the bias added and rounded once as
-// one 8-byte (2-byte types) / 16-byte (fp32) write.  A wave keeps the y
+// pixels of one output row, stored with the bias added and rounded once.
+// fp32: one 16-byte write per block (a store instruction covers 16 rows x 64
+// contiguous bytes).  2-byte types: the A rows of a pair of 16-pixel blocks
+// interleave 4-pixel groups (row m of block 2j+s is pixel 32j + 8*(m/4) + 4s
+// + m%4), so a lane holds 8 consecutive pixels of its row across the pair and
+// writes them as one 16 bytes (measured 27% faster than two 8-byte writes).  A wave keeps the y
 // operand of its 64 pixels in registers for every output row of its chunk and
 // streams the weight rows (16 bytes = 8 consecutive input channels per lane;
 // all waves read the same rows, so they come from L1 / L2).
@@ -35,7 +39,7 @@ struct GkGeom {
   int tiles;    // ceil(HW / kGkTP)
   int ochunks;  // output-row chunks per pixel tile
   int obpc;     // 16-row output blocks per chunk
-  int vec;      // HW % 4 == 0: a lane's 4 pixels are stored whole
+  int vec;      // HW % 8 == 0 (fp32: % 4): a lane's 8 (4) pixels are stored whole
   int wvec;     // C % 8 == 0: 8 consecutive weights are one aligned vector
 };
 
@@ -85,13 +89,17 @@ __global__ __launch_bounds__(kGkThreads) void gen_kernels_kernel(const T* __rest
   const int C = g.C, HW = g.HW, O = g.O;
   const int p0 = tile * kGkTP + wave * 16 * kGkBlocks;  // first pixel of this wave
 
-  // ---- y operand: A row m = pixel p0 + 16*blk + m, K = input channels
+  // ---- y operand: A row m of block blk = pixel p0 + 16*blk + m (fp32) or
+  //      p0 + 32*(blk/2) + 8*(m/4) + 4*(blk%2) + m%4 (2-byte types, the pair
+  //      interleave above), K = input channels
+  constexpr bool kPair = E == 2;
   V afr[kGkBlocks][NK][P];
   {
     const BufRes yres = make_buf(y + (int64_t)n * C * HW, (uint32_t)C * (uint32_t)HW * E);
 #pragma unroll
     for (int blk = 0; blk < kGkBlocks; ++blk) {
-      const int px = p0 + 16 * blk + col16;
+      const int px = kPair ? p0 + 32 * (blk >> 1) + 8 * (col16 >> 2) + 4 * (blk & 1) + (col16 & 3)
+                           : p0 + 16 * blk + col16;
       const uint32_t po = px < HW ? (uint32_t)px * E : kOob;
 #pragma unroll
       for (int kk = 0; kk < NK; ++kk) {
@@ -128,29 +136,55 @@ __global__ __launch_bounds__(kGkThreads) void gen_kernels_kernel(const T* __rest
     }
     const float bv = buf_load1<T>(bres, orow ? (uint32_t)o * E : kOob);
     const uint32_t rowoff = (uint32_t)o * (uint32_t)HW;
+    if constexpr (!kPair) {
+      // fp32: pixels px .. px+3 of row o per block
 #pragma unroll
-    for (int blk = 0; blk < kGkBlocks; ++blk) {
-      f32x4 acc = {bv, bv, bv, bv};
+      for (int blk = 0; blk < kGkBlocks; ++blk) {
+        f32x4 acc = {bv, bv, bv, bv};
 #pragma unroll
-      for (int kk = 0; kk < NK; ++kk) acc = M::mac(afr[blk][kk], bfr[kk], acc);
-      // pixels px .. px+3 of row o
-      const int px = p0 + 16 * blk + 4 * quad;
-      if (vec) {
-        const uint32_t off = (orow && px < HW) ? (rowoff + (uint32_t)px) * E : kOob;
-        if constexpr (E == 4) {
-          const u32x4 a = {__float_as_uint(acc[0]), __float_as_uint(acc[1]),
-                           __float_as_uint(acc[2]), __float_as_uint(acc[3])};
-          __builtin_amdgcn_raw_buffer_store_b128(a, ores, off, 0, 0);
+        for (int kk = 0; kk < NK; ++kk) acc = M::mac(afr[blk][kk], bfr[kk], acc);
+        const int px = p0 + 16 * blk + 4 * quad;
+        if (vec) {
+          const uint32_t off = (orow && px < HW) ? (rowoff + (uint32_t)px) * E : kOob;
+          __builtin_amdgcn_raw_buffer_store_b128(
+              (u32x4){__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]),
+                      __float_as_uint(acc[3])},
+              ores, off, 0, 0);
         } else {
-          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-          typedef T T4 __attribute__((ext_vector_type(4)));
-          const T4 t = {from_f<T>(acc[0]), from_f<T>(acc[1]), from_f<T>(acc[2]), from_f<T>(acc[3])};
-          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, t), ores, off, 0, 0);
-        }
-      } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          buf_store1<T>(ores, (orow && px + r < HW) ? (rowoff + (uint32_t)(px + r)) * E : kOob, acc[r]);
+          for (int r = 0; r < 4; ++r)
+            buf_store1<T>(ores, (orow && px + r < HW) ? (rowoff + (uint32_t)(px + r)) * E : kOob,
+                          acc[r]);
+        }
+      }
+    } else {
+      // 2-byte types: pixels px .. px+7 of row o per block pair, px = p0 + 32j + 8*quad
+#pragma unroll
+      for (int j = 0; j < kGkBlocks / 2; ++j) {
+        f32x4 acc[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          acc[s] = f32x4{bv, bv, bv, bv};
+#pragma unroll
+          for (int kk = 0; kk < NK; ++kk) acc[s] = M::mac(afr[2 * j + s][kk], bfr[kk], acc[s]);
+        }
+        const int px = p0 + 32 * j + 8 * quad;
+        if (vec) {
+          typedef T T8 __attribute__((ext_vector_type(8)));
+          const T8 t = {from_f<T>(acc[0][0]), from_f<T>(acc[0][1]), from_f<T>(acc[0][2]),
+                        from_f<T>(acc[0][3]), from_f<T>(acc[1][0]), from_f<T>(acc[1][1]),
+                        from_f<T>(acc[1][2]), from_f<T>(acc[1][3])};
+          const uint32_t off = (orow && px < HW) ? (rowoff + (uint32_t)px) * E : kOob;
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, t), ores, off, 0, 0);
+        } else {
+#pragma unroll
+          for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int pr = px + 4 * s + r;
+              buf_store1<T>(ores, (orow && pr < HW) ? (rowoff + (uint32_t)pr) * E : kOob, acc[s][r]);
+            }
+        }
       }
     }
   }
@@ -203,7 +237,7 @@ extern "C" int ddpm_gen_kernels(const void* y, const void* weight, const void* b
   if (want < 1) want = 1;
   g.obpc = (int)((nob + want - 1) / want);
   g.ochunks = (int)((nob + g.obpc - 1) / g.obpc);
-  g.vec = hw % 4 == 0 && (uintptr_t)kernels % 16 == 0;
+  g.vec = hw % (esz == 4 ? 4 : 8) == 0 && (uintptr_t)kernels % 16 == 0;
   g.wvec = c % 8 == 0 && (uintptr_t)weight % 16 == 0;
   const int64_t groups = n * g.tiles * g.ochunks;
   if (groups > 0x7fffffffLL) return kUnsupported;
