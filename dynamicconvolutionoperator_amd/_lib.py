@@ -28,6 +28,8 @@ SIGNATURES: dict[str, tuple[list, type]] = {
     "ddpm_status_string": ([_I], ctypes.c_char_p),
     "ddpm_gen_supported": ([_L, _I, _I], _I),
     "ddpm_gen_kernels": ([_P, _P, _P, _P, _L, _L, _L, _L, _I, _I, _P], _I),
+    "ddpm_gen_kernels_bwd_w_workspace_bytes": ([_L, _L, _L, _L, _I], _L),
+    "ddpm_gen_kernels_bwd_w": ([_P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _P], _I),
     "ddpm_filter_fwd": (_FILTER_ARGS, _I),
     "ddpm_filter_bwd_x": (_FILTER_ARGS, _I),
     "ddpm_filter_bwd_k": (_FILTER_ARGS, _I),

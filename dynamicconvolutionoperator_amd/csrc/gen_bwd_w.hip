@@ -498,6 +498,13 @@ __global__ __launch_bounds__(256) void gen_bwd_w_reduce_kernel(const float* __re
   }
 }
 
+int launch_ysplit(const float* y, uint16_t* ys, int64_t chw, int64_t total, hipStream_t stream) {
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(gen_ysplit_kernel, dim3((unsigned)((total + 2047) / 2048)), dim3(256), 0,
+                     stream, y, ys, chw, total);
+  return (int)hipGetLastError();
+}
+
 namespace {
 
 template <typename F>
@@ -609,10 +616,7 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
   float* pw = g.direct ? nullptr : (float*)workspace;
   float* pb = g.direct ? nullptr : pw + (int64_t)g.splits * 3 * kk * c * c;
   if (dtype == kF32) {
-    const int64_t total = n * c * h * w;
-    hipLaunchKernelGGL(gen_ysplit_kernel, dim3((unsigned)((total + 2047) / 2048)), dim3(256), 0,
-                       stream, (const float*)y, ys, c * h * w, total);
-    const int e = (int)hipGetLastError();
+    const int e = launch_ysplit((const float*)y, ys, c * h * w, n * c * h * w, stream);
     if (e != 0) return e;
   }
   return wg_with_type(dtype, [&](auto tag) {

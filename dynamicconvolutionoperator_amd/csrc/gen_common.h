@@ -20,4 +20,9 @@ int gen_make_geom(GenGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int k,
 // Largest dilation the fused backward kernels stage (their column halo).
 constexpr int kGenMaxDil = 8;
 
+// Launches the split of an fp32 y [n][C][H*W] (chw = C*H*W elements per
+// image, total = n*chw) into its bf16 hi / lo planes ys [n][2][C][H*W] on
+// `stream`; returns the launch status.
+int launch_ysplit(const float* y, uint16_t* ys, int64_t chw, int64_t total, hipStream_t stream);
+
 }  // namespace ddpm

@@ -23,6 +23,7 @@
 // all waves read the same rows, so they come from L1 / L2).
 
 #include "gen_common.h"
+#include <algorithm>
 #include <type_traits>
 
 namespace ddpm {
@@ -190,6 +191,431 @@ __global__ __launch_bounds__(kGkThreads) void gen_kernels_kernel(const T* __rest
   }
 }
 
+// ---------------------------------------------------------------------------
+// Backward of the generator convolution, weight and bias:
+//
+//   dW[o][i] = sum_{n,p} dK[n][o][p] * y[n][i][p],   db[o] = sum_{n,p} dK[n][o][p]
+//
+// (the Conv2d weight / bias gradients of `self.generator` on the reference's
+// materialized path, triton_impl.py:340-347, computed there by cuDNN's
+// backward-filter convolution).  dK is 3*K*K times the size of y and is read
+// exactly once, so the kernel is built around that stream.  MFMA GEMM with
+// M = 16 rows o, N = 16 channels i and K = 32 pixels: both operands are rows
+// of the [o][p] / [i][p] planes, so a lane's fragment is 8 consecutive pixels
+// of one row.  fp32 runs as three bf16 products against the bf16 hi / lo
+// planes of y (split once per call); db is summed from the same dK values on
+// the VALU (fp32 accumulation).
+//
+// gk_bwd_w_lds_kernel (16-byte aligned planes, H*W % 8 == 0): a workgroup
+// owns 64 rows (16 per wave) and a range of pixel steps.  Per step the dK
+// tile (64 rows x 256 bytes) and the y tile (all channels) are copied global
+// -> LDS by 16-byte buffer loads that write LDS directly, four rows x 256
+// contiguous bytes per copy (measured 6.8 TB/s for this pattern against 5.2
+// for the 16 rows x 64 bytes a direct fragment load touches), one step ahead
+// into a second buffer; chunk c of row r sits at position c ^ (r & mask) so
+// that fragment reads of 16 rows hit distinct banks.  The four waves share
+// the y tile and own disjoint rows: no cross-wave reduction.
+// gk_bwd_w_kernel (any shape): fragments loaded element-wise straight into
+// registers, 4 waves taking 32-pixel steps in turn, summed through LDS in
+// wave order.
+// Workgroups of one row tile write fp32 partials over disjoint pixel ranges
+// that a second kernel sums in split order: deterministic, no atomics.
+// ---------------------------------------------------------------------------
+
+constexpr int kGwWaves = 4;
+constexpr int kGwStep = 32;       // pixels per MFMA step
+constexpr int kGwSlots = 512;     // workgroups the splits aim for (two per CU)
+
+struct GwGeom {
+  int N, C, HW, O;
+  int sp;               // pixels per step
+  int spi;              // steps per image, ceil(HW / sp)
+  int steps;            // N * spi
+  int rows;             // rows per workgroup
+  int row_tiles;        // ceil(O / rows)
+  int splits;
+  int steps_per_split;
+};
+
+// LDS-staged tiling per dtype and channel blocks.
+template <typename T, int CB>
+struct GwLds {
+  static constexpr int E = (int)sizeof(T);
+  static constexpr int P = Mma<T>::P;
+  static constexpr int SP = (CB <= 4 ? 64 : 32) * (4 / E);     // pixels per step (LDS <= 64 KB)
+  static constexpr int KC = SP / 32;                          // MFMA k-chunks per step
+  static constexpr int CPX = 16 / E;                          // pixels per 16-byte chunk of dK
+  static constexpr int ACH = SP / CPX;                        // chunks per dK tile row
+  static constexpr int YC = SP / 8;                           // chunks per y tile row (2-byte)
+  static constexpr int YROWS = P * CB * 16;
+  static constexpr int NA = ACH;                              // 1 KB copies of the 64-row dK tile
+  static constexpr int NY = YROWS * YC / 64;                  // 1 KB copies of the y tile
+  static constexpr int ABYTES = 64 * ACH * 16;
+  static constexpr int BUF = ABYTES + YROWS * YC * 16;        // bytes per staging buffer
+  static_assert(NA % kGwWaves == 0 && NY % kGwWaves == 0, "copies split evenly over the waves");
+};
+
+// 8 consecutive elements (pixels) of a plane row as raw MFMA operand dwords:
+// one 16-byte load per 16 bytes when VEC (the row offset is a multiple of 8
+// elements and the 8 pixels are all in or all out of the image), else
+// element-wise with every pixel masked on its own.  `off` is the element
+// offset of the first pixel, `ok` whether the row exists, `nv` the number of
+// valid pixels from the first.
+template <typename T, bool VEC>
+__device__ __forceinline__ void gw_load_row8(BufRes r, uint32_t off, bool ok, int nv,
+                                             u32x4 (&d)[sizeof(T) == 4 ? 2 : 1]) {
+  constexpr uint32_t E = sizeof(T);
+  if constexpr (VEC) {
+    const uint32_t b = (ok && nv > 0) ? off * E : kOob;
+    d[0] = __builtin_amdgcn_raw_buffer_load_b128(r, b, 0, 0);
+    if constexpr (E == 4) d[1] = __builtin_amdgcn_raw_buffer_load_b128(r, b + (b == kOob ? 0u : 16u), 0, 0);
+  } else if constexpr (E == 4) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      d[e >> 2][e & 3] = __builtin_amdgcn_raw_buffer_load_b32(r, (ok && e < nv) ? (off + e) * 4u : kOob, 0, 0);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(r, (ok && 2 * e < nv) ? (off + 2 * e) * 2u : kOob, 0, 0);
+      const uint32_t hi =
+          __builtin_amdgcn_raw_buffer_load_b16(r, (ok && 2 * e + 1 < nv) ? (off + 2 * e + 1) * 2u : kOob, 0, 0);
+      d[0][e] = (lo & 0xffffu) | (hi << 16);
+    }
+  }
+}
+
+// yb: y itself (2-byte types) or its bf16 hi / lo planes [N][2][C][HW] (fp32).
+template <typename T, int RB, int CB, bool VEC>
+__global__ __launch_bounds__(64 * kGwWaves) void gk_bwd_w_kernel(const T* __restrict__ gk,
+                                                                const uint16_t* __restrict__ yb,
+                                                                float* __restrict__ pw,
+                                                                float* __restrict__ pb,
+                                                                T* __restrict__ dw, T* __restrict__ db,
+                                                                GwGeom g) {
+  typedef Mma<T> M;
+  typedef typename M::V V;
+  constexpr int P = M::P;
+  constexpr int AD = sizeof(T) == 4 ? 2 : 1;  // 16-byte dwords of a lane's 8 dK values
+  constexpr uint32_t E = sizeof(T);
+  constexpr int RS = CB * 16 + 1;
+  // 32-pixel steps per load batch: 16 (2-byte) or 8 (fp32) 16-byte loads of dK
+  // per wave, plus the y loads
+  constexpr int KC = 1;
+  __shared__ float red[RB * 16 * RS];
+  __shared__ float redb[RB * 16];
+
+  const int rt = blockIdx.x % g.row_tiles;
+  const int split = blockIdx.x / g.row_tiles;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int col16 = lane & 15, quad = lane >> 4;
+  const int C = g.C, HW = g.HW, O = g.O;
+  const int o0 = rt * 16 * RB;
+  const int s_beg = split * g.steps_per_split;
+  const int s_end = s_beg + g.steps_per_split < g.steps ? s_beg + g.steps_per_split : g.steps;
+
+  f32x4 acc[RB][CB];
+  float accb[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    accb[rb] = 0.f;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // this lane's rows o and channels i (element offsets of their rows)
+  uint32_t arow[RB], brow[CB][P];
+  bool aok[RB], bok[CB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int o = o0 + 16 * rb + col16;
+    aok[rb] = o < O;
+    arow[rb] = (uint32_t)o * (uint32_t)HW;
+  }
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    const int i = 16 * cb + col16;
+    bok[cb] = i < C;
+#pragma unroll
+    for (int pp = 0; pp < P; ++pp) brow[cb][pp] = (uint32_t)(pp * C + i) * (uint32_t)HW;
+  }
+
+  for (int u0 = s_beg + wave * KC; u0 < s_end; u0 += kGwWaves * KC) {
+    u32x4 ac[KC][RB][AD], bc[KC][CB][P];
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      const int u = u0 + k;
+      const int n = u / g.spi;
+      const int px = (u - n * g.spi) * kGwStep + 8 * quad;
+      const int nv = u < s_end ? HW - px : 0;  // steps past the split read zero
+      const BufRes ar = make_buf(gk + (int64_t)n * O * HW, (uint32_t)O * (uint32_t)HW * E);
+      const BufRes br = make_buf(yb + (int64_t)n * P * C * HW, (uint32_t)(P * C) * (uint32_t)HW * 2u);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) gw_load_row8<T, VEC>(ar, arow[rb] + (uint32_t)px, aok[rb], nv, ac[k][rb]);
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp) {
+          u32x4 t[1];
+          gw_load_row8<uint16_t, VEC>(br, brow[cb][pp] + (uint32_t)px, bok[cb], nv, t);
+          bc[k][cb][pp] = t[0];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      V bf[CB][P];
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp) bf[cb][pp] = __builtin_bit_cast(V, bc[k][cb][pp]);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        V af[P];
+        float sum = 0.f;
+        if constexpr (E == 4) {
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = __uint_as_float(ac[k][rb][e >> 2][e & 3]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sum += v[e];
+          M::pack(v, af);
+        } else {
+          typedef T T8 __attribute__((ext_vector_type(8)));
+          const T8 t = __builtin_bit_cast(T8, ac[k][rb][0]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sum += to_f(t[e]);
+          af[0] = __builtin_bit_cast(V, ac[k][rb][0]);
+        }
+        accb[rb] += sum;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = M::mac(af, bf[cb], acc[rb][cb]);
+      }
+    }
+  }
+
+  // db: the four lanes of a row (quads) hold partial sums of its pixels
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    accb[rb] += __shfl_xor(accb[rb], 16);
+    accb[rb] += __shfl_xor(accb[rb], 32);
+  }
+  // fixed-order sum over the waves: D row 4*quad + r of block rb is row
+  // o0 + 16*rb + 4*quad + r, column col16 of block cb is channel 16*cb + col16
+  for (int w = 0; w < kGwWaves; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float* dst = red + (16 * rb + 4 * quad + r) * RS + 16 * cb + col16;
+            *dst = (w == 0 ? 0.f : *dst) + acc[rb][cb][r];
+          }
+        if (quad == 0) {
+          float* dst = redb + 16 * rb + col16;
+          *dst = (w == 0 ? 0.f : *dst) + accb[rb];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  const bool direct = g.splits == 1;
+  for (int idx = tid; idx < RB * 16 * C; idx += 64 * kGwWaves) {
+    const int row = idx / C, i = idx - row * C;
+    const int o = o0 + row;
+    if (o >= O) break;
+    const float v = red[row * RS + i];
+    if (direct)
+      dw[(int64_t)o * C + i] = from_f<T>(v);
+    else
+      pw[((int64_t)split * O + o) * C + i] = v;
+  }
+  for (int row = tid; row < RB * 16; row += 64 * kGwWaves) {
+    const int o = o0 + row;
+    if (o >= O) break;
+    if (direct)
+      db[o] = from_f<T>(redb[row]);
+    else
+      pb[(int64_t)split * O + o] = redb[row];
+  }
+}
+
+template <typename T, int CB>
+__global__ __launch_bounds__(64 * kGwWaves) void gk_bwd_w_lds_kernel(const T* __restrict__ gk,
+                                                                    const uint16_t* __restrict__ yb,
+                                                                    float* __restrict__ pw,
+                                                                    float* __restrict__ pb,
+                                                                    T* __restrict__ dw,
+                                                                    T* __restrict__ db, GwGeom g) {
+  typedef GwLds<T, CB> L;
+  typedef Mma<T> M;
+  typedef typename M::V V;
+  constexpr int P = M::P;
+  constexpr uint32_t E = sizeof(T);
+  constexpr int NAW = L::NA / kGwWaves, NYW = L::NY / kGwWaves;  // copies per wave
+  extern __shared__ __attribute__((aligned(16))) uint32_t gsm[];
+
+  const int rt = blockIdx.x % g.row_tiles;
+  const int split = blockIdx.x / g.row_tiles;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int col16 = lane & 15, quad = lane >> 4;
+  const int C = g.C, HW = g.HW, O = g.O;
+  const int o0 = rt * 64;
+  const int s_beg = split * g.steps_per_split;
+  const int s_end = s_beg + g.steps_per_split < g.steps ? s_beg + g.steps_per_split : g.steps;
+
+  // this lane's chunks of the copies: element offset in the image's planes
+  // at pixel 0 and the chunk's first pixel (absent rows / channels: !ok)
+  uint32_t aoff[NAW], yoff[NYW];
+  int apx[NAW], ypx[NYW];
+  bool aok[NAW], yok[NYW];
+#pragma unroll
+  for (int j = 0; j < NAW; ++j) {
+    const int lc = (wave * NAW + j) * 64 + lane;
+    const int row = lc / L::ACH, pos = lc % L::ACH;
+    const int gc = pos ^ (row & (L::ACH - 1));
+    apx[j] = gc * L::CPX;
+    aok[j] = o0 + row < O;
+    aoff[j] = (uint32_t)(o0 + row) * (uint32_t)HW + (uint32_t)apx[j];
+  }
+#pragma unroll
+  for (int j = 0; j < NYW; ++j) {
+    const int lc = (wave * NYW + j) * 64 + lane;
+    const int r = lc / L::YC, pos = lc % L::YC;
+    const int gc = pos ^ (r & (L::YC - 1));
+    const int pp = r / (CB * 16), i = r - pp * (CB * 16);
+    ypx[j] = gc * 8;
+    yok[j] = i < C;
+    yoff[j] = (uint32_t)(pp * C + i) * (uint32_t)HW + (uint32_t)ypx[j];
+  }
+  auto stage = [&](int u, int buf) {
+    const int n = u / g.spi;
+    const int px0 = (u - n * g.spi) * L::SP;
+    const BufRes ar = make_buf(gk + (int64_t)n * O * HW, (uint32_t)O * (uint32_t)HW * E);
+    const BufRes yr = make_buf(yb + (int64_t)n * P * C * HW, (uint32_t)(P * C) * (uint32_t)HW * 2u);
+    char* dst = reinterpret_cast<char*>(gsm) + buf * L::BUF;
+#pragma unroll
+    for (int j = 0; j < NAW; ++j) {
+      const uint32_t off = (aok[j] && px0 + apx[j] < HW) ? (aoff[j] + (uint32_t)px0) * E : kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ar, (__attribute__((address_space(3))) void*)(dst + (wave * NAW + j) * 1024), 16, off, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < NYW; ++j) {
+      const uint32_t off = (yok[j] && px0 + ypx[j] < HW) ? (yoff[j] + (uint32_t)px0) * 2u : kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          yr, (__attribute__((address_space(3))) void*)(dst + L::ABYTES + (wave * NYW + j) * 1024), 16,
+          off, 0, 0, 0);
+    }
+  };
+
+  f32x4 acc[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float accb = 0.f;
+  const int arow = 16 * wave + col16;  // this lane's A row in the tile
+  const int nst = s_end > s_beg ? s_end - s_beg : 0;
+  if (nst > 0) stage(s_beg, 0);
+  for (int it = 0; it < nst; ++it) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // buffer it & 1 is whole; buffer (it + 1) & 1 is no longer read
+    if (it + 1 < nst) stage(s_beg + it + 1, (it + 1) & 1);
+    const char* bb = reinterpret_cast<const char*>(gsm) + (it & 1) * L::BUF;
+    const char* ab = bb + arow * (L::ACH * 16);
+#pragma unroll
+    for (int kc = 0; kc < L::KC; ++kc) {
+      V af[P];
+      float sum = 0.f;
+      if constexpr (E == 4) {
+        const int c0 = 8 * kc + 2 * quad;
+        const u32x4 a0 = *reinterpret_cast<const u32x4*>(ab + 16 * (c0 ^ (arow & (L::ACH - 1))));
+        const u32x4 a1 = *reinterpret_cast<const u32x4*>(ab + 16 * ((c0 + 1) ^ (arow & (L::ACH - 1))));
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = __uint_as_float(a0[e]);
+          v[4 + e] = __uint_as_float(a1[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += v[e];
+        M::pack(v, af);
+      } else {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(ab + 16 * ((4 * kc + quad) ^ (arow & (L::ACH - 1))));
+        typedef T T8 __attribute__((ext_vector_type(8)));
+        const T8 t = __builtin_bit_cast(T8, a);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += to_f(t[e]);
+        af[0] = __builtin_bit_cast(V, a);
+      }
+      accb += sum;
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        V bf[P];
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp) {
+          const int r = pp * CB * 16 + 16 * cb + col16;
+          bf[pp] = __builtin_bit_cast(
+              V, *reinterpret_cast<const u32x4*>(bb + L::ABYTES + r * (L::YC * 16) +
+                                                  16 * ((4 * kc + quad) ^ (r & (L::YC - 1)))));
+        }
+        acc[cb] = M::mac(af, bf, acc[cb]);
+      }
+    }
+  }
+
+  // db: the four lanes of a row (quads) hold partial sums of its pixels
+  accb += __shfl_xor(accb, 16);
+  accb += __shfl_xor(accb, 32);
+  // D row 4*quad + r of the wave's block is row o0 + 16*wave + 4*quad + r,
+  // column col16 of block cb is channel 16*cb + col16
+  const bool direct = g.splits == 1;
+  const int ob = o0 + 16 * wave;
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    const int i = 16 * cb + col16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int o = ob + 4 * quad + r;
+      if (o < O && i < C) {
+        if (direct)
+          dw[(int64_t)o * C + i] = from_f<T>(acc[cb][r]);
+        else
+          pw[((int64_t)split * O + o) * C + i] = acc[cb][r];
+      }
+    }
+  }
+  if (quad == 0 && ob + col16 < O) {
+    if (direct)
+      db[ob + col16] = from_f<T>(accb);
+    else
+      pb[(int64_t)split * O + ob + col16] = accb;
+  }
+}
+
+// Sum of the split partials in split order (also the zero gradients of an
+// empty batch: splits = 0).
+template <typename T>
+__global__ __launch_bounds__(256) void gk_bwd_w_reduce_kernel(const float* __restrict__ pw,
+                                                              const float* __restrict__ pb,
+                                                              T* __restrict__ dw, T* __restrict__ db,
+                                                              int64_t OC, int O, int splits) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx < OC) {
+    float v = 0.f;
+    for (int sp = 0; sp < splits; ++sp) v += pw[sp * OC + idx];
+    dw[idx] = from_f<T>(v);
+  } else if (idx < OC + O) {
+    const int64_t j = idx - OC;
+    float v = 0.f;
+    for (int sp = 0; sp < splits; ++sp) v += pb[sp * O + j];
+    db[j] = from_f<T>(v);
+  }
+}
+
 namespace {
 
 template <typename F>
@@ -204,6 +630,51 @@ int gk_with_type(int dt, F&& f) {
     default:
       return kBadArgument;
   }
+}
+
+}  // namespace
+
+namespace {
+
+// Row blocks per wave of the element-wise kernel by channel blocks
+// (accumulators RB x CB <= 16 tiles)
+int gw_cb(int64_t c) { return c <= 16 ? 1 : c <= 32 ? 2 : c <= 64 ? 4 : 8; }
+int gw_rb(int cb) { return cb == 8 ? 2 : 4; }
+
+// Splits of the pixel steps: as many as fill kGwSlots workgroups over the
+// row tiles, with at least `min_steps` steps per workgroup.
+void gw_geom(GwGeom& g, int64_t n, int64_t c, int64_t hw, int64_t o, int sp, int rows, int min_steps) {
+  g.N = (int)n;
+  g.C = (int)c;
+  g.HW = (int)hw;
+  g.O = (int)o;
+  g.sp = sp;
+  g.spi = (int)((hw + sp - 1) / sp);
+  g.steps = (int)(n * g.spi);
+  g.rows = rows;
+  g.row_tiles = (int)((o + rows - 1) / rows);
+  int64_t splits = kGwSlots / g.row_tiles;
+  const int64_t most = ((int64_t)g.steps + min_steps - 1) / min_steps;
+  if (splits > most) splits = most;
+  if (splits < 1) splits = 1;
+  g.steps_per_split = (int)((g.steps + splits - 1) / splits);
+  g.splits = g.steps == 0 ? 0 : (g.steps + g.steps_per_split - 1) / g.steps_per_split;
+}
+
+// LDS-staged kernel: 64 rows per workgroup, at least 8 steps per workgroup
+void gw_geom_lds(GwGeom& g, int64_t n, int64_t c, int64_t hw, int64_t o, int sp) {
+  gw_geom(g, n, c, hw, o, sp, 64, 8);
+}
+// element-wise kernel: 32-pixel steps, at least 8 per wave
+void gw_geom_elem(GwGeom& g, int64_t n, int64_t c, int64_t hw, int64_t o) {
+  gw_geom(g, n, c, hw, o, kGwStep, 16 * gw_rb(gw_cb(c)), 8 * kGwWaves);
+}
+
+int64_t gw_align(int64_t v) { return (v + 255) / 256 * 256; }
+
+int64_t gw_partial_bytes(const GwGeom& g) {
+  if (g.splits <= 1) return 0;
+  return (int64_t)g.splits * ((int64_t)g.O * g.C + g.O) * (int64_t)sizeof(float);
 }
 
 }  // namespace
@@ -258,6 +729,114 @@ extern "C" int ddpm_gen_kernels(const void* y, const void* weight, const void* b
         return launch(gen_kernels_kernel<T, 3>);
       default:
         return launch(gen_kernels_kernel<T, 4>);
+    }
+  });
+}
+
+
+extern "C" int64_t ddpm_gen_kernels_bwd_w_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w,
+                                                          int kernel_size) {
+  if (n <= 0 || c <= 0 || h <= 0 || w <= 0 || kernel_size < 1 || kernel_size % 2 == 0) return 0;
+  if (c > kGkMaxC || n * ((h * w + kGwStep - 1) / kGwStep) > 0x7fffffffLL) return 0;
+  const int64_t hw = h * w, o = 3 * c * kernel_size * kernel_size;
+  // the query takes no dtype or alignment: it covers the largest partials of
+  // either kernel and fp32, whose y planes come on top
+  GwGeom g;
+  int64_t most = 0;
+  const int sp1 = gw_cb(c) <= 4 ? 64 : 32;  // fp32 steps; 2-byte steps are twice as long
+  for (int sp : {sp1, 2 * sp1}) {
+    gw_geom_lds(g, n, c, hw, o, sp);
+    most = std::max(most, gw_partial_bytes(g));
+  }
+  gw_geom_elem(g, n, c, hw, o);
+  most = std::max(most, gw_partial_bytes(g));
+  return gw_align(most) + n * 2 * c * hw * 2;
+}
+
+extern "C" int ddpm_gen_kernels_bwd_w(const void* y, const void* grad_kernels, void* grad_weight,
+                                      void* grad_bias, void* workspace, int64_t workspace_bytes,
+                                      int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size,
+                                      int dtype, hipStream_t stream) {
+  if (dtype < kF32 || dtype > kF16) return kBadArgument;
+  if (n < 0 || c < 0 || h < 0 || w < 0) return kBadArgument;
+  if (kernel_size < 1 || kernel_size % 2 == 0) return kBadArgument;
+  if (c > kGkMaxC) return kUnsupported;
+  if (c == 0) return kOk;
+  if (!grad_weight || !grad_bias) return kBadArgument;
+  const int64_t esz = dtype == kF32 ? 4 : 2;
+  const int64_t hw = h * w, o = 3 * c * kernel_size * kernel_size;
+  if (n > 0 && hw > 0 && (!y || !grad_kernels)) return kBadArgument;
+  // 32-bit buffer offsets inside one image's planes (fp32 y: two 2-byte planes)
+  if (o * hw * esz > 0x7fffffffLL || 2 * c * hw * 2 > 0x7fffffffLL) return kUnsupported;
+  if (n * ((hw + kGwStep - 1) / kGwStep) > 0x7fffffffLL || o * c > 0x7fffffffLL) return kUnsupported;
+  const int cb = gw_cb(c);
+  // LDS-staged kernel: 16-byte chunks of every plane row (the fp32 y planes
+  // sit 256-byte aligned in the workspace)
+  const bool lds = hw % 8 == 0 && (uintptr_t)grad_kernels % 16 == 0 &&
+                   (dtype == kF32 ? (uintptr_t)workspace % 16 == 0 : (uintptr_t)y % 16 == 0);
+  GwGeom g;
+  if (lds)
+    gw_geom_lds(g, n, c, hw, o, (cb <= 4 ? 64 : 32) * (int)(4 / esz));
+  else
+    gw_geom_elem(g, n, c, hw, o);
+  const int64_t pbytes = gw_partial_bytes(g);
+  const int64_t need = dtype == kF32 && g.steps > 0 ? gw_align(pbytes) + n * 2 * c * hw * 2 : pbytes;
+  if (need > 0 && (!workspace || workspace_bytes < need)) return kWorkspaceTooSmall;
+  float* pw = (float*)workspace;
+  float* pb = pw ? pw + (int64_t)g.splits * o * c : nullptr;
+  const uint16_t* yb = (const uint16_t*)y;
+  if (dtype == kF32 && g.steps > 0) {
+    uint16_t* ys = (uint16_t*)((char*)workspace + gw_align(pbytes));
+    const int e = launch_ysplit((const float*)y, ys, c * hw, n * c * hw, stream);
+    if (e != 0) return e;
+    yb = ys;
+  }
+  return gk_with_type(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    auto launch = [&](auto kern, size_t shm) {
+      if (g.splits > 0) {
+        if (shm > 64 * 1024) {
+          const hipError_t ae = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+          if (ae != hipSuccess) return (int)ae;
+        }
+        hipLaunchKernelGGL(kern, dim3((unsigned)(g.row_tiles * g.splits)), dim3(64 * kGwWaves), shm,
+                           stream, (const T*)grad_kernels, yb, pw, pb, (T*)grad_weight,
+                           (T*)grad_bias, g);
+        const int e = (int)hipGetLastError();
+        if (e != 0 || g.splits == 1) return e;
+      }
+      const int64_t total = o * c + o;
+      hipLaunchKernelGGL((gk_bwd_w_reduce_kernel<T>), dim3((unsigned)((total + 255) / 256)),
+                         dim3(256), 0, stream, (const float*)pw, (const float*)pb, (T*)grad_weight,
+                         (T*)grad_bias, o * c, (int)o, g.splits);
+      return (int)hipGetLastError();
+    };
+    auto lds_launch = [&](auto cbc) {
+      constexpr int CB = decltype(cbc)::value;
+      return launch(gk_bwd_w_lds_kernel<T, CB>, (size_t)2 * GwLds<T, CB>::BUF);
+    };
+    if (lds) {
+      switch (cb) {
+        case 1:
+          return lds_launch(std::integral_constant<int, 1>());
+        case 2:
+          return lds_launch(std::integral_constant<int, 2>());
+        case 4:
+          return lds_launch(std::integral_constant<int, 4>());
+        default:
+          return lds_launch(std::integral_constant<int, 8>());
+      }
+    }
+    switch (cb) {
+      case 1:
+        return launch(gk_bwd_w_kernel<T, 4, 1, false>, 0);
+      case 2:
+        return launch(gk_bwd_w_kernel<T, 4, 2, false>, 0);
+      case 4:
+        return launch(gk_bwd_w_kernel<T, 4, 4, false>, 0);
+      default:
+        return launch(gk_bwd_w_kernel<T, 2, 8, false>, 0);
     }
   });
 }

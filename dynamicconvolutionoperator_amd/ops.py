@@ -257,8 +257,9 @@ class _GeneratorKernels(torch.autograd.Function):
     """``kernels = conv2d(y, weight, bias)`` for the 1x1 generator, as
     ``[N, 3CK², H, W]`` in y's dtype (the reference's ``self.generator(y)``,
     triton_impl.py:340-347).  Forward: one HIP MFMA kernel with the bias and
-    the output rounding fused.  Backward: the Conv2d gradients as batched
-    products -- dY = Wᵀ·dK, dW = Σ_n dK·yᵀ, db = Σ dK."""
+    the output rounding fused.  Backward: dW and db in one HIP kernel that
+    reads dK once (``ddpm_gen_kernels_bwd_w``), dY = Wᵀ·dK as a batched
+    product."""
 
     @staticmethod
     def forward(ctx, y, weight, bias, kernel_size):
@@ -282,6 +283,7 @@ class _GeneratorKernels(torch.autograd.Function):
         _lib.check(code, "ddpm_gen_kernels")
         ctx.save_for_backward(y, w2)
         ctx.weight_shape = tuple(weight.shape)
+        ctx.kernel_size = k
         return out
 
     @staticmethod
@@ -293,12 +295,21 @@ class _GeneratorKernels(torch.autograd.Function):
         grad_y = grad_w = grad_b = None
         if ctx.needs_input_grad[0]:
             grad_y = torch.matmul(w2.t().contiguous(), g).view(n, c, h, w)
-        if ctx.needs_input_grad[1]:
-            gw = torch.matmul(g, y.view(n, c, h * w).transpose(1, 2).contiguous())
-            gw = gw[0] if n == 1 else gw.float().sum(0).to(y.dtype)
-            grad_w = gw.reshape(ctx.weight_shape)
-        if ctx.needs_input_grad[2]:
-            grad_b = g.sum(dim=(0, 2))
+        if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
+            k = ctx.kernel_size
+            lib = _lib.load()
+            gw = torch.empty((o, c), dtype=y.dtype, device=y.device)
+            gb = torch.empty((o,), dtype=y.dtype, device=y.device)
+            with torch.cuda.device(y.device):
+                ws_bytes = int(lib.ddpm_gen_kernels_bwd_w_workspace_bytes(n, c, h, w, k))
+                ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=y.device)
+                code = lib.ddpm_gen_kernels_bwd_w(_ptr(y), _ptr(g), _ptr(gw), _ptr(gb), _ptr(ws),
+                                                  ws_bytes, n, c, h, w, k, _dt(y), _stream(y))
+            _lib.check(code, "ddpm_gen_kernels_bwd_w")
+            if ctx.needs_input_grad[1]:
+                grad_w = gw.reshape(ctx.weight_shape)
+            if ctx.needs_input_grad[2]:
+                grad_b = gb
         return grad_y, grad_w, grad_b, None
 
 

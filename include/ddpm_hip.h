@@ -62,6 +62,21 @@ int ddpm_gen_supported(int64_t c, int kernel_size, int max_dilation);
 int ddpm_gen_kernels(const void* y, const void* weight, const void* bias, void* kernels, int64_t n,
                      int64_t c, int64_t h, int64_t w, int kernel_size, int dtype, hipStream_t stream);
 
+/* Weight and bias gradients of that convolution:
+ * grad_weight[o][i] = sum_{n,p} grad_kernels[n][o][p] * y[n][i][p] and
+ * grad_bias[o] = sum_{n,p} grad_kernels[n][o][p], accumulated in fp32 and
+ * rounded once to `dtype` (deterministic: fixed-order split partials).
+ * grad_kernels: [n][3*c*k*k][h][w]; grad_weight: [3*c*k*k][c]; an empty
+ * batch writes zeros.  c <= 128.  Replaces the backward-filter convolution
+ * of self.generator on the reference's materialized path
+ * (triton_impl.py:340-347, autograd of nn.Conv2d). */
+int64_t ddpm_gen_kernels_bwd_w_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w,
+                                               int kernel_size);
+int ddpm_gen_kernels_bwd_w(const void* y, const void* grad_kernels, void* grad_weight,
+                           void* grad_bias, void* workspace, int64_t workspace_bytes, int64_t n,
+                           int64_t c, int64_t h, int64_t w, int kernel_size, int dtype,
+                           hipStream_t stream);
+
 /* ---- materialized dynamic filter ------------------------------------- */
 
 /* out = [x, d0, d1, d2] from materialized kernels; out has k_dtype, and the

@@ -173,6 +173,12 @@ def test_generator_dilation_sets(K, dil, fused, shape, dtype):
         ((1, 20, 16, 16), 3),  # C % 8 != 0: element-wise weight loads
         ((1, 64, 32, 32), 5),  # the K = 5 configuration's channel count
         ((1, 128, 8, 12), 1),  # the largest C, four 32-channel K steps
+        # weight / bias gradients summed over split partials (one workgroup
+        # per 64 rows and pixel range, partials reduced in split order):
+        ((2, 64, 48, 64), 5),  # 6 splits of pixel steps spanning both images
+        ((3, 8, 40, 40), 5),   # C = 8: one channel block, 5 (2-byte) / 10 (fp32) splits
+        ((2, 24, 45, 37), 3),  # odd H*W: element-wise operand loads, 4 splits
+        ((1, 128, 32, 64), 3),  # C = 128: 64-pixel steps, 4 splits
     ],
 )
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
@@ -196,6 +202,27 @@ def test_generator_kernels_match_oracle(shape, K, dtype):
     for name, a, ex in (("dy", yd.grad, dy), ("dw", wd.grad, dw), ("db", bd.grad, db)):
         scale = max(1.0, ex.abs().max().item())
         assert_close(a, ex, atol * scale, rtol, f"generator kernels {name}")
+
+
+def test_generator_kernels_weight_gradient_deterministic_and_empty():
+    """Split partials are summed in a fixed order: two backward passes agree
+    bit for bit.  An empty batch gives zero weight / bias gradients."""
+    c, K = 64, 5
+    say("generator kernels weight gradient determinism")
+    wt, b = default_generator_params(c, K, 74, torch.float32)
+    y = randn((2, c, 48, 64), 75).to(DEV)
+    g = randn((2, 3 * c * K * K, 48, 64), 76).to(DEV)
+    grads = []
+    for _ in range(2):
+        wd, bd = (t.to(DEV).requires_grad_() for t in (wt, b))
+        ops.generator_kernels(y, wd, bd, K).backward(g)
+        grads.append((wd.grad.clone(), bd.grad.clone()))
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+    say("generator kernels empty batch")
+    wd, bd = (t.to(DEV).requires_grad_() for t in (wt, b))
+    y0 = torch.zeros((0, c, 8, 8), device=DEV, requires_grad=True)
+    ops.generator_kernels(y0, wd, bd, K).sum().backward()
+    assert torch.count_nonzero(wd.grad) == 0 and torch.count_nonzero(bd.grad) == 0
 
 
 def test_generator_inference_has_no_autograd_graph():

@@ -57,6 +57,17 @@ def test_host_only_queries():
     # ... and 16x32 tiles when the R = 8 accumulator tile does not fit the LDS
     assert lib.ddpm_gen_bwd_x_workspace_bytes(1, 64, 256, 256, 3, 1, 3, 8) == 128 * 4 * 16 * 32 * 48 * 4
     assert lib.ddpm_gen_bwd_x_workspace_bytes(1, 64, 256, 256, 5, 1, 3, 5) == 0  # unsupported
+    # generator convolution weight gradient at 128x128, C = 64, K = 5: 4800 rows in
+    # 75 tiles of 64, 6 splits (450 workgroups for 512 slots) of (4800 x 64 + 4800)
+    # fp32 partials, then the bf16 hi / lo planes of an fp32 y
+    assert lib.ddpm_gen_kernels_bwd_w_workspace_bytes(1, 64, 128, 128, 5) == (
+        6 * (4800 * 64 + 4800) * 4 + ysplit(1, 64, 128, 128))
+    # 32x32: 16 steps of 64 pixels at 8 per workgroup give the most partials (2 splits)
+    assert lib.ddpm_gen_kernels_bwd_w_workspace_bytes(1, 64, 32, 32, 5) == (
+        2 * (4800 * 64 + 4800) * 4 + ysplit(1, 64, 32, 32))
+    # 8 steps of 32 pixels (4x64) or fewer: one split, no partials
+    assert lib.ddpm_gen_kernels_bwd_w_workspace_bytes(1, 64, 4, 64, 5) == ysplit(1, 64, 4, 64)
+    assert lib.ddpm_gen_kernels_bwd_w_workspace_bytes(1, 129, 32, 32, 5) == 0  # unsupported
 
 
 def test_entry_points_validate_arguments_before_touching_the_device():
@@ -72,6 +83,10 @@ def test_entry_points_validate_arguments_before_touching_the_device():
     assert lib.ddpm_gen_kernels(null, null, null, null, 1, 64, 8, 8, 4, 1, null) == 10001
     assert lib.ddpm_gen_kernels(null, null, null, null, 1, 129, 8, 8, 5, 1, null) == 10002
     assert lib.ddpm_gen_kernels(null, null, null, null, 1, 64, 8, 8, 5, 1, null) == 10001
+    # its weight gradient: even kernel size, more than 128 channels, null outputs
+    assert lib.ddpm_gen_kernels_bwd_w(null, null, null, null, null, 0, 1, 64, 8, 8, 4, 1, null) == 10001
+    assert lib.ddpm_gen_kernels_bwd_w(null, null, null, null, null, 0, 1, 129, 8, 8, 5, 1, null) == 10002
+    assert lib.ddpm_gen_kernels_bwd_w(null, null, null, null, null, 0, 1, 64, 8, 8, 5, 1, null) == 10001
     # empty tensors are a no-op
     assert lib.ddpm_filter_fwd(null, null, null, 0, 4, 4, 4, 3, 1, 3, 5, 0, 0, null) == 0
     assert lib.ddpm_gen_kernels(null, null, null, null, 0, 64, 8, 8, 5, 1, null) == 0
