@@ -13,8 +13,11 @@
 //     staged; the LDS tile is stored phase-split (column j at phase j % V,
 //     index j / V) so each of a lane's V shifted reads is bank-conflict free;
 //   * dX is a gather (kernel planes read at the shifted source pixels): a lane
-//     owns one pixel in each of U column blocks of 64, so every load of a
-//     kernel plane is 64 consecutive elements;
+//     owns 16 bytes of consecutive pixels and loads the two aligned 16-byte
+//     chunks around each tap's shifted window (realigned in registers by a
+//     wave-uniform shift) where the staged tiles fit two workgroups per CU;
+//     otherwise one pixel in each of U column blocks of 64, so every load of
+//     a kernel plane is 64 consecutive elements;
 //   * FP32 accumulation; outputs written once, no Unfold buffers.
 
 #include "ddpm_common.h"
@@ -366,6 +369,148 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_kernel(const TK* 
   }
 }
 
+// Elements s .. s+V-1 of the 2V consecutive kernel-plane elements held in
+// two aligned 16-byte chunks (c0 first), as fp32.  s is wave-uniform (it
+// depends only on the tap's column shift), so the dword selection is a
+// uniform branch and the odd 2-byte shift one v_alignbyte per dword.
+template <typename TK, int V>
+__device__ __forceinline__ void realign(const u32x4& c0, const u32x4& c1, int s, float (&out)[V]) {
+  const uint32_t D[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+  uint32_t e[5];
+  const int k = sizeof(TK) == 4 ? s : s >> 1;  // first dword
+  switch (k) {
+    case 0:
+#pragma unroll
+      for (int j = 0; j < 5; ++j) e[j] = D[j];
+      break;
+    case 1:
+#pragma unroll
+      for (int j = 0; j < 5; ++j) e[j] = D[j + 1];
+      break;
+    case 2:
+#pragma unroll
+      for (int j = 0; j < 5; ++j) e[j] = D[j + 2];
+      break;
+    default:
+#pragma unroll
+      for (int j = 0; j < 5; ++j) e[j] = D[j + 3];
+      break;
+  }
+  if constexpr (sizeof(TK) == 4) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) out[v] = __uint_as_float(e[v]);
+  } else {
+    const uint32_t sh = (uint32_t)(s & 1) * 2u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t w = __builtin_amdgcn_alignbyte(e[j + 1], e[j], sh);
+      typedef TK T2 __attribute__((ext_vector_type(2)));
+      const T2 t = __builtin_bit_cast(T2, w);
+      out[2 * j] = to_f(t[0]);
+      out[2 * j + 1] = to_f(t[1]);
+    }
+  }
+}
+
+// dX gather with V consecutive pixels per lane (16 bytes of kernel plane;
+// W % V == 0): the branch-gradient tiles are staged phase-split as in the
+// forward, and each tap's kernel values at the lane's shifted window come
+// from the two aligned 16-byte chunks around it -- two loads per V pixels
+// instead of V, every access aligned.  The K taps of a kernel row are
+// requested together, one row ahead of the FMAs.
+template <typename TX, typename TK, int KS, int V>
+__global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_vec_kernel(const TK* __restrict__ gout,
+                                                                            const TK* __restrict__ kern,
+                                                                            TX* __restrict__ gx,
+                                                                            FilterGeom g) {
+  static_assert(KS >= 1 && V * sizeof(TK) == 16, "16-byte kernel chunks, fixed K");
+  constexpr int KK = KS * KS, r = KS / 2;
+  constexpr uint32_t E = sizeof(TK);
+  extern __shared__ float gs[];
+  const int bid = blockIdx.x;
+  const int plane = bid / g.tiles;
+  const int tile = bid - plane * g.tiles;
+  const int n = plane / g.C, c = plane - n * g.C;
+  const int ty = tile / g.tiles_w, tx = tile - ty * g.tiles_w;
+  const int h0 = ty * g.TH, w0 = tx * g.TW;
+  const int64_t HW = (int64_t)g.H * g.W;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int lpr = 1 << g.lpr_log2;
+  const int trow = wave * (64 >> g.lpr_log2) + (lane >> g.lpr_log2);
+  const int cl = lane & (lpr - 1);
+  const int gh = h0 + trow, gw = w0 + V * cl;
+  const bool active = gh < g.H && gw < g.W && trow < g.TH;
+  const TK* __restrict__ gp = gout + ((int64_t)n * 4 * g.C + c) * HW;
+  const int64_t gstride = (int64_t)g.C * HW;
+  const int lplane = g.LH * g.RS;
+
+  // the K*K tap planes of branch b for this (n, c): one resource per branch
+  BufRes kres[3];
+#pragma unroll
+  for (int b = 0; b < 3; ++b)
+    kres[b] = make_buf(kern + (((int64_t)n * 3 + b) * g.C + c) * KK * HW, (uint32_t)(KK * HW * E));
+  // chunks of kernel row (b, ki): [tap kj][2]
+  auto load_row = [&](int b, int ki, u32x4 (&ch)[KS][2]) {
+    const int d = dil_of(b, g.d0, g.d1, g.d2);
+    const BufRes kr = b == 0 ? kres[0] : (b == 1 ? kres[1] : kres[2]);
+    const int sh = gh - (ki - r) * d;  // source row
+    const bool rok = active && (unsigned)sh < (unsigned)g.H;
+#pragma unroll
+    for (int kj = 0; kj < KS; ++kj) {
+      const int dw = (kj - r) * d;
+      const int s = ((-dw) % V + V) % V;
+      const int a0 = gw - dw - s;  // aligned start of the lane's window
+      const uint32_t base = (uint32_t)((ki * KS + kj) * HW + (int64_t)sh * g.W);
+      const bool ok0 = rok && a0 >= 0 && a0 < g.W;
+      const bool ok1 = rok && a0 + V < g.W && a0 + V >= 0;
+      ch[kj][0] = __builtin_amdgcn_raw_buffer_load_b128(kr, ok0 ? (base + (uint32_t)a0) * E : kOob, 0, 0);
+      ch[kj][1] = s == 0 ? u32x4{0u, 0u, 0u, 0u}
+                         : __builtin_amdgcn_raw_buffer_load_b128(
+                               kr, ok1 ? (base + (uint32_t)(a0 + V)) * E : kOob, 0, 0);
+    }
+  };
+
+  u32x4 nxt[KS][2];
+  load_row(0, 0, nxt);
+#pragma unroll
+  for (int b = 0; b < 3; ++b) stage_plane<TK, V>(gs + b * lplane, gp + (b + 1) * gstride, g, h0, w0);
+  __syncthreads();
+  if (!active) return;  // no barrier below
+
+  float acc[V];
+  {
+    const int64_t pix = (int64_t)gh * g.W + gw;
+    VecIO<TK, V>::load(gp + pix, acc);
+  }
+  const int jc = g.CP + V * cl;  // staged column of this lane's first pixel
+  // a runtime loop: unrolled, the compiler would hoist every row's loads
+#pragma unroll 1
+  for (int it = 0; it < 3 * KS; ++it) {
+    const int b = it / KS, ki = it - b * KS;
+    u32x4 cur[KS][2];
+#pragma unroll
+    for (int kj = 0; kj < KS; ++kj) {
+      cur[kj][0] = nxt[kj][0];
+      cur[kj][1] = nxt[kj][1];
+    }
+    if (it + 1 < 3 * KS) load_row((it + 1) / KS, (it + 1) % KS, nxt);
+    const int d = dil_of(b, g.d0, g.d1, g.d2);
+    const float* __restrict__ gb = gs + b * lplane;
+    const int lrow = trow + g.R - (ki - r) * d;
+#pragma unroll
+    for (int kj = 0; kj < KS; ++kj) {
+      const int dw = (kj - r) * d;
+      const int s = ((-dw) % V + V) % V;
+      float kv[V];
+      realign<TK, V>(cur[kj][0], cur[kj][1], s, kv);
+      const int j0 = jc - dw;
+#pragma unroll
+      for (int v = 0; v < V; ++v) acc[v] = fmaf(kv[v], staged<V>(gb, g, lrow, j0 + v), acc[v]);
+    }
+  }
+  VecIO<TX, V>::store(gx + (int64_t)plane * HW + (int64_t)gh * g.W + gw, acc);
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -387,7 +532,7 @@ constexpr size_t kFilterMaxLds = 160 * 1024;
 // Tiling for a lane width of `lw` pixels (V consecutive, or U strided) and
 // `planes` staged planes.
 int make_geom(FilterGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int k, int d0, int d1,
-              int d2, int vec, int lw, int planes) {
+              int d2, int vec, int lw, int planes, bool row_banks = false) {
   if (n < 0 || c < 0 || h < 0 || w < 0) return kBadArgument;
   if (k < 1 || (k % 2) == 0 || d0 < 1 || d1 < 1 || d2 < 1) return kBadArgument;
   if (c > (1 << 24) || h > (1 << 20) || w > (1 << 20) || h * w > ((int64_t)1 << 29)) return kUnsupported;
@@ -412,7 +557,15 @@ int make_geom(FilterGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int k, 
   g.LH = g.TH + 2 * g.R;
   const int cols = g.TW + 2 * g.CP;
   g.PS = (cols + vec - 1) / vec;
-  if (vec > 1) g.PS += ((64 / vec) - g.PS % 64 + 64) % 64;  // phases 64/V banks apart
+  if (row_banks) {
+    // the wave's image rows (lpr lanes each) start lpr banks apart, so one
+    // phase read of all its rows is conflict-free; no padding when the rows
+    // fill the wave or the pitch cannot reach lpr
+    if (lpr < 64 && lpr % vec == 0)
+      while ((vec * g.PS) % 64 != lpr) ++g.PS;
+  } else if (vec > 1) {
+    g.PS += ((64 / vec) - g.PS % 64 + 64) % 64;  // phases 64/V banks apart
+  }
   g.RS = vec * g.PS;
   if ((size_t)planes * g.LH * g.RS * sizeof(float) > kFilterMaxLds) return kUnsupported;
   g.tiles_w = (int)((w + g.TW - 1) / g.TW);
@@ -468,6 +621,11 @@ int launch_ks(FilterOp op, const void* a, const void* b, void* o, const FilterGe
         return launch_kernel(filter_bwd_k_kernel<TX, TK, KS, 4>, g, lds1, stream, (const TX*)a, (const TK*)b, (TK*)o, g);
       return launch_kernel(filter_bwd_k_kernel<TX, TK, KS, 1>, g, lds1, stream, (const TX*)a, (const TK*)b, (TK*)o, g);
     case FilterOp::kBwdX:
+      if constexpr (KS >= 1 && 16 % sizeof(TK) == 0) {
+        constexpr int VK = 16 / (int)sizeof(TK);
+        if (vec == VK)
+          return launch_kernel(filter_bwd_x_vec_kernel<TX, TK, KS, VK>, g, 3 * lds1, stream, (const TK*)a, (const TK*)b, (TX*)o, g);
+      }
       // 4 pixels per lane only for K <= 3 (larger K would not keep the
       // in-flight kernel values in registers)
       if constexpr (KS >= 1 && KS <= 3) {
@@ -505,8 +663,29 @@ int run_filter(FilterOp op, const void* a, const void* b, void* o, int64_t n, in
   if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
   if (!a || !b || !o) return kBadArgument;
   int vec = 1, lw = 1;
+  FilterGeom g;
   if (op == FilterOp::kBwdX) {
-    // gather: U = 4 pixels per lane, 64 lanes apart (K <= 3 keeps the
+    // gather with 16 bytes of kernel plane per lane (aligned chunks around
+    // each tap's window) where K has a kernel, rows hold whole chunks and a
+    // branch's K*K tap planes fit one buffer resource
+    const int v = k_dtype == kF32 ? 4 : 8;
+    const bool kvec = (k == 1 || k == 3 || k == 5) && w % v == 0 && aligned(a, 16) &&
+                      aligned(b, 16) && aligned(o, 16) &&
+                      (int64_t)k * k * h * w * (int64_t)esize(k_dtype) <= 0x7fffffffLL;
+    // ... and the three staged tiles leave room for two workgroups per CU
+    // (measured: at K = 5 with 2-byte kernels the tall halo tiles, ~90 KB,
+    // made the vector gather 30% slower than the one-pixel-per-lane one)
+    if (kvec && make_geom(g, n, c, h, w, k, d0, d1, d2, v, v, 3, true) == kOk &&
+        (size_t)3 * g.LH * g.RS * sizeof(float) <= kFilterMaxLds / 2) {
+      return with_type(x_dtype, [&](auto tx) {
+        using TX = decltype(tx);
+        return with_type(k_dtype, [&](auto tk) {
+          using TK = decltype(tk);
+          return launch_typed<TX, TK>(op, a, b, o, g, v, stream);
+        });
+      });
+    }
+    // otherwise U = 4 pixels per lane, 64 lanes apart (K <= 3 keeps the
     // in-flight kernel values within the register budget); unvectorized
     vec = 1;
     lw = (w >= 256 && k <= 3) ? 4 : 1;
@@ -518,7 +697,6 @@ int run_filter(FilterOp op, const void* a, const void* b, void* o, int64_t n, in
                     aligned(a, (size_t)v * esize(x_dtype));
     if (ok) vec = lw = v;
   }
-  FilterGeom g;
   int st = make_geom(g, n, c, h, w, k, d0, d1, d2, vec, lw, op == FilterOp::kBwdX ? 3 : 1);
   if (st != kOk) return st;
   return with_type(x_dtype, [&](auto tx) {

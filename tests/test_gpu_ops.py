@@ -79,9 +79,10 @@ def test_filter_matches_oracle(shape, K, dtype):
     assert_close(kd.grad, dk, atol, rtol, "filter dk")
 
 
-def test_filter_mixed_dtypes_autocast_layout():
+@pytest.mark.parametrize("w", [20, 32])  # W % 8 != 0 / == 0 (16-byte kernel chunks in dX)
+def test_filter_mixed_dtypes_autocast_layout(w):
     """x fp32 with bf16 kernels (the autocast case): out and dK in bf16, dX in fp32."""
-    n, c, h, w, K = 1, 8, 12, 20, 3
+    n, c, h, K = 1, 8, 12, 3
     x = randn((n, c, h, w), 20, torch.float32)
     k = randn((n, 3, c, K * K, h, w), 21, torch.bfloat16)
     g = randn((n, 4 * c, h, w), 22, torch.bfloat16)
