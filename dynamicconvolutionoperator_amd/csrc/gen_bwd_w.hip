@@ -179,7 +179,6 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
   const int C = g.C, H = g.H, W = g.W;
   const int64_t HW = (int64_t)H * W;
   const int64_t CHW = (int64_t)C * HW;
-  const uint32_t row_bytes = (uint32_t)(W * E);
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -206,7 +205,7 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
 #pragma unroll
   for (int part = 0; part < L::kXI; ++part) {
     const int po = 64 * part < L::kXD - 64 ? 64 * part : L::kXD - 64;
-    xlo[part] = ((po + lane) * L::kPerD - kWgPad) * E;
+    xlo[part] = (po + lane) * L::kPerD - kWgPad;  // column of the lane's dword relative to w0
   }
   uint32_t cpo[NJ];
   int cpc[NJ];
@@ -233,8 +232,12 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
     uint32_t* __restrict__ dstb = wsm + buf * L::kBuf;
     const uint32_t rowel = (uint32_t)(p.h * W);
     if (g.xdma) {
-      // x rows: copies of 64 dwords (lane l moves dword l) from a resource
-      // spanning one image row, so columns outside the image read zero
+      // x rows: copies of 64 dwords (lane l moves dword l) from one resource
+      // per image; a dword whose column is outside the image (or whose row or
+      // channel is) reads zero through its offset.  One resource per row
+      // instead cost ~20 scalar instructions per row and step (64-bit
+      // address arithmetic; measured bf16 60.6 -> 56.9 us)
+      const BufRes xres = make_buf(x + (int64_t)p.n * CHW, (uint32_t)(CHW * E));
 #pragma unroll
       for (int j = 0; j < (L::kXRows + NW - 1) / NW; ++j) {
         const int pr = wave + NW * j;
@@ -242,15 +245,15 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
         const int rr = pr >> 4, c = pr & 15;
         const int ch = cb * 16 + c, hh = p.h + (rr - r) * d;
         const bool ok = ch < C && (unsigned)hh < (unsigned)H;
-        const BufRes res =
-            make_buf(ok ? x + ((int64_t)p.n * C + ch) * HW + (int64_t)hh * W : x, ok ? row_bytes : 0u);
+        const uint32_t rowel = (uint32_t)ch * (uint32_t)HW + (uint32_t)(hh * W);
 #pragma unroll
         for (int part = 0; part < L::kXI; ++part) {
           // the last copy ends at the row end (it may overlap the previous one)
           const int po = 64 * part < L::kXD - 64 ? 64 * part : L::kXD - 64;
+          const int gw = p.w0 + xlo[part];
+          const uint32_t off = (ok && (unsigned)gw < (unsigned)W) ? (rowel + (uint32_t)gw) * E : kOob;
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              res, (__attribute__((address_space(3))) void*)(dstb + pr * L::kXSD + po), 4,
-              (uint32_t)(xlo[part] + p.w0 * E), 0, 0, 0);
+              xres, (__attribute__((address_space(3))) void*)(dstb + pr * L::kXSD + po), 4, off, 0, 0, 0);
         }
       }
     } else {
@@ -393,19 +396,39 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
         for (int e = 0; e < 8; ++e) gv[e] = to_f(t8[e]);
       }
     }
+    // The A fragment of tap tt+1 (x reads, products, bf16 split) is formed
+    // while tap tt's MFMAs run: the scheduling groups below put its LDS reads
+    // first and then interleave each MFMA with 3 VALU instructions (measured
+    // 3-5% faster than the compiler's clustering, which left the MFMA pipe
+    // idle during each tap's VALU stretch)
+    auto make_afr = [&](int tt, V (&af)[P]) {
+      float dk[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dk[e] = gv[e] * lds_elem<T>(bb, xel[tt] + e);
+      M::pack(dk, af);
+    };
+    V afc[P];
+    make_afr(0, afc);
 #pragma unroll
     for (int tt = 0; tt < TPH; ++tt) {
       const int t = th * TPH + tt;  // wave-uniform
       if (KK % NH != 0 && t >= KK) break;
-      float dk[8];
+      V afn[P];
+      if (tt + 1 < TPH) make_afr(tt + 1, afn);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dk[e] = gv[e] * lds_elem<T>(bb, xel[tt] + e);
-      V afr[P];
-      M::pack(dk, afr);
+      for (int ib = 0; ib < MB; ++ib) acc[tt][ib] = M::mac(afc, bfr[ib], acc[tt][ib]);
 #pragma unroll
-      for (int ib = 0; ib < MB; ++ib) acc[tt][ib] = M::mac(afr, bfr[ib], acc[tt][ib]);
+      for (int pp = 0; pp < P; ++pp) accb[tt] = M::mac1(afc[pp], ones, accb[tt]);
+      if (tt + 1 < TPH) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // LDS reads
 #pragma unroll
-      for (int pp = 0; pp < P; ++pp) accb[tt] = M::mac1(afr[pp], ones, accb[tt]);
+        for (int i = 0; i < MB * (P == 2 ? 3 : 1) + P; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+        }
+      }
+#pragma unroll
+      for (int pp = 0; pp < P; ++pp) afc[pp] = afn[pp];
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
