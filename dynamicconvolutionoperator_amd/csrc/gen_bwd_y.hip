@@ -127,8 +127,10 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
   const int lane = tid & 63;
   const int col16 = lane & 15, quad = lane >> 4;
   const int nstage = 3 * g.nc32 * KS;  // (b, cc, ki)
-  const uint32_t row_bytes = (uint32_t)(W * E);
 
+  // x planes of image n (per-row resources cost ~20 scalar instructions per
+  // row and stage; measured bf16 44.9 -> 41.6 us)
+  const BufRes xres = make_buf(x + (int64_t)n * C * HW, (uint32_t)(C * HW * (int64_t)E));
   // ---- stage s = ((b * nc32) + cc) * KS + ki -> LDS buffer `buf`
   auto stage = [&](int s, int buf) {
     const int ki = s % KS;
@@ -139,21 +141,24 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
     uint32_t* __restrict__ dstb = ysm + buf * L::kBuf;
     // x rows: 32 channels of row hh, columns w0 - pad .. w0 + TW + pad
     if (g.x4) {
+      // one resource for the image; a chunk outside the image (column, row or
+      // channel) reads zero through its offset (W % 8 == 0: chunks are whole)
 #pragma unroll
       for (int j = 0; j < 32 / kYtWaves; ++j) {
         const int cr = wave + kYtWaves * j;
         const int ch = cc * 32 + cr;
         const bool ok = ch < C && (unsigned)hh < (unsigned)H;
-        const BufRes res =
-            make_buf(ok ? x + ((int64_t)n * C + ch) * HW + (int64_t)hh * W : x, ok ? row_bytes : 0u);
+        const uint32_t rowel = (uint32_t)ch * (uint32_t)HW + (uint32_t)(hh * W);
 #pragma unroll
         for (int part = 0; part < (L::kXChunks + 63) / 64; ++part) {
           // the last copy ends at the row end (it may overlap the previous one)
           const int pc = 64 * part < L::kXChunks - 64 ? 64 * part : (L::kXChunks > 64 ? L::kXChunks - 64 : 0);
+          const int gw = w0 - kYtPad + (pc + lane) * 4 * L::kPerD;
+          const uint32_t off = (ok && (unsigned)gw < (unsigned)W) ? (rowel + (uint32_t)gw) * (uint32_t)E : kOob;
           if (L::kXChunks >= 64 || lane < L::kXChunks)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                res, (__attribute__((address_space(3))) void*)(dstb + L::kXOff + cr * L::kXS + 4 * pc),
-                16, (uint32_t)(w0 - kYtPad + (pc + lane) * 4 * L::kPerD) * (uint32_t)E, 0, 0, 0);
+                xres, (__attribute__((address_space(3))) void*)(dstb + L::kXOff + cr * L::kXS + 4 * pc),
+                16, off, 0, 0, 0);
         }
       }
     } else {
