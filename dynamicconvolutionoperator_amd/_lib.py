@@ -29,6 +29,8 @@ SIGNATURES: dict[str, tuple[list, type]] = {
     "ddpm_gen_supported": ([_L, _I, _I], _I),
     "ddpm_gen_kernels": ([_P, _P, _P, _P, _L, _L, _L, _L, _I, _I, _P], _I),
     "ddpm_gen_kernels_bwd_w_workspace_bytes": ([_L, _L, _L, _L, _I], _L),
+    "ddpm_gen_kernels_bwd_y_workspace_bytes": ([_L, _L, _L, _L, _I], _L),
+    "ddpm_gen_kernels_bwd_y": ([_P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _P], _I),
     "ddpm_gen_kernels_bwd_w": ([_P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _P], _I),
     "ddpm_filter_fwd": (_FILTER_ARGS, _I),
     "ddpm_filter_bwd_x": (_FILTER_ARGS, _I),
@@ -75,6 +77,9 @@ def available() -> bool:
         return True
     except HipLibraryError:
         return False
+
+
+STATUS_UNSUPPORTED = 10002
 
 
 def check(code: int, what: str) -> None:

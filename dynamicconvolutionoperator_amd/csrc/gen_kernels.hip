@@ -616,6 +616,230 @@ __global__ __launch_bounds__(256) void gk_bwd_w_reduce_kernel(const float* __res
   }
 }
 
+// ---------------------------------------------------------------------------
+// Backward of the generator convolution, input:
+//
+//   dY[n][i][p] = sum_o W[o][i] * dK[n][o][p]
+//
+// (the Conv2d input gradient of `self.generator` on the reference's
+// materialized path, triton_impl.py:340-347).  MFMA with M = 16 channels i,
+// N = 16 pixels, K = 32 rows o.  The A operand is W transposed, packed once
+// per call in fragment order (fp32: bf16 hi / lo parts).  The reduction runs
+// over the rows of dK, so a B fragment is 8 rows at one pixel: the dK tile
+// (32*KCH rows x 128 pixels) is copied global -> LDS by 16-byte LDS-direct
+// loads, 4 (2-byte) or 2 (fp32) rows x 256 / 512 contiguous bytes per copy,
+// and read transposed, one 2- or 4-byte LDS read per element; chunk c of row
+// r sits at position c ^ ((r >> 3) & 3) * (16 pixels / chunk width), so the
+// 4 row groups of a fragment read hit disjoint banks.  A workgroup = 4 waves
+// x 32 pixels, all channels; splits over o (fp32 partials summed in split
+// order by a second kernel) when the pixel tiles alone cannot fill the GPU.
+// ---------------------------------------------------------------------------
+
+constexpr int kGyPX = 128;    // pixels per workgroup
+constexpr int kGySlots = 512; // workgroups the splits aim for
+constexpr int kGyMinStages = 4;
+
+struct GyGeom {
+  int N, C, HW, O;
+  int tpi;               // pixel tiles per image
+  int tiles;             // N * tpi
+  int oc;                // 32-row chunks of o, ceil(O / 32)
+  int stages;            // ceil(oc / KCH)
+  int splits;
+  int stages_per_split;
+};
+
+template <typename T, int MB>
+struct GyLds {
+  static constexpr int E = (int)sizeof(T);
+  static constexpr int P = Mma<T>::P;
+  static constexpr int KCH = E == 2 ? 2 : 1;        // 32-row chunks per stage
+  static constexpr int ROWS = 32 * KCH;
+  static constexpr int CPX = 16 / E;                // pixels per 16-byte chunk
+  static constexpr int CPR = kGyPX / CPX;           // chunks per tile row
+  static constexpr int ROWB = kGyPX * E;            // bytes per tile row
+  static constexpr int SWZ = 16 / CPX;              // chunks per 16 pixels
+  static constexpr int DKB = ROWS * ROWB;           // dK tile bytes (16 KB)
+  static constexpr int NDK = DKB / 1024;            // 1 KB copies of the dK tile
+  static constexpr int NA = KCH * MB * P;           // 1 KB units of the W^T slice
+  static constexpr int BUF = DKB + NA * 1024;
+  static_assert(NDK % 4 == 0, "dK copies split evenly over the waves");
+};
+
+// W [O][C] -> packed A fragments: unit ((oc*MB + cb)*P + pp), lane m + 16q
+// holds part pp of W[32oc + 8q + e][16cb + m], e < 8 (zero outside W)
+template <typename T>
+__global__ __launch_bounds__(256) void gk_pack_wt_kernel(const T* __restrict__ w,
+                                                        uint32_t* __restrict__ pk, int O, int C,
+                                                        int MB, int64_t total) {
+  typedef Mma<T> M;
+  constexpr int P = M::P;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (oc, cb, lane)
+  if (idx >= total) return;
+  const int lane = (int)(idx & 63);
+  const int64_t u = idx >> 6;
+  const int cb = (int)(u % MB), oc = (int)(u / MB);
+  const int m = lane & 15, q = lane >> 4;
+  const int i = 16 * cb + m;
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int o = 32 * oc + 8 * q + e;
+    v[e] = (o < O && i < C) ? to_f(w[(int64_t)o * C + i]) : 0.f;
+  }
+  typename M::V f[P];
+  M::pack(v, f);
+  u32x4* __restrict__ dst = reinterpret_cast<u32x4*>(pk);
+#pragma unroll
+  for (int pp = 0; pp < P; ++pp) dst[(u * P + pp) * 64 + lane] = __builtin_bit_cast(u32x4, f[pp]);
+}
+
+template <typename T, int MB>
+__global__ __launch_bounds__(256) void gk_bwd_y_kernel(const T* __restrict__ gk,
+                                                      const uint32_t* __restrict__ pk,
+                                                      float* __restrict__ part, T* __restrict__ dy,
+                                                      GyGeom g) {
+  typedef GyLds<T, MB> L;
+  typedef Mma<T> M;
+  typedef typename M::V V;
+  constexpr int P = M::P;
+  constexpr uint32_t E = sizeof(T);
+  constexpr int NDW = L::NDK / 4;                 // dK copies per wave
+  constexpr int NAW = (L::NA + 3) / 4;            // W^T copies per wave (some idle)
+  extern __shared__ __attribute__((aligned(16))) uint32_t ysm[];
+
+  const int tile = blockIdx.x % g.tiles;
+  const int split = blockIdx.x / g.tiles;
+  const int n = tile / g.tpi;
+  const int px0 = (tile - n * g.tpi) * kGyPX;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int col16 = lane & 15, quad = lane >> 4;
+  const int C = g.C, HW = g.HW, O = g.O;
+  const int st_beg = split * g.stages_per_split;
+  const int st_end = st_beg + g.stages_per_split < g.stages ? st_beg + g.stages_per_split : g.stages;
+
+  // this lane's chunk of each dK copy: tile row and first pixel
+  int drow[NDW], dpx[NDW];
+#pragma unroll
+  for (int j = 0; j < NDW; ++j) {
+    const int lc = (wave * NDW + j) * 64 + lane;
+    const int row = lc / L::CPR, pos = lc % L::CPR;
+    drow[j] = row;
+    dpx[j] = (pos ^ (((row >> 3) & 3) * L::SWZ)) * L::CPX;
+  }
+  const BufRes dres = make_buf(gk + (int64_t)n * O * HW, (uint32_t)O * (uint32_t)HW * E);
+  auto stage = [&](int st, int buf) {
+    char* dst = reinterpret_cast<char*>(ysm) + buf * L::BUF;
+    const int o0 = st * L::ROWS;
+#pragma unroll
+    for (int j = 0; j < NDW; ++j) {
+      const int o = o0 + drow[j], px = px0 + dpx[j];
+      const uint32_t off = (o < O && px < HW) ? ((uint32_t)o * (uint32_t)HW + (uint32_t)px) * E : kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          dres, (__attribute__((address_space(3))) void*)(dst + (wave * NDW + j) * 1024), 16, off, 0, 0, 0);
+    }
+    // the stage's W^T slice: KCH chunks x MB x P units, contiguous in pk
+    const int units = (g.oc - st * L::KCH < L::KCH ? g.oc - st * L::KCH : L::KCH) * MB * P;
+    const BufRes pres = make_buf(pk + (int64_t)st * L::NA * 256, (uint32_t)units * 1024u);
+#pragma unroll
+    for (int j = 0; j < NAW; ++j) {
+      const int u = wave * NAW + j;
+      if (u < L::NA)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            pres, (__attribute__((address_space(3))) void*)(dst + L::DKB + u * 1024), 16,
+            (uint32_t)(u * 64 + lane) * 16u, 0, 0, 0);
+    }
+  };
+
+  f32x4 acc[2][MB];
+#pragma unroll
+  for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+    for (int ib = 0; ib < MB; ++ib) acc[pb][ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int nst = st_end > st_beg ? st_end - st_beg : 0;
+  if (nst > 0) stage(st_beg, 0);
+  for (int it = 0; it < nst; ++it) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // buffer it & 1 is whole; buffer (it + 1) & 1 is no longer read
+    if (it + 1 < nst) stage(st_beg + it + 1, (it + 1) & 1);
+    const char* bb = reinterpret_cast<const char*>(ysm) + (it & 1) * L::BUF;
+#pragma unroll
+    for (int kc = 0; kc < L::KCH; ++kc) {
+      V af[MB][P];
+#pragma unroll
+      for (int ib = 0; ib < MB; ++ib)
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp)
+          af[ib][pp] = __builtin_bit_cast(
+              V, *reinterpret_cast<const u32x4*>(bb + L::DKB + (((kc * MB + ib) * P + pp) * 64 + lane) * 16));
+#pragma unroll
+      for (int pb = 0; pb < 2; ++pb) {
+        const int pl = 32 * wave + 16 * pb + col16;  // pixel within the tile
+        const int c = pl / L::CPX, within = (pl % L::CPX) * (int)E;
+        V bf[P];
+        if constexpr (E == 4) {
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int row = 32 * kc + 8 * quad + e;
+            v[e] = *reinterpret_cast<const float*>(bb + row * L::ROWB +
+                                                   16 * (c ^ (((row >> 3) & 3) * L::SWZ)) + within);
+          }
+          M::pack(v, bf);
+        } else {
+          uint32_t wd[4];
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) {
+            const int r0 = 32 * kc + 8 * quad + 2 * e2;  // rows r0, r0 + 1 share (r >> 3)
+            const int sw = 16 * (c ^ (((r0 >> 3) & 3) * L::SWZ)) + within;
+            const uint32_t lo = *reinterpret_cast<const uint16_t*>(bb + r0 * L::ROWB + sw);
+            const uint32_t hi = *reinterpret_cast<const uint16_t*>(bb + (r0 + 1) * L::ROWB + sw);
+            wd[e2] = lo | (hi << 16);
+          }
+          bf[0] = __builtin_bit_cast(V, (u32x4){wd[0], wd[1], wd[2], wd[3]});
+        }
+#pragma unroll
+        for (int ib = 0; ib < MB; ++ib) acc[pb][ib] = M::mac(af[ib], bf, acc[pb][ib]);
+      }
+    }
+  }
+
+  // D row 4*quad + r of block ib is channel 16*ib + 4*quad + r, column col16
+  // of block pb is pixel px0 + 32*wave + 16*pb + col16
+  const bool direct = g.splits == 1;
+#pragma unroll
+  for (int pb = 0; pb < 2; ++pb) {
+    const int px = px0 + 32 * wave + 16 * pb + col16;
+    if (px >= HW) continue;
+#pragma unroll
+    for (int ib = 0; ib < MB; ++ib)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * ib + 4 * quad + r;
+        if (i >= C) continue;
+        const int64_t el = ((int64_t)n * C + i) * HW + px;
+        if (direct)
+          dy[el] = from_f<T>(acc[pb][ib][r]);
+        else
+          part[(int64_t)split * g.N * C * HW + el] = acc[pb][ib][r];
+      }
+  }
+}
+
+// dY = sum of the o-split partials in split order
+template <typename T>
+__global__ __launch_bounds__(256) void gk_bwd_y_reduce_kernel(const float* __restrict__ part,
+                                                             T* __restrict__ dy, int64_t total,
+                                                             int splits) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= total) return;
+  float v = 0.f;
+  for (int sp = 0; sp < splits; ++sp) v += part[sp * total + idx];
+  dy[idx] = from_f<T>(v);
+}
+
 namespace {
 
 template <typename F>
@@ -675,6 +899,33 @@ int64_t gw_align(int64_t v) { return (v + 255) / 256 * 256; }
 int64_t gw_partial_bytes(const GwGeom& g) {
   if (g.splits <= 1) return 0;
   return (int64_t)g.splits * ((int64_t)g.O * g.C + g.O) * (int64_t)sizeof(float);
+}
+
+
+// Channel blocks of the dY kernel and its o splits: as many as fill
+// kGySlots workgroups over the pixel tiles, at least kGyMinStages stages each.
+int gy_mb(int64_t c) { return c <= 16 ? 1 : c <= 32 ? 2 : c <= 64 ? 4 : 8; }
+
+void gy_geom(GyGeom& g, int64_t n, int64_t c, int64_t hw, int64_t o, int kch) {
+  g.N = (int)n;
+  g.C = (int)c;
+  g.HW = (int)hw;
+  g.O = (int)o;
+  g.tpi = (int)((hw + kGyPX - 1) / kGyPX);
+  g.tiles = (int)(n * g.tpi);
+  g.oc = (int)((o + 31) / 32);
+  g.stages = (g.oc + kch - 1) / kch;
+  int64_t splits = g.tiles > 0 ? kGySlots / g.tiles : 1;
+  const int64_t most = (g.stages + kGyMinStages - 1) / kGyMinStages;
+  if (splits > most) splits = most;
+  if (splits < 1) splits = 1;
+  g.stages_per_split = (g.stages + (int)splits - 1) / (int)splits;
+  g.splits = (g.stages + g.stages_per_split - 1) / g.stages_per_split;
+}
+
+int64_t gy_pack_bytes(const GyGeom& g, int parts) { return (int64_t)g.oc * gy_mb(g.C) * parts * 1024; }
+int64_t gy_part_bytes(const GyGeom& g) {
+  return g.splits > 1 ? (int64_t)g.splits * g.N * g.C * g.HW * (int64_t)sizeof(float) : 0;
 }
 
 }  // namespace
@@ -837,6 +1088,85 @@ extern "C" int ddpm_gen_kernels_bwd_w(const void* y, const void* grad_kernels, v
         return launch(gk_bwd_w_kernel<T, 4, 4, false>, 0);
       default:
         return launch(gk_bwd_w_kernel<T, 2, 8, false>, 0);
+    }
+  });
+}
+
+
+extern "C" int64_t ddpm_gen_kernels_bwd_y_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w,
+                                                          int kernel_size) {
+  if (n <= 0 || c <= 0 || h <= 0 || w <= 0 || kernel_size < 1 || kernel_size % 2 == 0) return 0;
+  if (c > kGkMaxC || n * ((h * w + kGyPX - 1) / kGyPX) > 0x7fffffffLL) return 0;
+  const int64_t o = 3 * c * kernel_size * kernel_size;
+  // the query takes no dtype: the largest of the 2-byte and fp32 layouts
+  int64_t most = 0;
+  for (int fp32 = 0; fp32 < 2; ++fp32) {
+    GyGeom g;
+    gy_geom(g, n, c, h * w, o, fp32 ? 1 : 2);
+    most = std::max(most, gw_align(gy_pack_bytes(g, fp32 ? 2 : 1)) + gy_part_bytes(g));
+  }
+  return most;
+}
+
+extern "C" int ddpm_gen_kernels_bwd_y(const void* weight, const void* grad_kernels, void* grad_y,
+                                      void* workspace, int64_t workspace_bytes, int64_t n, int64_t c,
+                                      int64_t h, int64_t w, int kernel_size, int dtype,
+                                      hipStream_t stream) {
+  if (dtype < kF32 || dtype > kF16) return kBadArgument;
+  if (n < 0 || c < 0 || h < 0 || w < 0) return kBadArgument;
+  if (kernel_size < 1 || kernel_size % 2 == 0) return kBadArgument;
+  if (c > kGkMaxC) return kUnsupported;
+  if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
+  if (!weight || !grad_kernels || !grad_y) return kBadArgument;
+  const int64_t esz = dtype == kF32 ? 4 : 2;
+  const int64_t hw = h * w, o = 3 * c * kernel_size * kernel_size;
+  // 16-byte chunks of whole dK rows; 32-bit offsets inside one image's planes
+  if (hw % 8 != 0 || (uintptr_t)grad_kernels % 16 != 0) return kUnsupported;
+  if (o * hw * esz > 0x7fffffffLL || n * ((hw + kGyPX - 1) / kGyPX) > 0x7fffffffLL) return kUnsupported;
+  GyGeom g;
+  gy_geom(g, n, c, hw, o, esz == 2 ? 2 : 1);
+  const int parts = esz == 4 ? 2 : 1;
+  const int64_t pkb = gy_pack_bytes(g, parts);
+  if (!workspace || (uintptr_t)workspace % 16 != 0 ||
+      workspace_bytes < gw_align(pkb) + gy_part_bytes(g))
+    return kWorkspaceTooSmall;
+  uint32_t* pk = (uint32_t*)workspace;
+  float* part = (float*)((char*)workspace + gw_align(pkb));
+  const int mb = gy_mb(c);
+  return gk_with_type(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    const int64_t ptotal = (int64_t)g.oc * mb * 64;
+    hipLaunchKernelGGL((gk_pack_wt_kernel<T>), dim3((unsigned)((ptotal + 255) / 256)), dim3(256), 0,
+                       stream, (const T*)weight, pk, (int)o, (int)c, mb, ptotal);
+    int e = (int)hipGetLastError();
+    if (e != 0) return e;
+    auto launch = [&](auto mbc) {
+      constexpr int MB = decltype(mbc)::value;
+      const size_t shm = (size_t)2 * GyLds<T, MB>::BUF;
+      auto kern = gk_bwd_y_kernel<T, MB>;
+      if (shm > 64 * 1024) {
+        const hipError_t ae = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+        if (ae != hipSuccess) return (int)ae;
+      }
+      hipLaunchKernelGGL(kern, dim3((unsigned)(g.tiles * g.splits)), dim3(256), shm, stream,
+                         (const T*)grad_kernels, (const uint32_t*)pk, part, (T*)grad_y, g);
+      int e2 = (int)hipGetLastError();
+      if (e2 != 0 || g.splits == 1) return e2;
+      const int64_t total = n * c * hw;
+      hipLaunchKernelGGL((gk_bwd_y_reduce_kernel<T>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                         stream, (const float*)part, (T*)grad_y, total, g.splits);
+      return (int)hipGetLastError();
+    };
+    switch (mb) {
+      case 1:
+        return launch(std::integral_constant<int, 1>());
+      case 2:
+        return launch(std::integral_constant<int, 2>());
+      case 4:
+        return launch(std::integral_constant<int, 4>());
+      default:
+        return launch(std::integral_constant<int, 8>());
     }
   });
 }

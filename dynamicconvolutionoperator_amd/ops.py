@@ -258,8 +258,8 @@ class _GeneratorKernels(torch.autograd.Function):
     ``[N, 3CK², H, W]`` in y's dtype (the reference's ``self.generator(y)``,
     triton_impl.py:340-347).  Forward: one HIP MFMA kernel with the bias and
     the output rounding fused.  Backward: dW and db in one HIP kernel that
-    reads dK once (``ddpm_gen_kernels_bwd_w``), dY = Wᵀ·dK as a batched
-    product."""
+    reads dK once (``ddpm_gen_kernels_bwd_w``), dY = Wᵀ·dK in another
+    (``ddpm_gen_kernels_bwd_y``)."""
 
     @staticmethod
     def forward(ctx, y, weight, bias, kernel_size):
@@ -294,7 +294,7 @@ class _GeneratorKernels(torch.autograd.Function):
         g = grad.to(y.dtype).contiguous().view(n, o, h * w)
         grad_y = grad_w = grad_b = None
         if ctx.needs_input_grad[0]:
-            grad_y = torch.matmul(w2.t().contiguous(), g).view(n, c, h, w)
+            grad_y = _generator_kernels_input_grad(w2, g, n, c, h, w, ctx.kernel_size)
         if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
             k = ctx.kernel_size
             lib = _lib.load()
@@ -311,6 +311,22 @@ class _GeneratorKernels(torch.autograd.Function):
             if ctx.needs_input_grad[2]:
                 grad_b = gb
         return grad_y, grad_w, grad_b, None
+
+
+def _generator_kernels_input_grad(w2, g, n, c, h, w, k):
+    """dY = Wᵀ·dK of the generator convolution through ``ddpm_gen_kernels_bwd_y``;
+    shapes it does not cover (H·W not a multiple of 8) use a batched product."""
+    lib = _lib.load()
+    grad_y = torch.empty((n, c, h, w), dtype=g.dtype, device=g.device)
+    with torch.cuda.device(g.device):
+        ws_bytes = int(lib.ddpm_gen_kernels_bwd_y_workspace_bytes(n, c, h, w, k))
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=g.device)
+        code = lib.ddpm_gen_kernels_bwd_y(_ptr(w2), _ptr(g), _ptr(grad_y), _ptr(ws), ws_bytes, n, c, h,
+                                          w, k, _dt(g), _stream(g))
+    if code == _lib.STATUS_UNSUPPORTED:
+        return torch.matmul(w2.t().contiguous(), g).view(n, c, h, w)
+    _lib.check(code, "ddpm_gen_kernels_bwd_y")
+    return grad_y
 
 
 def generator_kernels(y, weight, bias, kernel_size):

@@ -180,6 +180,7 @@ def test_generator_dilation_sets(K, dil, fused, shape, dtype):
         ((3, 8, 40, 40), 5),   # C = 8: one channel block, 5 (2-byte) / 10 (fp32) splits
         ((2, 24, 45, 37), 3),  # odd H*W: element-wise operand loads, 4 splits
         ((1, 128, 32, 64), 3),  # C = 128: 64-pixel steps, 4 splits
+        ((1, 8, 16, 24), 3),   # 216 rows o: dY in one o split, written directly
     ],
 )
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])

@@ -68,6 +68,11 @@ def test_host_only_queries():
     # 8 steps of 32 pixels (4x64) or fewer: one split, no partials
     assert lib.ddpm_gen_kernels_bwd_w_workspace_bytes(1, 64, 4, 64, 5) == ysplit(1, 64, 4, 64)
     assert lib.ddpm_gen_kernels_bwd_w_workspace_bytes(1, 129, 32, 32, 5) == 0  # unsupported
+    # its input gradient: 150 chunks of 32 rows packed as fp32 hi / lo fragments
+    # (2 KB per chunk and 16-channel block), then 4 o splits of fp32 dY partials
+    # (128 pixel tiles x 4 = 512 workgroups)
+    assert lib.ddpm_gen_kernels_bwd_y_workspace_bytes(1, 64, 128, 128, 5) == (
+        150 * 4 * 2 * 1024 + 4 * 64 * 128 * 128 * 4)
 
 
 def test_entry_points_validate_arguments_before_touching_the_device():
@@ -87,6 +92,9 @@ def test_entry_points_validate_arguments_before_touching_the_device():
     assert lib.ddpm_gen_kernels_bwd_w(null, null, null, null, null, 0, 1, 64, 8, 8, 4, 1, null) == 10001
     assert lib.ddpm_gen_kernels_bwd_w(null, null, null, null, null, 0, 1, 129, 8, 8, 5, 1, null) == 10002
     assert lib.ddpm_gen_kernels_bwd_w(null, null, null, null, null, 0, 1, 64, 8, 8, 5, 1, null) == 10001
+    assert lib.ddpm_gen_kernels_bwd_y(null, null, null, null, 0, 1, 64, 8, 8, 4, 1, null) == 10001
+    assert lib.ddpm_gen_kernels_bwd_y(null, null, null, null, 0, 1, 129, 8, 8, 5, 1, null) == 10002
+    assert lib.ddpm_gen_kernels_bwd_y(null, null, null, null, 0, 0, 64, 8, 8, 5, 1, null) == 0
     # empty tensors are a no-op
     assert lib.ddpm_filter_fwd(null, null, null, 0, 4, 4, 4, 3, 1, 3, 5, 0, 0, null) == 0
     assert lib.ddpm_gen_kernels(null, null, null, null, 0, 64, 8, 8, 5, 1, null) == 0
