@@ -3,7 +3,7 @@
 * 256x256 fused recompute training, fp32 and bf16, against the float64 CPU
   oracle (forward and all gradients);
 * 128x128 fused inference, fp32;
-* K=5 128x128 bf16 materialized inference and training;
+* K=5 128x128 bf16 materialized inference and training, fp32 training;
 * size-independent adjoint identities of the fused operator at 256x256:
   the fused op is linear in x and affine in y, W and b, so
   <F(x + v) - F(x), g> = <v, dX(g)> and likewise for y, W and b; both sides
@@ -54,6 +54,13 @@ def test_k5_128_bf16_materialized():
         actual = cand(x.to(DEV), y.to(DEV))
     assert_close(actual, expected, 5e-2, 5e-2, "out K5 bf16")
     check_training(64, 128, 128, 5, torch.bfloat16, fused=False, n=1, seed=23)
+
+
+def test_k5_128_fp32_materialized_training():
+    """The materialized route's fp32 backward: the generator convolution's
+    weight / bias and input gradients run as split-bf16 MFMA kernels."""
+    say("full-size K=5 128x128 fp32 materialized training")
+    check_training(64, 128, 128, 5, torch.float32, fused=False, n=1, seed=24)
 
 
 def _dot(a, b):
