@@ -45,11 +45,15 @@ __global__ __launch_bounds__(256) void gen_bwd_x_reduce_kernel(const float* __re
                                                                T* __restrict__ gx, TileGeom g) {
   typedef float FV __attribute__((ext_vector_type(4)));
   typedef T TV __attribute__((ext_vector_type(4)));
+  // one thread per (row, group of VEC columns), flattened over all rows so
+  // that every lane has work (a block per row left 3 of 4 waves idle at
+  // W = 256)
   const int gpr = (g.W + VEC - 1) / VEC;  // column groups per row
-  const int segs = (gpr + 255) / 256;
-  const int row = blockIdx.x / segs;      // (n*C + c)*H + h
-  const int gi = (blockIdx.x - row * segs) * 256 + threadIdx.x;
-  if (gi >= gpr) return;
+  const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t rows = (int64_t)g.N * g.C * g.H;
+  if (item >= rows * gpr) return;
+  const int row = (int)(item / gpr);      // (n*C + c)*H + h
+  const int gi = (int)(item - (int64_t)row * gpr);
   const int w = gi * VEC;
   const int nc = row / g.H, h = row - nc * g.H;
   const int n = nc / g.C, c = nc - n * g.C;
@@ -156,10 +160,10 @@ extern "C" int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bia
   // 32-bit buffer offsets inside one image's [C][H][W] planes (and 16 planes
   // past a channel block's first one)
   if (c * h * w * esz > 0x7fffffffLL || 16 * h * w * esz > 0x7fffffffLL) return kUnsupported;
-  // one reduce workgroup per 256 column groups of a row
+  // reduce: one thread per group of `vec` columns of every row
   const int vec = w % 4 == 0 ? 4 : 1;
-  const int64_t rsegs = ((w + vec - 1) / vec + 255) / 256;
-  if (n * c * h * rsegs > 0x7fffffffLL) return kUnsupported;
+  const int64_t ritems = n * c * h * ((w + vec - 1) / vec);
+  if ((ritems + 255) / 256 > 0x7fffffffLL || n * c * h > 0x7fffffffLL) return kUnsupported;
   TileGeom g;
   int cb;
   size_t lds;
@@ -182,7 +186,7 @@ extern "C" int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bia
                          (const T*)weight, (const T*)bias, part, g);
       int e = (int)hipGetLastError();
       if (e != 0) return e;
-      const dim3 rgrid((unsigned)(n * c * h * rsegs));
+      const dim3 rgrid((unsigned)((ritems + 255) / 256));
       if (vec == 4)
         hipLaunchKernelGGL((gen_bwd_x_reduce_kernel<T, 4>), rgrid, dim3(256), 0, stream,
                            (const float*)part, (const T*)grad_out, (T*)grad_x, g);
