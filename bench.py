@@ -102,9 +102,9 @@ class LaunchTimer:
     """Brackets every call of the named C-ABI entry points with HIP events.
 
     Every entry point takes the stream it launches on as its last argument
-    (the current stream, or a side stream for two of the backward entry
-    points); the events are recorded on that stream, so each (start, end)
-    pair spans exactly that entry point's kernels on their own stream.
+    (the operators pass the current stream); the events are recorded on that
+    stream, so each (start, end) pair spans exactly that entry point's
+    kernels, also for a caller that launches on a stream of its own.
     """
 
     def __init__(self, lib, names):
