@@ -135,7 +135,9 @@ __global__ __launch_bounds__(kGkThreads) void gen_kernels_kernel(const T* __rest
   constexpr int RPI = 64 / LPR;           // tile rows per store instruction
   __shared__ __attribute__((aligned(16))) char wtile[kPair ? kGkWaves : 1][kPair ? 16 * TROW : 16];
   char* __restrict__ wtp = wtile[kPair ? wave : 0];
-#pragma unroll 2
+  // one output block per iteration: the body is too large to unroll (asking
+  // for two leaves the code unchanged)
+#pragma unroll 1
   for (int ob = ob0; ob < ob1; ++ob) {
     const int o = ob * 16 + col16;  // this lane's output row (B column)
     const bool orow = o < O;
@@ -281,21 +283,14 @@ struct GwLds {
   static_assert(NA % kGwWaves == 0 && NY % kGwWaves == 0, "copies split evenly over the waves");
 };
 
-// 8 consecutive elements (pixels) of a plane row as raw MFMA operand dwords:
-// one 16-byte load per 16 bytes when VEC (the row offset is a multiple of 8
-// elements and the 8 pixels are all in or all out of the image), else
-// element-wise with every pixel masked on its own.  `off` is the element
-// offset of the first pixel, `ok` whether the row exists, `nv` the number of
-// valid pixels from the first.
-template <typename T, bool VEC>
+// 8 consecutive elements (pixels) of a plane row as raw MFMA operand dwords,
+// element-wise with every pixel masked on its own (any H*W).  `off` is the
+// element offset of the first pixel, `ok` whether the row exists, `nv` the
+// number of valid pixels from the first.
+template <typename T>
 __device__ __forceinline__ void gw_load_row8(BufRes r, uint32_t off, bool ok, int nv,
                                              u32x4 (&d)[sizeof(T) == 4 ? 2 : 1]) {
-  constexpr uint32_t E = sizeof(T);
-  if constexpr (VEC) {
-    const uint32_t b = (ok && nv > 0) ? off * E : kOob;
-    d[0] = __builtin_amdgcn_raw_buffer_load_b128(r, b, 0, 0);
-    if constexpr (E == 4) d[1] = __builtin_amdgcn_raw_buffer_load_b128(r, b + (b == kOob ? 0u : 16u), 0, 0);
-  } else if constexpr (E == 4) {
+  if constexpr (sizeof(T) == 4) {
 #pragma unroll
     for (int e = 0; e < 8; ++e)
       d[e >> 2][e & 3] = __builtin_amdgcn_raw_buffer_load_b32(r, (ok && e < nv) ? (off + e) * 4u : kOob, 0, 0);
@@ -311,7 +306,7 @@ __device__ __forceinline__ void gw_load_row8(BufRes r, uint32_t off, bool ok, in
 }
 
 // yb: y itself (2-byte types) or its bf16 hi / lo planes [N][2][C][HW] (fp32).
-template <typename T, int RB, int CB, bool VEC>
+template <typename T, int RB, int CB>
 __global__ __launch_bounds__(64 * kGwWaves) void gk_bwd_w_kernel(const T* __restrict__ gk,
                                                                 const uint16_t* __restrict__ yb,
                                                                 float* __restrict__ pw,
@@ -324,9 +319,7 @@ __global__ __launch_bounds__(64 * kGwWaves) void gk_bwd_w_kernel(const T* __rest
   constexpr int AD = sizeof(T) == 4 ? 2 : 1;  // 16-byte dwords of a lane's 8 dK values
   constexpr uint32_t E = sizeof(T);
   constexpr int RS = CB * 16 + 1;
-  // 32-pixel steps per load batch: 16 (2-byte) or 8 (fp32) 16-byte loads of dK
-  // per wave, plus the y loads
-  constexpr int KC = 1;
+  constexpr int KC = 1;  // 32-pixel steps per iteration of a wave
   __shared__ float red[RB * 16 * RS];
   __shared__ float redb[RB * 16];
 
@@ -378,13 +371,13 @@ __global__ __launch_bounds__(64 * kGwWaves) void gk_bwd_w_kernel(const T* __rest
       const BufRes ar = make_buf(gk + (int64_t)n * O * HW, (uint32_t)O * (uint32_t)HW * E);
       const BufRes br = make_buf(yb + (int64_t)n * P * C * HW, (uint32_t)(P * C) * (uint32_t)HW * 2u);
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) gw_load_row8<T, VEC>(ar, arow[rb] + (uint32_t)px, aok[rb], nv, ac[k][rb]);
+      for (int rb = 0; rb < RB; ++rb) gw_load_row8<T>(ar, arow[rb] + (uint32_t)px, aok[rb], nv, ac[k][rb]);
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
         for (int pp = 0; pp < P; ++pp) {
           u32x4 t[1];
-          gw_load_row8<uint16_t, VEC>(br, brow[cb][pp] + (uint32_t)px, bok[cb], nv, t);
+          gw_load_row8<uint16_t>(br, brow[cb][pp] + (uint32_t)px, bok[cb], nv, t);
           bc[k][cb][pp] = t[0];
         }
     }
@@ -1107,13 +1100,13 @@ extern "C" int ddpm_gen_kernels_bwd_w(const void* y, const void* grad_kernels, v
     }
     switch (cb) {
       case 1:
-        return launch(gk_bwd_w_kernel<T, 4, 1, false>, 0);
+        return launch(gk_bwd_w_kernel<T, 4, 1>, 0);
       case 2:
-        return launch(gk_bwd_w_kernel<T, 4, 2, false>, 0);
+        return launch(gk_bwd_w_kernel<T, 4, 2>, 0);
       case 4:
-        return launch(gk_bwd_w_kernel<T, 4, 4, false>, 0);
+        return launch(gk_bwd_w_kernel<T, 4, 4>, 0);
       default:
-        return launch(gk_bwd_w_kernel<T, 2, 8, false>, 0);
+        return launch(gk_bwd_w_kernel<T, 2, 8>, 0);
     }
   });
 }
