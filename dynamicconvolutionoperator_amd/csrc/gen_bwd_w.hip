@@ -116,35 +116,36 @@ struct WgPos {
 };
 
 // fp32 y -> bf16 hi / lo planes ys[n][part][c][hw] (hi = top 16 bits of the
-// fp32 pattern, lo = the remainder rounded to nearest even).  Each thread
+// fp32 pattern, lo = the remainder rounded to nearest even).  Grid: x over
+// one image's C*H*W elements, 8 per thread; y over images.  Each thread
 // splits 8 consecutive elements: two 16-byte loads, two 16-byte stores when
 // one image's planes hold a multiple of 8 elements, element-wise otherwise.
 __global__ __launch_bounds__(256) void gen_ysplit_kernel(const float* __restrict__ y,
-                                                         uint16_t* __restrict__ ys, int64_t chw,
-                                                         int64_t total) {
-  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
-  if (i0 >= total) return;
-  if (chw % 8 == 0) {
-    // 8 elements of one image (i0 and chw are multiples of 8)
-    const int64_t n = i0 / chw;
-    const f32x4 a = *reinterpret_cast<const f32x4*>(y + i0);
-    const f32x4 c = *reinterpret_cast<const f32x4*>(y + i0 + 4);
-    uint32_t hi[4], lo[4];
-    split_bf16x2(a[0], a[1], hi[0], lo[0]);
-    split_bf16x2(a[2], a[3], hi[1], lo[1]);
-    split_bf16x2(c[0], c[1], hi[2], lo[2]);
-    split_bf16x2(c[2], c[3], hi[3], lo[3]);
-    uint16_t* __restrict__ h = ys + n * chw + i0;  // = ys + n*2*chw + (i0 - n*chw)
-    *reinterpret_cast<u32x4*>(h) = (u32x4){hi[0], hi[1], hi[2], hi[3]};
-    *reinterpret_cast<u32x4*>(h + chw) = (u32x4){lo[0], lo[1], lo[2], lo[3]};
-    return;
-  }
-  for (int64_t i = i0; i < total && i < i0 + 8; ++i) {
-    uint32_t h2, l2;
-    split_bf16x2(y[i], 0.f, h2, l2);
-    uint16_t* __restrict__ h = ys + (i / chw) * chw + i;
-    h[0] = (uint16_t)h2;
-    h[chw] = (uint16_t)l2;
+                                                         uint16_t* __restrict__ ys, uint32_t chw,
+                                                         uint32_t nimg) {
+  const uint32_t i0 = (blockIdx.x * 256u + threadIdx.x) * 8u;
+  if (i0 >= chw) return;
+  for (uint32_t n = blockIdx.y; n < nimg; n += gridDim.y) {
+    const float* __restrict__ src = y + (int64_t)n * chw;
+    uint16_t* __restrict__ h = ys + (int64_t)n * 2 * chw;
+    if (chw % 8 == 0) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(src + i0);
+      const f32x4 c = *reinterpret_cast<const f32x4*>(src + i0 + 4);
+      uint32_t hi[4], lo[4];
+      split_bf16x2(a[0], a[1], hi[0], lo[0]);
+      split_bf16x2(a[2], a[3], hi[1], lo[1]);
+      split_bf16x2(c[0], c[1], hi[2], lo[2]);
+      split_bf16x2(c[2], c[3], hi[3], lo[3]);
+      *reinterpret_cast<u32x4*>(h + i0) = (u32x4){hi[0], hi[1], hi[2], hi[3]};
+      *reinterpret_cast<u32x4*>(h + chw + i0) = (u32x4){lo[0], lo[1], lo[2], lo[3]};
+    } else {
+      for (uint32_t i = i0; i < chw && i < i0 + 8; ++i) {
+        uint32_t h2, l2;
+        split_bf16x2(src[i], 0.f, h2, l2);
+        h[i] = (uint16_t)h2;
+        h[chw + i] = (uint16_t)l2;
+      }
+    }
   }
 }
 
@@ -233,11 +234,20 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
     const uint32_t rowel = (uint32_t)(p.h * W);
     if (g.xdma) {
       // x rows: copies of 64 dwords (lane l moves dword l) from one resource
-      // per image; a dword whose column is outside the image (or whose row or
-      // channel is) reads zero through its offset.  One resource per row
-      // instead cost ~20 scalar instructions per row and step (64-bit
-      // address arithmetic; measured bf16 60.6 -> 56.9 us)
+      // per image.  The row's byte offset is the scalar offset of the copy
+      // and the lane's column byte offset (kOob outside the image) is formed
+      // once per step, so a copy costs no vector instructions; a row outside
+      // the image (or a channel >= C) copies through a resource with no
+      // records and reads zero.  (Per-lane offsets formed per copy cost ~4
+      // vector instructions each: measured 2-5% slower.)
       const BufRes xres = make_buf(x + (int64_t)p.n * CHW, (uint32_t)(CHW * E));
+      const BufRes xnul = make_buf(x, 0u);
+      uint32_t colb[L::kXI];
+#pragma unroll
+      for (int part = 0; part < L::kXI; ++part) {
+        const int gw = p.w0 + xlo[part];
+        colb[part] = (unsigned)gw < (unsigned)W ? (uint32_t)gw * E : kOob;
+      }
 #pragma unroll
       for (int j = 0; j < (L::kXRows + NW - 1) / NW; ++j) {
         const int pr = wave + NW * j;
@@ -245,15 +255,15 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
         const int rr = pr >> 4, c = pr & 15;
         const int ch = cb * 16 + c, hh = p.h + (rr - r) * d;
         const bool ok = ch < C && (unsigned)hh < (unsigned)H;
-        const uint32_t rowel = (uint32_t)ch * (uint32_t)HW + (uint32_t)(hh * W);
+        const uint32_t soff = ok ? ((uint32_t)ch * (uint32_t)HW + (uint32_t)(hh * W)) * E : 0u;
+        const BufRes rs = ok ? xres : xnul;
 #pragma unroll
         for (int part = 0; part < L::kXI; ++part) {
           // the last copy ends at the row end (it may overlap the previous one)
           const int po = 64 * part < L::kXD - 64 ? 64 * part : L::kXD - 64;
-          const int gw = p.w0 + xlo[part];
-          const uint32_t off = (ok && (unsigned)gw < (unsigned)W) ? (rowel + (uint32_t)gw) * E : kOob;
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              xres, (__attribute__((address_space(3))) void*)(dstb + pr * L::kXSD + po), 4, off, 0, 0, 0);
+              rs, (__attribute__((address_space(3))) void*)(dstb + pr * L::kXSD + po), 4, colb[part],
+              soff, 0, 0);
         }
       }
     } else {
@@ -274,25 +284,32 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
     const BufRes yres = make_buf(yb + (int64_t)p.n * P * CHW, (uint32_t)(P * CHW * 2));
     const BufRes gres = make_buf(gbase + (int64_t)p.n * 4 * CHW, (uint32_t)(CHW * E));
     if (g.x4) {
-      // 1 KB copies: lane l moves one 16-byte chunk
+      // 1 KB copies: lane l moves one 16-byte chunk; the step's byte offset
+      // is the scalar offset, and lanes past the image's right edge are
+      // masked only in a partial column block
       const uint32_t ystep = (rowel + (uint32_t)p.w0) * 2u, gstep = (rowel + (uint32_t)p.w0) * E;
+      auto copies = [&](auto masked) {
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int ii = wave + NW * j;
-        if ((NY + NG) % NW != 0 && ii >= NY + NG) break;
-        const bool colok = p.w0 + cpc[j] < W;
-        if (ii < NY) {
-          const uint32_t off = colok ? cpo[j] + ystep : kOob;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              yres, (__attribute__((address_space(3))) void*)(dstb + L::kYOff + ii * 256), 16, off,
-              0, 0, 0);
-        } else {
-          const uint32_t off = colok ? cpo[j] + gstep : kOob;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              gres, (__attribute__((address_space(3))) void*)(dstb + L::kGOff + (ii - NY) * 256), 16,
-              off, 0, 0, 0);
+        for (int j = 0; j < NJ; ++j) {
+          const int ii = wave + NW * j;
+          if ((NY + NG) % NW != 0 && ii >= NY + NG) break;
+          uint32_t vo = cpo[j];
+          if constexpr (decltype(masked)::value) vo = p.w0 + cpc[j] < W ? vo : kOob;
+          if (ii < NY) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                yres, (__attribute__((address_space(3))) void*)(dstb + L::kYOff + ii * 256), 16, vo,
+                ystep, 0, 0);
+          } else {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                gres, (__attribute__((address_space(3))) void*)(dstb + L::kGOff + (ii - NY) * 256), 16,
+                vo, gstep, 0, 0);
+          }
         }
-      }
+      };
+      if (p.w0 + kWgTW <= W)
+        copies(std::false_type{});
+      else
+        copies(std::true_type{});
     } else {
       // element-wise through registers
       uint16_t* __restrict__ dy = reinterpret_cast<uint16_t*>(dstb + L::kYOff);
@@ -491,40 +508,65 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
 }
 
 // Fixed-order sum of the split partials, written in Conv2d parameter layout.
-template <typename T>
-__global__ __launch_bounds__(256) void gen_bwd_w_reduce_kernel(const float* __restrict__ pw,
+// A thread sums V consecutive input channels i of one (branch and tap,
+// channel) row over the splits in order; the bias partials follow, one per
+// thread.  Indices are 32-bit (the host bounds 3*K*K*C*(C+1) below 2^31).
+constexpr int kWgRedThreads = 256;
+template <typename T, int V>
+__global__ __launch_bounds__(kWgRedThreads) void gen_bwd_w_reduce_kernel(const float* __restrict__ pw,
                                                                  const float* __restrict__ pb,
                                                                  T* __restrict__ dw_out,
-                                                                 T* __restrict__ db_out, int C,
-                                                                 int KK, int splits) {
-  const int64_t per = (int64_t)3 * KK * C * C;
-  const int64_t perb = (int64_t)3 * KK * C;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx < per) {
-    float v = 0.f;
+                                                                 T* __restrict__ db_out,
+                                                                 uint32_t C, uint32_t KK,
+                                                                 int splits) {
+  const uint32_t per = 3u * KK * C * C, perb = 3u * KK * C;
+  const uint32_t nv = per / V;
+  const uint32_t item = blockIdx.x * (uint32_t)kWgRedThreads + threadIdx.x;
+  if (item < nv) {
+    const uint32_t idx = item * V;
+    float v[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) v[e] = 0.f;
 #pragma unroll 8
-    for (int s = 0; s < splits; ++s) v += pw[s * per + idx];
+    for (int s = 0; s < splits; ++s) {
+      const float* __restrict__ src = pw + (size_t)s * per + idx;
+      if constexpr (V == 4) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(src);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += a[e];
+      } else {
+        v[0] += src[0];
+      }
+    }
     // idx = (bt*C + c)*C + i  ->  row o = (b*C + c)*KK + t
-    const int64_t i = idx % C;
-    const int64_t c = (idx / C) % C;
-    const int64_t bt = idx / ((int64_t)C * C);
-    const int64_t b = bt / KK, t = bt % KK;
-    dw_out[((b * C + c) * KK + t) * C + i] = from_f<T>(v);
-  } else if (idx < per + perb) {
-    const int64_t j = idx - per;
+    const uint32_t row = idx / C, i = idx - row * C;
+    const uint32_t bt = row / C, c = row - bt * C;
+    const uint32_t b = bt / KK, t = bt - b * KK;
+    T* __restrict__ dst = dw_out + ((size_t)(b * C + c) * KK + t) * C + i;
+    if constexpr (V == 4) {
+      typedef T T4 __attribute__((ext_vector_type(4)));
+      *reinterpret_cast<T4*>(dst) =
+          (T4){from_f<T>(v[0]), from_f<T>(v[1]), from_f<T>(v[2]), from_f<T>(v[3])};
+    } else {
+      dst[0] = from_f<T>(v[0]);
+    }
+  } else if (item < nv + perb) {
+    const uint32_t j = item - nv;
     float v = 0.f;
 #pragma unroll 8
-    for (int s = 0; s < splits; ++s) v += pb[s * perb + j];
-    const int64_t c = j % C, bt = j / C;
-    const int64_t b = bt / KK, t = bt % KK;
+    for (int s = 0; s < splits; ++s) v += pb[(size_t)s * perb + j];
+    const uint32_t bt = j / C, c = j - bt * C;
+    const uint32_t b = bt / KK, t = bt - b * KK;
     db_out[(b * C + c) * KK + t] = from_f<T>(v);
   }
 }
 
 int launch_ysplit(const float* y, uint16_t* ys, int64_t chw, int64_t total, hipStream_t stream) {
   if (total == 0) return 0;
-  hipLaunchKernelGGL(gen_ysplit_kernel, dim3((unsigned)((total + 2047) / 2048)), dim3(256), 0,
-                     stream, y, ys, chw, total);
+  const int64_t n = total / chw;
+  const dim3 grid((unsigned)((chw + 2047) / 2048), (unsigned)(n < 65535 ? n : 65535));
+  hipLaunchKernelGGL(gen_ysplit_kernel, grid, dim3(256), 0, stream, y, ys, (uint32_t)chw,
+                     (uint32_t)n);
   return (int)hipGetLastError();
 }
 
@@ -624,6 +666,8 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
   const int esz = dtype == kF32 ? 4 : 2;
   // 32-bit buffer offsets inside one image's planes (fp32 y: two 2-byte planes)
   if (((c + 15) / 16) * 16 * h * w * 4 > 0x7fffffffLL) return kUnsupported;
+  // 32-bit indices of the split reduction
+  if ((int64_t)3 * kernel_size * kernel_size * c * (c + 1) > 0x7fffffffLL) return kUnsupported;
   WGradGeom g;
   wgrad_geom(g, n, c, h, w, gg.d0, gg.d1, gg.d2);
   const int64_t pbytes = wg_partial_bytes(g, c, kernel_size);
@@ -665,10 +709,22 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
                          ysrc, (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g);
       int e = (int)hipGetLastError();
       if (e != 0 || g.direct) return e;
-      const int64_t total = (int64_t)3 * KKc * c * c + (int64_t)3 * KKc * c;
-      hipLaunchKernelGGL((gen_bwd_w_reduce_kernel<T>), dim3((unsigned)((total + 255) / 256)),
-                         dim3(256), 0, stream, pw, pb, (T*)grad_weight, (T*)grad_bias, (int)c, KKc,
-                         g.splits);
+      const int64_t total_w = (int64_t)3 * KKc * c * c;
+      // four input channels per thread when the rows allow 16-byte partial
+      // loads and 4-element stores
+      const bool v4 = c % 4 == 0 && reinterpret_cast<uintptr_t>(pw) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(grad_weight) % (4 * sizeof(T)) == 0;
+      const int64_t items = (v4 ? total_w / 4 : total_w) + 3 * KKc * c;
+      if (v4)
+        hipLaunchKernelGGL((gen_bwd_w_reduce_kernel<T, 4>),
+                           dim3((unsigned)((items + kWgRedThreads - 1) / kWgRedThreads)),
+                           dim3(kWgRedThreads), 0, stream, pw, pb, (T*)grad_weight, (T*)grad_bias,
+                           (uint32_t)c, (uint32_t)KKc, g.splits);
+      else
+        hipLaunchKernelGGL((gen_bwd_w_reduce_kernel<T, 1>),
+                           dim3((unsigned)((items + kWgRedThreads - 1) / kWgRedThreads)),
+                           dim3(kWgRedThreads), 0, stream, pw, pb, (T*)grad_weight, (T*)grad_bias,
+                           (uint32_t)c, (uint32_t)KKc, g.splits);
       return (int)hipGetLastError();
     };
     return wg_with_mb(mb, [&](auto mbc) {
