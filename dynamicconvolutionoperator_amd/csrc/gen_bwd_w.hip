@@ -451,11 +451,19 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
     __syncthreads();
   }
 
-  // ---- deterministic reduction over the segments (fixed order) through LDS
+  // ---- deterministic reduction over the segments (fixed order) through LDS:
+  //      each segment's waves write their sums to the segment's own slice (one
+  //      round, one barrier), and the store loop adds the slices in segment
+  //      order -- the same sum, bit for bit, as accumulating segment by
+  //      segment into one slice, which took four rounds of LDS
+  //      read-modify-writes and barriers.  A thread stores 4 consecutive
+  //      input channels (16 bytes of fp32 partials).
   constexpr int NO = MB * 16;
   constexpr int RS = NO + 1;
-  float* __restrict__ red = reinterpret_cast<float*>(wsm);  // [KK][16 c][RS]
-  float* __restrict__ rb = red + KK * 16 * RS;              // [KK][segs][16 c]
+  constexpr int SL = KK * 16 * RS;                          // floats of one slice
+  static_assert(kWgSegs == 4, "the slice sum below adds four segments");
+  float* __restrict__ red = reinterpret_cast<float*>(wsm);  // [segs][KK][16 c][RS]
+  float* __restrict__ rb = red + kWgSegs * SL;              // [KK][segs][16 c]
   if (col16 == 0) {
 #pragma unroll
     for (int tt = 0; tt < TPH; ++tt) {
@@ -465,34 +473,48 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
         for (int e = 0; e < 4; ++e) rb[(t * kWgSegs + sg) * 16 + 4 * quad + e] = accb[tt][e];
     }
   }
-  for (int w = 0; w < kWgSegs; ++w) {
-    if (sg == w) {
 #pragma unroll
-      for (int tt = 0; tt < TPH; ++tt) {
-        const int t = th * TPH + tt;
-        if (t >= KK) break;
+  for (int tt = 0; tt < TPH; ++tt) {
+    const int t = th * TPH + tt;
+    if (t >= KK) break;
 #pragma unroll
-        for (int ib = 0; ib < MB; ++ib)
+    for (int ib = 0; ib < MB; ++ib)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float* dst = red + (t * 16 + 4 * quad + e) * RS + ib * 16 + col16;
-            *dst = (w == 0 ? 0.f : *dst) + acc[tt][ib][e];
-          }
-      }
-    }
-    __syncthreads();
+      for (int e = 0; e < 4; ++e)
+        red[sg * SL + (t * 16 + 4 * quad + e) * RS + ib * 16 + col16] = acc[tt][ib][e];
   }
-  for (int idx = tid; idx < KK * 16 * NO; idx += NT) {
-    const int t = idx / (16 * NO);
-    const int rem2 = idx - t * 16 * NO;
+  __syncthreads();
+  // this workgroup's rows: partial row ((split*3 + b)*KK + t)*C + ch, or
+  // grad_weight row (b*C + ch)*KK + t (32-bit offsets from these bases)
+  float* __restrict__ pwb = pw + ((int64_t)split * 3 + b) * KK * C * C;
+  T* __restrict__ dwb = dw_out + (int64_t)b * C * KK * C;
+  const bool v4 = C % 4 == 0 && reinterpret_cast<uintptr_t>(pw) % 16 == 0;
+  for (int idx = tid; idx < KK * 16 * NO / 4; idx += NT) {
+    const int q = 4 * idx;
+    const int t = q / (16 * NO);
+    const int rem2 = q - t * 16 * NO;
     const int c = rem2 / NO, i = rem2 - c * NO;
     const int ch = cb * 16 + c;
     if (ch >= C || i >= C) continue;
-    const float v = red[(t * 16 + c) * RS + i];
-    if (g.direct)
-      dw_out[((int64_t)(b * C + ch) * KK + t) * C + i] = from_f<T>(v);
-    else
-      pw[(((int64_t)split * 3 * KK + b * KK + t) * C + ch) * C + i] = v;
+    const float* __restrict__ sp = red + (t * 16 + c) * RS + i;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = ((sp[e] + sp[SL + e]) + sp[2 * SL + e]) + sp[3 * SL + e];
+    if (g.direct) {
+      T* __restrict__ dst = dwb + (uint32_t)((ch * KK + t) * C + i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (i + e < C) dst[e] = from_f<T>(v[e]);
+    } else {
+      float* __restrict__ dst = pwb + (uint32_t)((t * C + ch) * C + i);
+      if (v4) {
+        *reinterpret_cast<f32x4*>(dst) = (f32x4){v[0], v[1], v[2], v[3]};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (i + e < C) dst[e] = v[e];
+      }
+    }
   }
   for (int idx = tid; idx < KK * 16; idx += NT) {
     const int t = idx >> 4, c = idx & 15;
@@ -694,7 +716,7 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
       constexpr int KKc = KS * KS;
       typedef WgLds<T, KS, MB> L;
       const size_t stage = (size_t)2 * L::kBuf * 4;
-      const size_t red = (size_t)(KKc * 16 * (MB * 16 + 1) + KKc * kWgSegs * 16) * sizeof(float);
+      const size_t red = (size_t)(kWgSegs * KKc * 16 * (MB * 16 + 1) + KKc * kWgSegs * 16) * sizeof(float);
       const size_t lds = stage > red ? stage : red;
       const dim3 grid((unsigned)(g.splits * 3 * g.cblocks));
       if (lds > 64 * 1024) {
