@@ -18,6 +18,7 @@ SHAPES = [
     (2, 24, 15, 17),  # non-aligned channels and width (scalar path)
     (1, 16, 16, 32),  # W % 4 == 0 (vector path), C = 16
     (1, 64, 20, 64),  # C = 64, several tiles
+    (1, 10, 12, 40),  # C % 4 != 0: element-wise tails of the weight-gradient stores
 ]
 
 
@@ -244,6 +245,8 @@ def test_generator_inference_has_no_autograd_graph():
     [
         (2, 32, 40, 64),  # 80 steps (row segments of 128 columns) -> 20 splits of fp32 partials
         (1, 24, 4, 17),   # 4 steps -> one split writes the gradients directly
+        (1, 10, 24, 40),  # C % 4 != 0, 24 steps -> 6 splits, scalar split reduction
+        (1, 10, 3, 20),   # C % 4 != 0, 3 steps -> direct write
     ],
 )
 def test_generator_weight_gradient_splits(shape):
