@@ -1,6 +1,6 @@
 """Oracle for the DDPM hot path.
 
-THIS PACKAGE IS TEST INFRASTRUCTURE. It is the checker, never the product:
+THIS PACKAGE IS TEST INFRASTRUCTURE. It is what the product is tested against, never the product:
 only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import it.  The product package
 (``dynamicconvolutionoperator_amd``) never imports anything from here, and its

@@ -1,8 +1,8 @@
 /*
  * Loop-level double-precision restatement of the DDPM hot path.
  *
- * Test infrastructure only: the checker for the HIP kernels and a second,
- * independent restatement that pins the torch Unfold oracle.  Nothing in the
+ * Test infrastructure only: the reference the HIP kernels are tested against,
+ * and a second, independent restatement that pins the torch Unfold oracle.  Nothing in the
  * product library links or loads this file.
  *
  * Layouts (all contiguous, NCHW-style):
