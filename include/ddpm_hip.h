@@ -154,14 +154,18 @@ int ddpm_gen_bwd_y(const void* x, const void* weight, const void* grad_out, void
                    int64_t w, int kernel_size, int d0, int d1, int d2, int dtype,
                    hipStream_t stream);
 
-/* Bytes of fp32 workspace ddpm_gen_bwd_w needs for its split partials
- * (0 when it writes grad_weight / grad_bias directly).
+/* Bytes of workspace ddpm_gen_bwd_w needs: its fp32 split partials (none
+ * when one split writes grad_weight / grad_bias directly), then, for fp32
+ * inputs, the bf16 hi / lo planes of y (the query covers fp32; 2-byte dtypes
+ * use only the partials).
  * Replaces the partial-buffer sizing of _GeneratorDynamicCat.backward (_triton_kernels.py:1001-1017). */
 int64_t ddpm_gen_bwd_w_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size);
 
 /* grad_weight[o,i] = sum_p dK[o,p] y[i,p], grad_bias[o] = sum_p dK[o,p]; split
- * over <= 16 token ranges into fp32 partials in `workspace`, then summed in
- * a fixed order (deterministic).
+ * over as many token ranges as give every CU one workgroup (21 at C = 64)
+ * into fp32 partials in `workspace`, then summed in a fixed order
+ * (deterministic).  DDPM_STATUS_UNSUPPORTED for a dilation above 8 or
+ * 3*K*K*C*(C+1) >= 2^31.
  * Replaces _generator_dynamic_cat_bwd_weight_partial + _bwd_weight_reduce
  * (_triton_kernels.py:626-811, launched at :973-1053). */
 int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out, void* grad_weight,
