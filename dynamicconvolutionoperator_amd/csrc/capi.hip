@@ -1,5 +1,30 @@
-// Library-level C-ABI helpers: status strings, ABI version, support queries.
+// Library-level C-ABI helpers: status strings, ABI version, support queries,
+// and the host-side launch helper shared by every entry point.
 #include "gen_common.h"
+
+#include <map>
+#include <mutex>
+#include <utility>
+
+namespace ddpm {
+
+int allow_dynamic_lds(const void* fn, size_t bytes) {
+  if (bytes <= 64 * 1024) return 0;  // the default limit
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, size_t> granted;  // (kernel, device) -> bytes
+  std::lock_guard<std::mutex> lock(mu);
+  size_t& have = granted[std::make_pair(fn, dev)];
+  if (have >= bytes) return 0;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e != hipSuccess) return (int)e;
+  have = bytes;
+  return 0;
+}
+
+}  // namespace ddpm
 
 using namespace ddpm;
 
@@ -14,7 +39,7 @@ extern "C" const char* ddpm_status_string(int code) {
     case kUnsupported:
       return "shape or kernel size not supported by this kernel";
     case kWorkspaceTooSmall:
-      return "workspace missing or smaller than ddpm_gen_bwd_w_workspace_bytes()";
+      return "workspace missing or smaller than the entry point's *_workspace_bytes() query";
     default:
       return hipGetErrorString((hipError_t)code);
   }

@@ -270,4 +270,10 @@ __device__ __forceinline__ int dil_of(int b, int d0, int d1, int d2) {
   return b == 0 ? d0 : (b == 1 ? d1 : d2);
 }
 
+// Host: lets kernel `fn` launch with `bytes` of dynamic LDS (up to the 160 KB
+// of a gfx950 CU) on the current device.  hipFuncSetAttribute runs only the
+// first time a (kernel, device) pair needs more than the limit already set,
+// not on every launch.  Returns 0 or the hipError_t of the attribute call.
+int allow_dynamic_lds(const void* fn, size_t bytes);
+
 }  // namespace ddpm

@@ -593,11 +593,8 @@ enum class FilterOp { kFwd, kBwdX, kBwdK };
 
 template <typename Kern, typename... Args>
 int launch_kernel(Kern kern, const FilterGeom& g, size_t lds, hipStream_t stream, Args... args) {
-  if (lds > 64 * 1024) {
-    const hipError_t ae = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (ae != hipSuccess) return (int)ae;
-  }
+  const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
+  if (ae != 0) return ae;
   hipLaunchKernelGGL(kern, dim3((unsigned)((int64_t)g.tiles * g.N * g.C)), dim3(kFilterThreads), lds,
                      stream, args...);
   return (int)hipGetLastError();

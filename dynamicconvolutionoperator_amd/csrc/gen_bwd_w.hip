@@ -719,13 +719,9 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
       const size_t red = (size_t)(kWgSegs * KKc * 16 * (MB * 16 + 1) + KKc * kWgSegs * 16) * sizeof(float);
       const size_t lds = stage > red ? stage : red;
       const dim3 grid((unsigned)(g.splits * 3 * g.cblocks));
-      if (lds > 64 * 1024) {
-        // up to 160 KB of LDS per workgroup on gfx950
-        const hipError_t ae = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&gen_bwd_w_partial_kernel<T, KS, MB>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (ae != hipSuccess) return (int)ae;
-      }
+      const int ae = allow_dynamic_lds(
+          reinterpret_cast<const void*>(&gen_bwd_w_partial_kernel<T, KS, MB>), lds);
+      if (ae != 0) return ae;
       hipLaunchKernelGGL((gen_bwd_w_partial_kernel<T, KS, MB>), grid,
                          dim3(64 * kWgSegs * WgTaps<KS>::kGroups), lds, stream, (const T*)x,
                          ysrc, (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g);

@@ -175,12 +175,8 @@ extern "C" int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bia
   return xt_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
     auto launch = [&](auto kern) {
-      if (lds > 64 * 1024) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)lds);
-        if (e != hipSuccess) return (int)e;
-      }
+      const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
+      if (ae != 0) return ae;
       hipLaunchKernelGGL(kern, dim3((unsigned)((int64_t)g.N * g.tiles * g.cblocks)),
                          dim3(kGtThreads), lds, stream, (const T*)grad_out, (const T*)y,
                          (const T*)weight, (const T*)bias, part, g);

@@ -370,12 +370,9 @@ extern "C" int ddpm_gen_bwd_y(const void* x, const void* weight, const void* gra
         int e = (int)hipGetLastError();
         if (e != 0) return e;
         const size_t lds = (size_t)2 * L::kBuf * 4;
-        if (lds > 64 * 1024) {
-          const hipError_t ae = hipFuncSetAttribute(
-              reinterpret_cast<const void*>(&gen_bwd_y_kernel<T, KS, MB>),
-              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-          if (ae != hipSuccess) return (int)ae;
-        }
+        const int ae =
+            allow_dynamic_lds(reinterpret_cast<const void*>(&gen_bwd_y_kernel<T, KS, MB>), lds);
+        if (ae != 0) return ae;
         hipLaunchKernelGGL((gen_bwd_y_kernel<T, KS, MB>), dim3((unsigned)tiles), dim3(kYtThreads), lds,
                            stream, (const T*)x, (const uint32_t*)workspace, (const T*)grad_out,
                            (T*)grad_y, g);

@@ -952,6 +952,26 @@ int64_t gy_part_bytes(const GyGeom& g) {
 
 using namespace ddpm;
 
+// 1 when ddpm_gen_kernels and ddpm_gen_kernels_bwd_w take this shape and
+// dtype: their 32-bit buffer offsets cover one image's planes (the 3CK^2
+// generated planes, and for fp32 the two 2-byte planes of y) and their grids
+// stay below 2^31 workgroups.  Host-only; the same bounds the entry points
+// apply before launching.
+extern "C" int ddpm_gen_kernels_supported(int64_t n, int64_t c, int64_t h, int64_t w,
+                                          int kernel_size, int dtype) {
+  if (dtype < kF32 || dtype > kF16) return 0;
+  if (n < 0 || c < 1 || h < 0 || w < 0 || c > kGkMaxC) return 0;
+  if (kernel_size < 1 || kernel_size % 2 == 0) return 0;
+  const int64_t esz = dtype == kF32 ? 4 : 2;
+  const int64_t hw = h * w, o = 3 * c * kernel_size * kernel_size;
+  if (o * hw * esz > 0x7fffffffLL || c * hw * esz > 0x7fffffffLL || o * c * esz > 0x7fffffffLL)
+    return 0;
+  if (2 * c * hw * 2 > 0x7fffffffLL || o * c > 0x7fffffffLL) return 0;
+  if (n * ((hw + kGwStep - 1) / kGwStep) > 0x7fffffffLL) return 0;
+  if (n * ((hw + kGkTP - 1) / kGkTP) * ((o + 15) / 16) > 0x7fffffffLL) return 0;
+  return 1;
+}
+
 extern "C" int ddpm_gen_kernels(const void* y, const void* weight, const void* bias, void* kernels,
                                 int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size,
                                 int dtype, hipStream_t stream) {
@@ -1065,11 +1085,8 @@ extern "C" int ddpm_gen_kernels_bwd_w(const void* y, const void* grad_kernels, v
     using T = decltype(tag);
     auto launch = [&](auto kern, size_t shm) {
       if (g.splits > 0) {
-        if (shm > 64 * 1024) {
-          const hipError_t ae = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-          if (ae != hipSuccess) return (int)ae;
-        }
+        const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), shm);
+        if (ae != 0) return ae;
         hipLaunchKernelGGL(kern, dim3((unsigned)(g.row_tiles * g.splits)), dim3(64 * kGwWaves), shm,
                            stream, (const T*)grad_kernels, yb, pw, pb, (T*)grad_weight,
                            (T*)grad_bias, g);
@@ -1163,11 +1180,8 @@ extern "C" int ddpm_gen_kernels_bwd_y(const void* weight, const void* grad_kerne
       constexpr int MB = decltype(mbc)::value;
       const size_t shm = (size_t)2 * GyLds<T, MB>::BUF;
       auto kern = gk_bwd_y_kernel<T, MB>;
-      if (shm > 64 * 1024) {
-        const hipError_t ae = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-        if (ae != hipSuccess) return (int)ae;
-      }
+      const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), shm);
+      if (ae != 0) return ae;
       hipLaunchKernelGGL(kern, dim3((unsigned)(g.tiles * g.splits)), dim3(256), shm, stream,
                          (const T*)grad_kernels, (const uint32_t*)pk, part, (T*)grad_y, g);
       int e2 = (int)hipGetLastError();

@@ -102,7 +102,7 @@ class DDPM(nn.Module):
     def _route(self, x: torch.Tensor, y: torch.Tensor, gen_supported) -> str:
         """Returns "fused" or "materialized" with the reference's rules
         (triton_impl.py:311-329); shapes outside the fused kernels' coverage
-        (K > 3 or C > 64) use the materialized route."""
+        (``ops.generator_supported``) use the materialized route."""
         tokens = x.shape[0] * x.shape[2] * x.shape[3]
         requested = self.fused_generator_training
         if requested is None:
@@ -117,7 +117,7 @@ class DDPM(nn.Module):
             and x.dtype == y.dtype == self.generator.weight.dtype
             and bias is not None
             and bias.dtype == x.dtype
-            and gen_supported(self.dim, self.kernel_size, self.dilations)
+            and gen_supported(self.dim, self.kernel_size, self.dilations, x.shape, x.dtype)
         )
         return "fused" if can_fuse else "materialized"
 

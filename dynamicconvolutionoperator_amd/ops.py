@@ -133,10 +133,23 @@ def fused_dynamic_cat(x, kernels, kernel_size, dilations):
 # ---------------------------------------------------------------------------
 # Fused generator path
 # ---------------------------------------------------------------------------
-def generator_supported(channels: int, kernel_size: int, dilations=(1, 3, 5)) -> bool:
-    """Whether the fused generator kernels handle this shape (K in {1,3}, C <= 64,
-    halo tile within 64 KB of LDS)."""
-    return bool(_lib.load().ddpm_gen_supported(int(channels), int(kernel_size), int(max(dilations))))
+# The fused kernels address one image's [C][H][W] planes with 32-bit byte offsets.
+_FUSED_MAX_IMAGE_BYTES = 2**31 - 1
+
+
+def generator_supported(channels: int, kernel_size: int, dilations=(1, 3, 5), shape=None,
+                        dtype=None) -> bool:
+    """Whether the fused generator kernels handle this configuration
+    (``ddpm_gen_supported``: channel count, K in {1, 3}, largest dilation) and,
+    given ``shape`` ``[N, C, H, W]`` and ``dtype``, whether one image's planes
+    fit their 32-bit offsets."""
+    if not _lib.load().ddpm_gen_supported(int(channels), int(kernel_size), int(max(dilations))):
+        return False
+    if shape is not None:
+        esize = torch.empty((), dtype=dtype if dtype is not None else torch.float32).element_size()
+        if int(shape[1]) * int(shape[2]) * int(shape[3]) * esize > _FUSED_MAX_IMAGE_BYTES:
+            return False
+    return True
 
 
 def _check_generator_inputs(x, y, weight, bias, k: int) -> None:
@@ -243,14 +256,21 @@ GENERATOR_KERNELS_MAX_CHANNELS = 128  # ddpm_gen_kernels keeps y's K operand in 
 
 
 def generator_kernels_supported(y, weight, bias) -> bool:
-    """Whether ``ddpm_gen_kernels`` computes this generator convolution: one
-    dtype for y, weight and bias, and at most 128 channels."""
-    return (
-        bias is not None
-        and y.dtype in _DTYPES
-        and y.dtype == weight.dtype == bias.dtype
-        and y.shape[1] <= GENERATOR_KERNELS_MAX_CHANNELS
-    )
+    """Whether ``ddpm_gen_kernels`` (and its backward) computes this generator
+    convolution: one dtype for y, weight and bias, at most 128 channels, and
+    one image's generated planes within the kernels' 32-bit offsets
+    (``ddpm_gen_kernels_supported``)."""
+    if bias is None or y.dtype not in _DTYPES or not (y.dtype == weight.dtype == bias.dtype):
+        return False
+    if y.ndim != 4 or y.shape[1] > GENERATOR_KERNELS_MAX_CHANNELS:
+        return False
+    o, c = weight.shape[0], y.shape[1]
+    k2, rem = divmod(o, 3 * c)
+    k = int(round(k2 ** 0.5))
+    if rem or k * k != k2:
+        return False
+    n, _, h, w = y.shape
+    return bool(_lib.load().ddpm_gen_kernels_supported(n, c, h, w, k, _DTYPES[y.dtype]))
 
 
 class _GeneratorKernels(torch.autograd.Function):
@@ -353,12 +373,13 @@ def fused_generator_dynamic_cat(x, y, weight, bias, kernel_size, dilations):
 
     Uses the autograd Function when grad is enabled and any input requires
     grad, else a single forward launch.  Shapes outside the fused kernels'
-    coverage (K > 3 or C > 64) run the generator as a 1x1 convolution and the
-    HIP materialized filter, with the same result and autograd outputs.
+    coverage (:func:`generator_supported`) run the generator as a 1x1
+    convolution and the HIP materialized filter, with the same result and
+    autograd outputs.
     """
     k = _check_kernel_size(kernel_size)
     dil = _check_dilations(dilations)
-    if not generator_supported(x.shape[1], k, dil):
+    if not generator_supported(x.shape[1], k, dil, x.shape, x.dtype):
         return _materialized_generator_dynamic_cat(x, y, weight, bias, k, dil)
     if torch.is_grad_enabled() and any(t.requires_grad for t in (x, y, weight, bias)):
         return _GeneratorDynamicCat.apply(x, y, weight, bias, k, dil)

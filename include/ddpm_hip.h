@@ -51,6 +51,14 @@ const char* ddpm_status_string(int code);
  * (ddpm_filter_*), with identical results. */
 int ddpm_gen_supported(int64_t c, int kernel_size, int max_dilation);
 
+/* 1 when ddpm_gen_kernels and ddpm_gen_kernels_bwd_w accept this shape and
+ * dtype (c <= 128, one image's generated planes within 2^31 - 1 bytes, grids
+ * below 2^31 workgroups), else 0; host-only.  Callers compute other shapes
+ * with a library convolution.  Part of the routing of the reference's
+ * materialized path (triton_impl.py:340-347). */
+int ddpm_gen_kernels_supported(int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size,
+                               int dtype);
+
 /* The generator's 1x1 convolution on the materialized route:
  * kernels[n][o][p] = sum_i weight[o][i] * y[n][i][p] + bias[o] for
  * o < 3*c*k*k, rounded once to `dtype`, written in the [n][3][c][k*k][h][w]
