@@ -41,6 +41,8 @@ SIGNATURES: dict[str, tuple[list, type]] = {
     "ddpm_gen_bwd_x": ([_P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
     "ddpm_gen_bwd_y_workspace_bytes": ([_L, _I], _L),
     "ddpm_gen_bwd_y": ([_P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
+    "ddpm_gen_bwd_y_noalloc": ([_P, _P, _P, _P, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
+    "ddpm_gen_bwd_y_noalloc_scratch_bytes": ([], _L),
     "ddpm_gen_bwd_w_workspace_bytes": ([_L, _L, _L, _L, _I], _L),
     "ddpm_gen_bwd_w": ([_P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
 }

@@ -40,6 +40,9 @@ extern "C" const char* ddpm_status_string(int code) {
       return "shape or kernel size not supported by this kernel";
     case kWorkspaceTooSmall:
       return "workspace missing or smaller than the entry point's *_workspace_bytes() query";
+    case kScratchTooSmall:
+      return "shape needs more scratch than the no-allocation entry point's fixed device buffer "
+             "(ddpm_gen_bwd_y_noalloc_scratch_bytes())";
     default:
       return hipGetErrorString((hipError_t)code);
   }

@@ -31,6 +31,7 @@ enum Status : int {
   kBadArgument = 10001,
   kUnsupported = 10002,
   kWorkspaceTooSmall = 10003,
+  kScratchTooSmall = 10004,  // shape exceeds a no-allocation entry point's fixed scratch
 };
 
 template <typename T>

@@ -26,6 +26,9 @@
 //     products (hi*hi + hi*lo + lo*hi).
 
 #include "gen_common.h"
+
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 namespace ddpm {
@@ -316,6 +319,70 @@ int64_t yt_pack_bytes(int64_t c, int k, int dtype) {
   return 3 * nc32 * (int64_t)k * k * mb * (dtype == kF32 ? 2 : 1) * 64 * 16;
 }
 
+// Validates the arguments of both dY entry points; kOk, an error, or
+// kOk with `empty` set when there is nothing to compute.
+int yt_check(const void* x, const void* weight, const void* grad_out, void* grad_y, int64_t n,
+             int64_t c, int64_t h, int64_t w, int kernel_size, int d0, int d1, int d2, int dtype,
+             GenGeom& gg, bool& empty) {
+  empty = false;
+  if (dtype < kF32 || dtype > kF16) return kBadArgument;
+  int st = gen_make_geom(gg, n, c, h, w, kernel_size, d0, d1, d2);
+  if (st != kOk) return st;
+  if (n == 0 || c == 0 || h == 0 || w == 0) {
+    empty = true;
+    return kOk;
+  }
+  if (!x || !weight || !grad_out || !grad_y) return kBadArgument;
+  if (gg.d0 > kYtMaxDil || gg.d1 > kYtMaxDil || gg.d2 > kYtMaxDil) return kUnsupported;
+  // 32-bit buffer offsets inside one image's [C][H][W] planes
+  if (c * h * w * (dtype == kF32 ? 4 : 2) > 0x7fffffffLL) return kUnsupported;
+  if (n * h * ((w + kYtTW - 1) / kYtTW) > 0x7fffffffLL) return kUnsupported;
+  return kOk;
+}
+
+// Packs the weight into `packed` and launches the dY kernel (arguments
+// already validated by yt_check; `packed` holds yt_pack_bytes bytes).
+int yt_launch(const void* x, const void* weight, const void* grad_out, void* grad_y, void* packed,
+              int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size, const GenGeom& gg,
+              int dtype, hipStream_t stream);
+
+}  // namespace
+
+// Scratch of the no-allocation entry point: the packed weight, at most
+// kYtScratchBytes (enough for every channel count and kernel size the fused
+// kernels accept).  Each device holds its own copy for the life of the
+// process; host code reaches it only through the address that
+// hipGetSymbolAddress returns for the current device.
+constexpr int64_t kYtScratchBytes = (int64_t)2 << 20;
+static __device__ __align__(256) unsigned char scratch[kYtScratchBytes];
+
+namespace {
+
+constexpr int kYtMaxDevices = 64;
+std::atomic<void*> g_scratch[kYtMaxDevices];
+std::mutex g_scratch_mu;
+
+// This device's address of `scratch`, looked up once per device.
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kYtMaxDevices) return kUnsupported;
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return (int)e;
+      if (p == nullptr) return (int)hipErrorInvalidSymbol;
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return kOk;
+}
+
 }  // namespace
 }  // namespace ddpm
 
@@ -330,17 +397,42 @@ extern "C" int ddpm_gen_bwd_y(const void* x, const void* weight, const void* gra
                               void* grad_y, void* workspace, int64_t workspace_bytes, int64_t n,
                               int64_t c, int64_t h, int64_t w, int kernel_size, int d0, int d1,
                               int d2, int dtype, hipStream_t stream) {
-  if (dtype < kF32 || dtype > kF16) return kBadArgument;
   GenGeom gg;
-  int st = gen_make_geom(gg, n, c, h, w, kernel_size, d0, d1, d2);
-  if (st != kOk) return st;
-  if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
-  if (!x || !weight || !grad_out || !grad_y) return kBadArgument;
-  if (gg.d0 > kYtMaxDil || gg.d1 > kYtMaxDil || gg.d2 > kYtMaxDil) return kUnsupported;
-  // 32-bit buffer offsets inside one image's [C][H][W] planes
-  if (c * h * w * (dtype == kF32 ? 4 : 2) > 0x7fffffffLL) return kUnsupported;
+  bool empty;
+  const int st =
+      yt_check(x, weight, grad_out, grad_y, n, c, h, w, kernel_size, d0, d1, d2, dtype, gg, empty);
+  if (st != kOk || empty) return st;
   const int64_t need = yt_pack_bytes(c, kernel_size, dtype);
   if (!workspace || workspace_bytes < need) return kWorkspaceTooSmall;
+  return yt_launch(x, weight, grad_out, grad_y, workspace, n, c, h, w, kernel_size, gg, dtype,
+                   stream);
+}
+
+extern "C" int ddpm_gen_bwd_y_noalloc(const void* x, const void* weight, const void* grad_out,
+                                      void* grad_y, int64_t n, int64_t c, int64_t h, int64_t w,
+                                      int kernel_size, int d0, int d1, int d2, int dtype,
+                                      hipStream_t stream) {
+  GenGeom gg;
+  bool empty;
+  int st =
+      yt_check(x, weight, grad_out, grad_y, n, c, h, w, kernel_size, d0, d1, d2, dtype, gg, empty);
+  if (st != kOk || empty) return st;
+  if (yt_pack_bytes(c, kernel_size, dtype) > kYtScratchBytes) return kScratchTooSmall;
+  void* packed = nullptr;
+  st = scratch_address(&packed);
+  if (st != kOk) return st;
+  return yt_launch(x, weight, grad_out, grad_y, packed, n, c, h, w, kernel_size, gg, dtype, stream);
+}
+
+extern "C" int64_t ddpm_gen_bwd_y_noalloc_scratch_bytes(void) { return kYtScratchBytes; }
+
+namespace ddpm {
+namespace {
+
+int yt_launch(const void* x, const void* weight, const void* grad_out, void* grad_y, void* packed,
+              int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size, const GenGeom& gg,
+              int dtype, hipStream_t stream) {
+  void* workspace = packed;
   YGeom g;
   g.N = (int)n;
   g.C = (int)c;
@@ -351,11 +443,8 @@ extern "C" int ddpm_gen_bwd_y(const void* x, const void* weight, const void* gra
   g.d2 = gg.d2;
   g.col_tiles = (int)((w + kYtTW - 1) / kYtTW);
   g.nc32 = (int)((c + 31) / 32);
-  const size_t esz = dtype == kF32 ? 4 : 2;
   g.x4 = (w % 8 == 0) && ((uintptr_t)x % 16 == 0);
-  (void)esz;
-  const int64_t tiles = n * h * g.col_tiles;
-  if (tiles > 0x7fffffffLL) return kUnsupported;
+  const int64_t tiles = n * h * g.col_tiles;  // below 2^31 (yt_check)
   const int mb = (int)((c + 15) / 16);
   return yt_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
@@ -384,3 +473,6 @@ extern "C" int ddpm_gen_bwd_y(const void* x, const void* weight, const void* gra
     });
   });
 }
+
+}  // namespace
+}  // namespace ddpm

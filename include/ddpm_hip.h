@@ -32,6 +32,7 @@ extern "C" {
 #define DDPM_STATUS_BAD_ARGUMENT 10001
 #define DDPM_STATUS_UNSUPPORTED 10002
 #define DDPM_STATUS_WORKSPACE_TOO_SMALL 10003
+#define DDPM_STATUS_SCRATCH_TOO_SMALL 10004
 
 #define DDPM_DTYPE_F32 0
 #define DDPM_DTYPE_BF16 1
@@ -161,6 +162,22 @@ int ddpm_gen_bwd_y(const void* x, const void* weight, const void* grad_out, void
                    void* workspace, int64_t workspace_bytes, int64_t n, int64_t c, int64_t h,
                    int64_t w, int kernel_size, int d0, int d1, int d2, int dtype,
                    hipStream_t stream);
+
+/* ddpm_gen_bwd_y without a workspace argument: allocates nothing.
+ * No counterpart in the reference; it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The packed weight goes to a fixed
+ * device buffer of ddpm_gen_bwd_y_noalloc_scratch_bytes() bytes (2 MiB,
+ * enough for every shape the fused kernels accept) that the library holds on
+ * each device it runs on until the process ends; a shape that needs more
+ * returns DDPM_STATUS_SCRATCH_TOO_SMALL.  Every call on one device shares
+ * that buffer, so calls that overlap on one device (different streams, or
+ * other host threads) race; calls in one stream's order do not.  Same
+ * arguments otherwise, and bit-identical results to ddpm_gen_bwd_y. */
+int ddpm_gen_bwd_y_noalloc(const void* x, const void* weight, const void* grad_out, void* grad_y,
+                           int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size, int d0,
+                           int d1, int d2, int dtype, hipStream_t stream);
+int64_t ddpm_gen_bwd_y_noalloc_scratch_bytes(void);
 
 /* Bytes of workspace ddpm_gen_bwd_w needs: its fp32 split partials (none
  * when one split writes grad_weight / grad_bias directly), then, for fp32
