@@ -6,15 +6,29 @@ drop-in DDPM module -- forward and backward of ``module(x, y).square().mean()``
 -- at B=1, C=64, K=3, H=W=256, fp32, synthetic N(0,1) inputs and seeded
 default-init weights.  This is the configuration on which the reference
 quotes its absolute fused training time (3.66 ms on an RTX 5090,
-README.md:161-162).
+README.md:161-162).  The timed loop runs the module as a user would, with no
+instrumentation.
 
-Also reported on the same line: bf16 training, fused inference (fp32/bf16),
-the materialized dynamic filter's HBM bandwidth at 256x256 (the
-"dyn-filter HBM TB/s" part of the metric), peak temporary memory of the fused
-step vs the Unfold route, the Unfold route's GPU step time, a roofline entry
-for the dominant HIP kernel of the step (HIP events around each launch on its
-stream, inside the timed region) and a CPU baseline (the Unfold oracle
-restatement timed on the host cores).
+Also reported on the same line (``extra``):
+  * bf16 training, fused inference (fp32 / bf16) at 256x256;
+  * a per-entry-point breakdown of the fp32 and bf16 steps (HIP events around
+    each C-ABI launch on its stream, in a separate pass after the headline
+    loop) and the ``roofline`` entry of the dominant HIP kernel;
+  * the dynamic filter's HBM bandwidth (forward, dX, dK; fp32 and bf16, K=3
+    256x256, rotating buffer sets so repeats do not run out of the MALL);
+  * 128x128 C=64 K=3 fp32 inference: filter-only ms and GB/s and fused
+    end-to-end ms (gpu_bench.py:94-118);
+  * K=5 128x128 C=64 bf16 on the materialized route: inference and
+    forward+backward ms (gpu_bench.py:265-345);
+  * peak temporary memory of the fused and Unfold training steps, each route
+    in its own child process started before this process uses the GPU, with
+    gradients released before the baseline is read (gpu_memory_bench.py:47-76);
+  * the Unfold route's GPU step time.
+``cpu_baseline``: the reference's CPU path, timed on this host's cores in
+the same run -- the CPU branch of the drop-in module (streaming with
+per-tile checkpoint at fp32, triton_impl.py:169-244,381-391; Unfold training
+at bf16, :373-376) and the Unfold oracle, warm-up 3 / repeats 20
+(bench.py:138-165 of the reference), each leg capped in time.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10]
 """
@@ -50,6 +64,11 @@ def parse_args():
     )
     p.add_argument("--dtype", choices=("f32", "bf16"), default="f32", help="with --kernel")
     p.add_argument("--reps", type=int, default=3, help="launches per entry point with --kernel")
+    p.add_argument("--peak-mem", nargs=2, metavar=("ROUTE", "DTYPE"),
+                   help="child mode: peak temporary memory of one training step of ROUTE "
+                   "(fused|unfold) in DTYPE (float32|bfloat16); prints one JSON line")
+    p.add_argument("--cpu-budget", type=float, default=12.0,
+                   help="seconds per CPU-baseline leg at most (after its warm-up)")
     return p.parse_args()
 
 
@@ -186,35 +205,56 @@ def load_traffic(kernel_entry, dtype_name):
 
 
 # --------------------------------------------------------------------------- measurements
-def filter_bandwidth(dtype, repeats=30):
-    """Materialized dynamic filter forward at 256x256, rotating two buffer sets
-    (2 x 537 MB for fp32) so repeats do not run out of the 256 MB MALL."""
+def filter_op_bandwidth(op, dtype, h=H, w=W, k=K, sets=2, repeats=30):
+    """One materialized-filter entry point (``ddpm_filter_fwd`` / ``_bwd_x`` /
+    ``_bwd_k``) through the C-ABI, HIP events around each launch, rotating
+    `sets` input sets so that repeats do not run out of the 256 MB MALL.
+    Algorithmic bytes: (3K^2+5)E (forward, dX) and (3K^2+4)E (dK) elements."""
+    import ctypes
+
     import torch
 
-    from dynamicconvolutionoperator_amd import ops
+    from dynamicconvolutionoperator_amd import _lib
 
-    sets = []
-    for s in range(2):
-        g = torch.Generator(device="cuda").manual_seed(10 + s)
-        x = torch.randn(B, C, H, W, device="cuda", dtype=dtype, generator=g)
-        k = torch.randn(B, 3, C, K * K, H, W, device="cuda", dtype=dtype, generator=g)
-        sets.append((x, k))
-    with torch.inference_mode():
-        for i in range(4):
-            ops.fused_dynamic_cat(*sets[i % 2], K, DIL)
-        torch.cuda.synchronize()
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(repeats)]
-        for i in range(repeats):
-            ev[i][0].record()
-            ops.fused_dynamic_cat(*sets[i % 2], K, DIL)
-            ev[i][1].record()
-        torch.cuda.synchronize()
-    ms = sum(s.elapsed_time(e) for s, e in ev) / repeats
+    lib = _lib.load()
+    code = 0 if dtype == torch.float32 else 1
     esize = torch.empty((), dtype=dtype).element_size()
-    nbytes = (3 * K * K + 5) * B * C * H * W * esize
-    del sets
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    bufs = []
+    for s_ in range(sets):
+        g = torch.Generator(device="cuda").manual_seed(10 + s_)
+        rnd = lambda *shape: torch.randn(*shape, device="cuda", generator=g).to(dtype)  # noqa: E731
+        x = rnd(B, C, h, w)
+        kern = rnd(B, 3, C, k * k, h, w)
+        go = rnd(B, 4 * C, h, w)
+        if op == "ddpm_filter_fwd":
+            a, bb, o = x, kern, torch.empty(B, 4 * C, h, w, device="cuda", dtype=dtype)
+        elif op == "ddpm_filter_bwd_x":
+            a, bb, o = go, kern, torch.empty_like(x)
+        else:
+            a, bb, o = x, go, torch.empty_like(kern)
+        bufs.append((a, bb, o))
+    fn = getattr(lib, op)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    call = lambda i: fn(ptr(bufs[i][0]), ptr(bufs[i][1]), ptr(bufs[i][2]), B, C, h, w, k, *DIL,  # noqa: E731
+                        code, code, s)
+    for i in range(2 * sets):
+        rc = call(i % sets)
+        if rc:
+            raise RuntimeError(f"{op} failed with status {rc}")
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(repeats)]
+    for i in range(repeats):
+        ev[i][0].record()
+        call(i % sets)
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    ms = sum(a.elapsed_time(e) for a, e in ev) / repeats
+    nbytes = (3 * k * k + (4 if op == "ddpm_filter_bwd_k" else 5)) * B * C * h * w * esize
+    del bufs
     torch.cuda.empty_cache()
-    return {"ms": ms, "bytes": nbytes, "GB/s": nbytes / ms / 1e6, "frac_of_8TBps": nbytes / ms / 1e6 / HBM_PEAK_GBS}
+    return {"ms": ms, "bytes": nbytes, "GB/s": nbytes / ms / 1e6,
+            "frac_of_8TBps": nbytes / ms / 1e6 / HBM_PEAK_GBS}
 
 
 def unfold_route_step(params, x, y):
@@ -233,34 +273,85 @@ def unfold_route_step(params, x, y):
     return F.conv2d(torch.cat(outs, 1), fw, fb, padding=1)
 
 
-def peak_temp_mib(step):
+def peak_mem_child(route, dtype_name, warmup=2):
+    """Child mode: one route's peak temporary memory, measured as the
+    reference's gpu_memory_bench.py:47-76 does (warm-up, gradients released,
+    empty cache, reset peak, baseline, one step)."""
     import torch
 
-    for _ in range(2):
+    dtype = {"float32": torch.float32, "bfloat16": torch.bfloat16}[dtype_name]
+    module = make_module(dtype)
+    x, y = make_inputs(dtype)
+    params = list(module.parameters())
+
+    def step():
+        module.zero_grad(set_to_none=True)
+        x.grad = None
+        y.grad = None
+        out = module(x, y) if route == "fused" else unfold_route_step(params, x, y)
+        out.square().mean().backward()
+
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    module.zero_grad(set_to_none=True)
+    x.grad = None
+    y.grad = None
     torch.cuda.empty_cache()
     torch.cuda.reset_peak_memory_stats()
     base = torch.cuda.memory_allocated()
     step()
     torch.cuda.synchronize()
-    return (torch.cuda.max_memory_allocated() - base) / 2**20
+    peak = torch.cuda.max_memory_allocated()
+    print(json.dumps({"route": route, "dtype": dtype_name, "baseline_mib": base / 2**20,
+                      "peak_mib": peak / 2**20, "temporary_peak_mib": (peak - base) / 2**20}))
 
 
-def cpu_baseline(budget_s=20.0):
-    """The Unfold oracle restatement (fp32, torch on the host cores) running the
-    same training step; a bounded number of steps (about `budget_s` seconds)."""
+def peak_memory_children():
+    """Runs peak_mem_child for each (route, dtype) in its own process."""
+    import subprocess
+
+    out = {}
+    for dtype_name, key in (("float32", "fp32"), ("bfloat16", "bf16")):
+        res = {}
+        for route in ("fused", "unfold"):
+            proc = subprocess.run(
+                [sys.executable, os.path.abspath(__file__), "--peak-mem", route, dtype_name],
+                capture_output=True, text=True, timeout=300,
+            )
+            if proc.returncode != 0:
+                raise RuntimeError(f"peak-memory child {route} {dtype_name} failed:\n{proc.stderr[-2000:]}")
+            res[route] = json.loads(proc.stdout.strip().splitlines()[-1])["temporary_peak_mib"]
+        out[f"peak_temp_mib_{key}"] = {"fused": res["fused"], "unfold": res["unfold"],
+                                       "fused_over_unfold": res["fused"] / res["unfold"],
+                                       "method": "own process per route, gradients released "
+                                       "before the baseline (gpu_memory_bench.py:47-76)"}
+    return out
+
+
+def cpu_model():
+    cpu = platform.processor() or "cpu"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return cpu
+
+
+def cpu_leg(make_model, dtype, budget_s, warmup=3, repeats=20):
+    """Mean ms of the training step on the CPU: `warmup` untimed steps, then up
+    to `repeats` timed ones (perf_counter each, as bench.py:138-165 of the
+    reference), stopping early once `budget_s` seconds have been spent."""
     import torch
 
-    from oracle.unfold_ref import UnfoldDDPM
-
-    # the host's CPU share: OMP_NUM_THREADS when the environment sets it
-    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or os.cpu_count() or 1
-    torch.set_num_threads(threads)
     torch.manual_seed(21)
-    model = UnfoldDDPM(C, K).train()
-    x = torch.randn(B, C, H, W, requires_grad=True)
-    y = torch.randn(B, C, H, W, requires_grad=True)
+    model = make_model().to(dtype).train()
+    torch.manual_seed(22)
+    x = torch.randn(B, C, H, W, dtype=dtype, requires_grad=True)
+    y = torch.randn(B, C, H, W, dtype=dtype, requires_grad=True)
 
     def step():
         model.zero_grad(set_to_none=True)
@@ -268,30 +359,49 @@ def cpu_baseline(budget_s=20.0):
         y.grad = None
         model(x, y).square().mean().backward()
 
-    t0 = time.perf_counter()
-    step()  # warm-up (allocations, oneDNN primitive creation)
-    first = time.perf_counter() - t0
-    n = max(1, min(20, int(budget_s / max(first, 1e-3))))
-    t0 = time.perf_counter()
-    for _ in range(n):
+    for _ in range(warmup):
         step()
-    ms = (time.perf_counter() - t0) * 1e3 / n
-    cpu = platform.processor() or "cpu"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    times = []
+    start = time.perf_counter()
+    while len(times) < repeats and (not times or time.perf_counter() - start < budget_s):
+        t0 = time.perf_counter()
+        step()
+        times.append((time.perf_counter() - t0) * 1e3)
+    return sum(times) / len(times), len(times)
+
+
+def cpu_baseline(budget_s):
+    """The reference's CPU path on this host's cores: the drop-in module's CPU
+    branch (fp32: streaming with per-tile checkpoint, the route the 256 MiB
+    generated-kernel budget selects at 256x256; bf16: Unfold training) and the
+    Unfold oracle restatement, all at B1 C64 K3 256x256."""
+    import torch
+
+    from dynamicconvolutionoperator_amd import DDPM
+    from oracle.unfold_ref import UnfoldDDPM
+
+    # the host's CPU share for this process (OMP_NUM_THREADS where the
+    # environment sets it -- a shared host's core count is not ours to use)
+    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    branch_ms, n1 = cpu_leg(lambda: DDPM(C, K), torch.float32, budget_s)
+    progress(f"CPU branch fp32 {branch_ms:.1f} ms")
+    unfold_ms, n2 = cpu_leg(lambda: UnfoldDDPM(C, K), torch.float32, budget_s)
+    progress(f"CPU Unfold fp32 {unfold_ms:.1f} ms")
+    branch_bf16_ms, n3 = cpu_leg(lambda: DDPM(C, K), torch.bfloat16, budget_s)
+    progress(f"CPU branch bf16 {branch_bf16_ms:.1f} ms")
     return {
-        "value": ms,
+        "value": branch_ms,
         "unit": "ms per training step",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{n} timed steps (after 1 warm-up) of the full B1 C64 K3 256x256 fp32 "
-        f"Unfold-route training step on {cpu}",
+        "sample": f"B1 C64 K3 256x256 training step (fwd+bwd of out.square().mean()) on {cpu_model()}, "
+        f"{torch.get_num_threads()} threads of os.cpu_count()={os.cpu_count()}: value = the module's CPU "
+        f"branch at fp32 (streaming + per-tile checkpoint), {n1} timed steps after 3 warm-up; "
+        f"unfold_fp32_ms over {n2}, branch_bf16_ms (Unfold training route) over {n3}",
+        "unfold_fp32_ms": unfold_ms,
+        "branch_bf16_ms": branch_bf16_ms,
+        "os_cpu_count": os.cpu_count(),
     }
 
 
@@ -323,7 +433,7 @@ def kernel_mode(args):
     out = torch.empty(B, 4 * C, H, W, device="cuda", dtype=dt)
     dx, dy, dk = torch.empty_like(x), torch.empty_like(y), torch.empty_like(kern)
     dw, db = torch.empty_like(wt), torch.empty_like(bs)
-    wsb = max(int(lib.ddpm_gen_bwd_w_workspace_bytes(B, C, H, W, K)),
+    wsb = max(int(lib.ddpm_gen_bwd_w_workspace_bytes(B, C, H, W, K, code)),
               int(lib.ddpm_gen_bwd_y_workspace_bytes(C, K)),
               int(lib.ddpm_gen_bwd_x_workspace_bytes(B, C, H, W, K, *DIL)), 1)
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
@@ -358,6 +468,24 @@ def kernel_mode(args):
 
 
 # --------------------------------------------------------------------------- main
+def kernel_breakdown(lib, timer, module, x, y, steps=10):
+    """Per-entry-point HIP-event timing of the training step (a separate pass:
+    the headline loop runs uninstrumented)."""
+    import torch
+
+    for rec in timer.records.values():
+        rec.clear()
+    timer.active = True
+    for _ in range(steps):
+        train_step(module, x, y)
+    torch.cuda.synchronize()
+    timer.active = False
+    per_entry = timer.mean_ms()
+    counts = timer.counts()
+    return {n: {"ms": per_entry[n], "launches_per_step": counts[n] // steps,
+                "share_of_step_ms": per_entry[n] * counts[n] / steps} for n in per_entry}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -370,38 +498,48 @@ def main():
 
     import torch
 
-    from dynamicconvolutionoperator_amd import _lib
-
-    if not torch.cuda.is_available():
+    if args.peak_mem:
+        peak_mem_child(*args.peak_mem)
+        return
+    # device_count() does not initialise the GPU: the peak-memory children
+    # below start before this process uses it
+    if torch.cuda.device_count() < 1:
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     if args.kernel:
         kernel_mode(args)
         return
-    lib = _lib.load()
-    entries = [n for n in _lib.SIGNATURES if n.startswith(("ddpm_gen_fwd", "ddpm_gen_bwd_x", "ddpm_gen_bwd_y", "ddpm_gen_bwd_w", "ddpm_filter_"))]
-    entries = [n for n in entries if not n.endswith("_workspace_bytes")]
-    timer = LaunchTimer(lib, entries)
+    extra = {}
+    if not args.quick:
+        extra.update(peak_memory_children())
+        progress("peak temporary memory (child processes) done")
 
-    # ---- headline: fp32 fused recompute training step
+    from dynamicconvolutionoperator_amd import _lib
+
+    lib = _lib.load()
+    entries = [n for n in _lib.SIGNATURES if n.startswith(("ddpm_gen_fwd", "ddpm_gen_bwd_x", "ddpm_gen_bwd_y", "ddpm_gen_bwd_w", "ddpm_filter_", "ddpm_gen_kernels"))]
+    entries = [n for n in entries if not n.endswith(("_workspace_bytes", "_supported", "_scratch_bytes"))]
+
+    # ---- headline: fp32 fused recompute training step, uninstrumented
     module = make_module(torch.float32)
     x, y = make_inputs(torch.float32)
     for _ in range(args.warmup):
         train_step(module, x, y)
     torch.cuda.synchronize()
-    timer.active = True
     t0 = time.perf_counter()
     for _ in range(args.steps):
         train_step(module, x, y)
     torch.cuda.synchronize()
     train_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    timer.active = False
-    per_entry = timer.mean_ms()
-    counts = timer.counts()
-    step_share = {n: per_entry[n] * counts[n] / args.steps for n in per_entry}
-    dominant = max(step_share, key=step_share.get)
+    progress(f"fp32 training step {train_ms:.3f} ms")
+
+    # ---- per-entry-point breakdown (separate pass, wrappers installed only
+    #      now) and the roofline entry
+    timer = LaunchTimer(lib, entries)
+    kernels = kernel_breakdown(lib, timer, module, x, y)
+    dominant = max(kernels, key=lambda n: kernels[n]["share_of_step_ms"])
     nbytes, flops = work_per_launch(dominant, 4)
-    dom_ms = per_entry[dominant]
+    dom_ms = kernels[dominant]["ms"]
     if flops > 0:
         # fp32 operands run as three bf16 MFMA products: ceiling = bf16 dense peak / 3
         peak = BF16_DENSE_TFLOPS / 3.0
@@ -420,21 +558,16 @@ def main():
         "algorithmic_flops": flops,
         "hbm_GB/s_algorithmic": nbytes / dom_ms / 1e6,
     })
-    kernels = {
-        n: {"ms": per_entry[n], "launches_per_step": counts[n] // args.steps,
-            "share_of_step_ms": step_share[n]}
-        for n in per_entry
-    }
+    extra["kernels_fp32_train"] = kernels
     del module, x, y
     torch.cuda.empty_cache()
-    progress(f"fp32 training step {train_ms:.3f} ms")
 
-    extra = {"kernels_fp32_train": kernels}
     if not args.quick:
-        # ---- bf16 training, inference
+        # ---- bf16 training (+ breakdown), inference
         module = make_module(torch.bfloat16)
         x, y = make_inputs(torch.bfloat16)
         extra["train_ms_bf16"] = time_loop(lambda: train_step(module, x, y), args.steps, args.warmup)
+        extra["kernels_bf16_train"] = kernel_breakdown(lib, timer, module, x, y)
         module.eval()
         with torch.inference_mode():
             extra["infer_ms_bf16"] = time_loop(lambda: module(x, y), args.steps, args.warmup)
@@ -445,19 +578,50 @@ def main():
             extra["infer_ms_fp32"] = time_loop(lambda: module(x, y), args.steps, args.warmup)
         del module, x, y
         torch.cuda.empty_cache()
-
         progress("bf16 training and inference done")
-        # ---- dynamic filter bandwidth (materialized path)
-        extra["filter_fwd_fp32"] = filter_bandwidth(torch.float32)
-        extra["filter_fwd_bf16"] = filter_bandwidth(torch.bfloat16)
 
+        # ---- materialized dynamic filter at 256x256: forward, dX, dK
+        extra["filter_256"] = {
+            f"{op[12:]}_{name}": filter_op_bandwidth(op, dt)
+            for op in ("ddpm_filter_fwd", "ddpm_filter_bwd_x", "ddpm_filter_bwd_k")
+            for name, dt in (("fp32", torch.float32), ("bf16", torch.bfloat16))
+        }
         progress("filter bandwidth done")
-        # ---- peak temporary memory and Unfold-route time (GPU)
+
+        # ---- 128x128 C=64 K=3 fp32 inference: filter only and end to end
+        #      (three buffer sets of 134 MB rotate past the 256 MB MALL)
+        c2 = {"filter_fwd": filter_op_bandwidth("ddpm_filter_fwd", torch.float32, 128, 128, sets=3)}
+        module = make_module(torch.float32).eval()
+        torch.manual_seed(20)
+        x = torch.randn(1, C, 128, 128, device="cuda")
+        y = torch.randn_like(x)
+        with torch.inference_mode():
+            c2["fused_infer_ms"] = time_loop(lambda: module(x, y), args.steps, args.warmup)
+        extra["c2_infer_128_fp32"] = c2
+        del module, x, y
+
+        # ---- K=5 128x128 C=64 bf16, materialized route: inference, fwd+bwd
+        from dynamicconvolutionoperator_amd import DDPM
+
+        torch.manual_seed(21)
+        module = DDPM(C, 5).cuda().to(torch.bfloat16).train()
+        x = torch.randn(1, C, 128, 128, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+        y = torch.randn_like(x, requires_grad=True)
+        c4 = {"train_ms": time_loop(lambda: train_step(module, x, y), args.steps, args.warmup)}
+        module.eval()
+        with torch.inference_mode():
+            c4["infer_ms"] = time_loop(lambda: module(x, y), args.steps, args.warmup)
+        c4["route"] = "materialized (HIP generator GEMMs + HIP filter)"
+        extra["c4_k5_128_bf16"] = c4
+        del module, x, y
+        torch.cuda.empty_cache()
+        progress("128x128 cases done")
+
+        # ---- the Unfold route on the GPU (time only)
         for name, dtype in (("fp32", torch.float32), ("bf16", torch.bfloat16)):
             module = make_module(dtype)
             x, y = make_inputs(dtype)
-            fused_mib = peak_temp_mib(lambda: train_step(module, x, y))
-            params = [p for p in module.parameters()]
+            params = list(module.parameters())
 
             def unfold_step():
                 for p in params:
@@ -466,17 +630,14 @@ def main():
                 y.grad = None
                 unfold_route_step(params, x, y).square().mean().backward()
 
-            unfold_mib = peak_temp_mib(unfold_step)
-            extra[f"peak_temp_mib_{name}"] = {"fused": fused_mib, "unfold": unfold_mib,
-                                              "fused_over_unfold": fused_mib / unfold_mib}
             extra[f"unfold_route_train_ms_{name}"] = time_loop(unfold_step, 10, 3)
             del module, x, y, params
             torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu_baseline:
-        progress("CPU baseline (about 20 s)")
-        cpu = cpu_baseline()
+        progress("CPU baseline")
+        cpu = cpu_baseline(args.cpu_budget)
 
     result = {
         "metric": METRIC,

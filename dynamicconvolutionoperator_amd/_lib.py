@@ -43,9 +43,12 @@ SIGNATURES: dict[str, tuple[list, type]] = {
     "ddpm_gen_bwd_y": ([_P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
     "ddpm_gen_bwd_y_noalloc": ([_P, _P, _P, _P, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
     "ddpm_gen_bwd_y_noalloc_scratch_bytes": ([], _L),
-    "ddpm_gen_bwd_w_workspace_bytes": ([_L, _L, _L, _L, _I], _L),
+    "ddpm_gen_bwd_w_workspace_bytes": ([_L, _L, _L, _L, _I, _I], _L),
     "ddpm_gen_bwd_w": ([_P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
 }
+
+
+ABI_VERSION = 2  # include/ddpm_hip.h
 
 
 class HipLibraryError(RuntimeError):
@@ -69,7 +72,7 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = res
-    if lib.ddpm_abi_version() != 1:
+    if lib.ddpm_abi_version() != ABI_VERSION:
         raise HipLibraryError("libddpm_hip.so ABI version mismatch; rebuild it")
     return lib
 

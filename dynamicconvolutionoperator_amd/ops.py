@@ -234,7 +234,7 @@ class _GeneratorDynamicCat(torch.autograd.Function):
             if ctx.needs_input_grad[2] or ctx.needs_input_grad[3]:
                 grad_w = torch.empty_like(weight)
                 grad_b = torch.empty_like(bias)
-                ws_bytes = int(lib.ddpm_gen_bwd_w_workspace_bytes(n, c, h, w, k))
+                ws_bytes = int(lib.ddpm_gen_bwd_w_workspace_bytes(n, c, h, w, k, dt))
                 ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
                 _lib.check(
                     lib.ddpm_gen_bwd_w(_ptr(x), _ptr(y), _ptr(grad_out), _ptr(grad_w),

@@ -38,7 +38,7 @@ extern "C" {
 #define DDPM_DTYPE_BF16 1
 #define DDPM_DTYPE_F16 2
 
-/* ABI version of this header (1). */
+/* ABI version of this header (2). */
 int ddpm_abi_version(void);
 
 /* Text for any status code returned by this library (static storage). */
@@ -179,18 +179,18 @@ int ddpm_gen_bwd_y_noalloc(const void* x, const void* weight, const void* grad_o
                            int d1, int d2, int dtype, hipStream_t stream);
 int64_t ddpm_gen_bwd_y_noalloc_scratch_bytes(void);
 
-/* Bytes of workspace ddpm_gen_bwd_w needs: its fp32 split partials (none
- * when one split writes grad_weight / grad_bias directly), then, for fp32
- * inputs, the bf16 hi / lo planes of y (the query covers fp32; 2-byte dtypes
- * use only the partials).
+/* Bytes of workspace ddpm_gen_bwd_w needs for `dtype`: its fp32 split
+ * partials (none when one split writes grad_weight / grad_bias directly),
+ * then, for fp32, the bf16 hi / lo planes of y; 0 for an invalid dtype.
  * Replaces the partial-buffer sizing of _GeneratorDynamicCat.backward (_triton_kernels.py:1001-1017). */
-int64_t ddpm_gen_bwd_w_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size);
+int64_t ddpm_gen_bwd_w_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size,
+                                       int dtype);
 
 /* grad_weight[o,i] = sum_p dK[o,p] y[i,p], grad_bias[o] = sum_p dK[o,p]; split
- * over as many token ranges as give every CU one workgroup (21 at C = 64)
- * into fp32 partials in `workspace`, then summed in a fixed order
- * (deterministic).  DDPM_STATUS_UNSUPPORTED for a dilation above 8 or
- * 3*K*K*C*(C+1) >= 2^31.
+ * over at most 16 token ranges (of at least 4 row segments of 128 columns)
+ * into fp32 partials in `workspace`, then summed in split order
+ * (deterministic); one split writes the gradients directly.
+ * DDPM_STATUS_UNSUPPORTED for a dilation above 8 or 3*K*K*C*(C+1) >= 2^31.
  * Replaces _generator_dynamic_cat_bwd_weight_partial + _bwd_weight_reduce
  * (_triton_kernels.py:626-811, launched at :973-1053). */
 int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out, void* grad_weight,

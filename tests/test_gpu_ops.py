@@ -243,10 +243,13 @@ def test_generator_inference_has_no_autograd_graph():
 @pytest.mark.parametrize(
     "shape",
     [
-        (2, 32, 40, 64),  # 80 steps (row segments of 128 columns) -> 20 splits of fp32 partials
-        (1, 24, 4, 17),   # 4 steps -> one split writes the gradients directly
-        (1, 10, 24, 40),  # C % 4 != 0, 24 steps -> 6 splits, scalar split reduction
-        (1, 10, 3, 20),   # C % 4 != 0, 3 steps -> direct write
+        # steps = row segments of 128 columns; at most 16 splits of at least 4 steps
+        (2, 32, 40, 64),     # 80 steps -> 16 splits of 5
+        (1, 24, 4, 17),      # 4 steps -> one split writes the gradients directly
+        (1, 10, 3, 20),      # C % 4 != 0, direct
+        (1, 10, 24, 40),     # C % 4 != 0, 24 steps -> 6 splits, scalar split reduction
+        (2, 64, 128, 136),   # 512 steps -> 16 splits, a partial 128-column block per row
+        (1, 24, 150, 130),   # W % 8 != 0 (element-wise y / gradient copies), 16 splits
     ],
 )
 def test_generator_weight_gradient_splits(shape):
