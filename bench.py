@@ -64,6 +64,11 @@ def parse_args():
     )
     p.add_argument("--dtype", choices=("f32", "bf16"), default="f32", help="with --kernel")
     p.add_argument("--reps", type=int, default=3, help="launches per entry point with --kernel")
+    p.add_argument("--kernel-size", type=int, default=K, help="with --kernel: K (filter entry points "
+                   "take any odd K; the fused ones 1 or 3)")
+    p.add_argument("--res", type=int, default=H, help="with --kernel: H = W")
+    p.add_argument("--sets", type=int, default=1, help="with --kernel: input sets the launches "
+                   "rotate through (2 keeps a 150 MB tensor from being re-read out of the MALL)")
     p.add_argument("--peak-mem", nargs=2, metavar=("ROUTE", "DTYPE"),
                    help="child mode: peak temporary memory of one training step of ROUTE "
                    "(fused|unfold) in DTYPE (float32|bfloat16); prints one JSON line")
@@ -410,10 +415,11 @@ COPY_BYTES = 2**30  # 'copy': a plain 1 GiB device copy (4x the MALL; reads and 
 
 
 def kernel_mode(args):
-    """Launches the named entry points `reps` times each at B1 C64 K3 256x256
-    (dilations 1/3/5) on seeded inputs, and 'copy' as a plain device copy of
-    COPY_BYTES, so that rocprofv3 --pmc can read each kernel's HBM counters
-    (FETCH_SIZE / WRITE_SIZE) and the copy calibrates them."""
+    """Launches the named entry points `reps` times each at B1 C64 (K, res from
+    the arguments; dilations 1/3/5) on seeded inputs, rotating through `sets`
+    input sets, and 'copy' as a plain device copy of COPY_BYTES, so that
+    rocprofv3 can read each kernel's duration and HBM counters (FETCH_SIZE /
+    WRITE_SIZE) and the copy calibrates them."""
     import ctypes
 
     import torch
@@ -423,51 +429,59 @@ def kernel_mode(args):
     lib = _lib.load()
     dt = {"f32": torch.float32, "bf16": torch.bfloat16}[args.dtype]
     code = 0 if dt == torch.float32 else 1
+    k, hw = args.kernel_size, args.res
     ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     g = torch.Generator(device="cuda").manual_seed(1)
     rnd = lambda *shape: torch.randn(*shape, device="cuda", generator=g).to(dt)  # noqa: E731
-    x, y = rnd(B, C, H, W), rnd(B, C, H, W)
-    go = rnd(B, 4 * C, H, W)
-    wt, bs = rnd(3 * C * K * K, C) * 0.1, rnd(3 * C * K * K) * 0.1
-    kern = rnd(B, 3, C, K * K, H, W)
-    out = torch.empty(B, 4 * C, H, W, device="cuda", dtype=dt)
-    dx, dy, dk = torch.empty_like(x), torch.empty_like(y), torch.empty_like(kern)
+    sets = []
+    for _ in range(max(1, args.sets)):
+        sets.append({
+            "x": rnd(B, C, hw, hw), "y": rnd(B, C, hw, hw), "go": rnd(B, 4 * C, hw, hw),
+            "kern": rnd(B, 3, C, k * k, hw, hw),
+        })
+    wt, bs = rnd(3 * C * k * k, C) * 0.1, rnd(3 * C * k * k) * 0.1
+    out = torch.empty(B, 4 * C, hw, hw, device="cuda", dtype=dt)
+    dx, dy = torch.empty(B, C, hw, hw, device="cuda", dtype=dt), torch.empty(B, C, hw, hw, device="cuda", dtype=dt)
+    dk = torch.empty_like(sets[0]["kern"])
     dw, db = torch.empty_like(wt), torch.empty_like(bs)
-    wsb = max(int(lib.ddpm_gen_bwd_w_workspace_bytes(B, C, H, W, K, code)),
-              int(lib.ddpm_gen_bwd_y_workspace_bytes(C, K)),
-              int(lib.ddpm_gen_bwd_x_workspace_bytes(B, C, H, W, K, *DIL)), 1)
+    wsb = max(int(lib.ddpm_gen_bwd_w_workspace_bytes(B, C, hw, hw, k, code)),
+              int(lib.ddpm_gen_bwd_y_workspace_bytes(C, k)),
+              int(lib.ddpm_gen_bwd_x_workspace_bytes(B, C, hw, hw, k, *DIL)), 1)
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    shp = (B, C, H, W, K, *DIL)
+    shp = (B, C, hw, hw, k, *DIL)
     calls = {
-        "ddpm_gen_fwd": lambda: lib.ddpm_gen_fwd(ptr(x), ptr(y), ptr(wt), ptr(bs), ptr(out), *shp, code, s),
-        "ddpm_gen_bwd_x": lambda: lib.ddpm_gen_bwd_x(ptr(y), ptr(wt), ptr(bs), ptr(go), ptr(dx), ptr(ws), wsb,
-                                                     *shp, code, s),
-        "ddpm_gen_bwd_y": lambda: lib.ddpm_gen_bwd_y(ptr(x), ptr(wt), ptr(go), ptr(dy), ptr(ws), wsb, *shp,
-                                                     code, s),
-        "ddpm_gen_bwd_w": lambda: lib.ddpm_gen_bwd_w(ptr(x), ptr(y), ptr(go), ptr(dw), ptr(db), ptr(ws), wsb,
-                                                     *shp, code, s),
-        "ddpm_filter_fwd": lambda: lib.ddpm_filter_fwd(ptr(x), ptr(kern), ptr(out), *shp, code, code, s),
-        "ddpm_filter_bwd_x": lambda: lib.ddpm_filter_bwd_x(ptr(go), ptr(kern), ptr(dx), *shp, code, code, s),
-        "ddpm_filter_bwd_k": lambda: lib.ddpm_filter_bwd_k(ptr(x), ptr(go), ptr(dk), *shp, code, code, s),
-        "copy": lambda: (dst.copy_(src), 0)[1],
+        "ddpm_gen_fwd": lambda t: lib.ddpm_gen_fwd(ptr(t["x"]), ptr(t["y"]), ptr(wt), ptr(bs), ptr(out), *shp,
+                                                   code, s),
+        "ddpm_gen_bwd_x": lambda t: lib.ddpm_gen_bwd_x(ptr(t["y"]), ptr(wt), ptr(bs), ptr(t["go"]), ptr(dx),
+                                                       ptr(ws), wsb, *shp, code, s),
+        "ddpm_gen_bwd_y": lambda t: lib.ddpm_gen_bwd_y(ptr(t["x"]), ptr(wt), ptr(t["go"]), ptr(dy), ptr(ws),
+                                                       wsb, *shp, code, s),
+        "ddpm_gen_bwd_w": lambda t: lib.ddpm_gen_bwd_w(ptr(t["x"]), ptr(t["y"]), ptr(t["go"]), ptr(dw),
+                                                       ptr(db), ptr(ws), wsb, *shp, code, s),
+        "ddpm_filter_fwd": lambda t: lib.ddpm_filter_fwd(ptr(t["x"]), ptr(t["kern"]), ptr(out), *shp, code,
+                                                         code, s),
+        "ddpm_filter_bwd_x": lambda t: lib.ddpm_filter_bwd_x(ptr(t["go"]), ptr(t["kern"]), ptr(dx), *shp,
+                                                             code, code, s),
+        "ddpm_filter_bwd_k": lambda t: lib.ddpm_filter_bwd_k(ptr(t["x"]), ptr(t["go"]), ptr(dk), *shp, code,
+                                                             code, s),
+        "copy": lambda t: (dst.copy_(src), 0)[1],
     }
     names = args.kernel.split(",")
     for name in names:
         if name not in calls:
             raise SystemExit(f"unknown --kernel {name}; choose from {', '.join(calls)}")
     for name in names:
-        for _ in range(args.reps):
-            rc = calls[name]()
+        for i in range(args.reps):
+            rc = calls[name](sets[i % len(sets)])
             if rc:
                 raise SystemExit(f"{name} failed with status {rc}")
         torch.cuda.synchronize()
-        print(f"ran {name} x{args.reps} ({args.dtype})", flush=True)
+        print(f"ran {name} x{args.reps} ({args.dtype}, K={k}, {hw}x{hw}, {len(sets)} input sets)", flush=True)
 
 
-# --------------------------------------------------------------------------- main
 def kernel_breakdown(lib, timer, module, x, y, steps=10):
     """Per-entry-point HIP-event timing of the training step (a separate pass:
     the headline loop runs uninstrumented)."""
