@@ -44,6 +44,9 @@ SIGNATURES: dict[str, tuple[list, type]] = {
     "ddpm_gen_bwd_y_noalloc": ([_P, _P, _P, _P, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
     "ddpm_gen_bwd_y_noalloc_scratch_bytes": ([], _L),
     "ddpm_gen_bwd_w_workspace_bytes": ([_L, _L, _L, _L, _I, _I], _L),
+    "ddpm_fuse_conv_workspace_bytes": ([_L, _I], _L),
+    "ddpm_fuse_conv_fwd": ([_P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _P], _I),
+    "ddpm_fuse_conv_bwd_data": ([_P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _P], _I),
     "ddpm_gen_bwd_w": ([_P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
 }
 

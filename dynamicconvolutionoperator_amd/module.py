@@ -11,7 +11,10 @@ with the GPU route backed by HIP kernels for gfx950:
   If the HIP library is missing it raises instead of falling back.
 * CPU tensors -> the reference's CPU branch (triton_impl.py:353-391).
 
-The final 3x3 ``fuse`` convolution is a plain ``nn.Conv2d`` (MIOpen on ROCm).
+The final 3x3 ``fuse`` convolution is a plain ``nn.Conv2d`` (its parameters and
+state-dict keys are the reference's); on ROCm tensors its forward and input
+gradient run as HIP MFMA kernels (``fuse_conv_backend = "library"`` selects
+MIOpen through ``self.fuse`` instead).
 """
 
 from __future__ import annotations
@@ -36,7 +39,8 @@ def _load_hip_ops():
     from . import _lib, ops
 
     _lib.load()
-    return ops.fused_dynamic_cat, ops.fused_generator_dynamic_cat, ops.generator_supported, ops._generate
+    return (ops.fused_dynamic_cat, ops.fused_generator_dynamic_cat, ops.generator_supported,
+            ops._generate, ops.fuse_conv3x3)
 
 
 def _check_inputs(x: torch.Tensor, y: torch.Tensor, channels: int) -> None:
@@ -91,6 +95,10 @@ class DDPM(nn.Module):
         self.fused_generator_inference = fused_generator_inference
         self.fused_generator_training = fused_generator_training
         self.dilations = _DEFAULT_DILATIONS
+        # the 3x3 fuse convolution on ROCm tensors: "hip" runs it as this
+        # library's MFMA kernels (same Conv2d parameters), "library" calls
+        # self.fuse (MIOpen), as the reference calls cuDNN
+        self.fuse_conv_backend = "hip"
         # creation order (generator, then fuse) fixes the seeded default init
         self.generator = nn.Conv2d(dim, 3 * dim * kernel_size**2, 1)
         self.fuse = nn.Conv2d(4 * dim, dim, 3, 1, 1)
@@ -122,7 +130,7 @@ class DDPM(nn.Module):
         return "fused" if can_fuse else "materialized"
 
     def _cuda_cat(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
-        fused_dynamic_cat, fused_generator_dynamic_cat, gen_supported, generate = _load_hip_ops()
+        fused_dynamic_cat, fused_generator_dynamic_cat, gen_supported, generate, _ = _load_hip_ops()
         if self._route(x, y, gen_supported) == "fused":
             return fused_generator_dynamic_cat(
                 x, y, self.generator.weight, self.generator.bias, self.kernel_size, self.dilations
@@ -163,10 +171,19 @@ class DDPM(nn.Module):
             self.recompute and self.training,
         )
 
+    def _cuda_fuse(self, cat_out: torch.Tensor) -> torch.Tensor:
+        """The fuse convolution of a ROCm concat: the HIP kernels unless the
+        backend is "library" or autocast is on (the Conv2d then runs in the
+        autocast dtype, as the reference's does)."""
+        if self.fuse_conv_backend == "hip" and not torch.is_autocast_enabled(cat_out.device.type):
+            fuse_conv3x3 = _load_hip_ops()[4]
+            return fuse_conv3x3(cat_out, self.fuse.weight, self.fuse.bias)
+        return self.fuse(cat_out)
+
     def forward(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         _check_inputs(x, y, self.dim)
         if x.is_cuda:
-            cat_out = self._cuda_cat(x, y)
+            return self._cuda_fuse(self._cuda_cat(x, y))
         elif x.device.type == "cpu":
             cat_out = self._cpu_cat(x, y)
         else:

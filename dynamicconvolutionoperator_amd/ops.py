@@ -386,7 +386,94 @@ def fused_generator_dynamic_cat(x, y, weight, bias, kernel_size, dilations):
     return _launch_generator_dynamic_cat(x, y, weight, bias, k, dil)
 
 
+# ---------------------------------------------------------------------------
+# The 3x3 fuse convolution
+# ---------------------------------------------------------------------------
+def fuse_conv_supported(cat, weight, bias) -> bool:
+    """Whether the HIP fuse convolution takes this call: Conv2d(4C -> C, 3,
+    padding 1) weights, one dtype for the concat, weight and bias, a ROCm
+    device, and one image's planes within 32-bit byte offsets."""
+    if cat.ndim != 4 or weight.ndim != 4 or cat.dtype not in _DTYPES:
+        return False
+    n, ci, h, w = cat.shape
+    c = weight.shape[0]
+    if tuple(weight.shape) != (c, ci, 3, 3) or ci != 4 * c:
+        return False
+    if weight.dtype != cat.dtype or (bias is not None and bias.dtype != cat.dtype):
+        return False
+    if cat.device.type != "cuda" or weight.device != cat.device:
+        return False
+    return ci * h * w * cat.element_size() <= 2**31 - 1
+
+
+def _fuse_conv_workspace(c, dt, device):
+    nbytes = int(_lib.load().ddpm_fuse_conv_workspace_bytes(c, dt))
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device), nbytes
+
+
+class _FuseConv3x3(torch.autograd.Function):
+    """``F.conv2d(cat, weight, bias, padding=1)`` for the DDPM fuse
+    convolution: forward and input gradient as HIP implicit-GEMM MFMA kernels
+    (``ddpm_fuse_conv_fwd`` / ``_bwd_data``); the weight and bias gradients
+    through the library convolution."""
+
+    @staticmethod
+    def forward(ctx, cat, weight, bias):
+        cat = cat.contiguous()
+        weight = weight.contiguous()
+        n, ci, h, w = cat.shape
+        c = weight.shape[0]
+        out = torch.empty((n, c, h, w), dtype=cat.dtype, device=cat.device)
+        dt = _dt(cat)
+        lib = _lib.load()
+        with torch.cuda.device(cat.device):
+            ws, nbytes = _fuse_conv_workspace(c, dt, cat.device)
+            code = lib.ddpm_fuse_conv_fwd(_ptr(cat), _ptr(weight),
+                                          _ptr(bias.contiguous()) if bias is not None else None,
+                                          _ptr(out), _ptr(ws), nbytes, n, c, h, w, dt, _stream(cat))
+        _lib.check(code, "ddpm_fuse_conv_fwd")
+        ctx.save_for_backward(cat, weight)
+        ctx.has_bias = bias is not None
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        cat, weight = ctx.saved_tensors
+        grad_out = grad_out.to(cat.dtype).contiguous()
+        n, ci, h, w = cat.shape
+        c = weight.shape[0]
+        grad_cat = grad_w = grad_b = None
+        if ctx.needs_input_grad[0]:
+            grad_cat = torch.empty_like(cat)
+            dt = _dt(cat)
+            lib = _lib.load()
+            with torch.cuda.device(cat.device):
+                ws, nbytes = _fuse_conv_workspace(c, dt, cat.device)
+                code = lib.ddpm_fuse_conv_bwd_data(_ptr(grad_out), _ptr(weight), _ptr(grad_cat),
+                                                   _ptr(ws), nbytes, n, c, h, w, dt, _stream(cat))
+            _lib.check(code, "ddpm_fuse_conv_bwd_data")
+        need_w = ctx.needs_input_grad[1]
+        need_b = ctx.has_bias and ctx.needs_input_grad[2]
+        if need_w or need_b:
+            _, gw, gb = torch.ops.aten.convolution_backward(
+                grad_out, cat, weight, [c] if ctx.has_bias else None, [1, 1], [1, 1], [1, 1], False,
+                [0, 0], 1, [False, need_w, need_b])
+            grad_w = gw if need_w else None
+            grad_b = gb if need_b else None
+        return grad_cat, grad_w, grad_b
+
+
+def fuse_conv3x3(cat, weight, bias=None):
+    """The DDPM fuse convolution ``Conv2d(4C -> C, 3, padding=1)`` on the HIP
+    path (shapes of :func:`fuse_conv_supported`), else the library one."""
+    if fuse_conv_supported(cat, weight, bias):
+        return _FuseConv3x3.apply(cat, weight, bias)
+    return torch.nn.functional.conv2d(cat, weight, bias, padding=1)
+
+
 __all__ = [
+    "fuse_conv3x3",
+    "fuse_conv_supported",
     "fused_dynamic_cat",
     "fused_generator_dynamic_cat",
     "generator_supported",

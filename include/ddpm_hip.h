@@ -198,6 +198,30 @@ int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out, void* gra
                    int64_t h, int64_t w, int kernel_size, int d0, int d1, int d2, int dtype,
                    hipStream_t stream);
 
+/* ---- the 3x3 fuse convolution (Conv2d(4C -> C, 3, padding 1)) -------- */
+
+/* Bytes of workspace ddpm_fuse_conv_fwd / _bwd_data need for their packed
+ * weight (MFMA fragment order; fp32 as bf16 hi / lo): the larger of the two
+ * directions, so one buffer serves both. */
+int64_t ddpm_fuse_conv_workspace_bytes(int64_t c, int dtype);
+
+/* out[n][co][h][w] = bias[co] + sum_{ci,ki,kj} weight[co][ci][ki][kj] *
+ *                    cat[n][ci][h+ki-1][w+kj-1]  (zero padding), accumulated in
+ * fp32 (fp32 operands as three bf16 MFMA products) and rounded once to
+ * `dtype`.  cat: [n][4c][h][w]; weight: [c][4c][3][3]; bias: [c] or NULL.
+ * Replaces the cuDNN forward of self.fuse (triton_impl.py:294, 392). */
+int ddpm_fuse_conv_fwd(const void* cat, const void* weight, const void* bias, void* out,
+                       void* workspace, int64_t workspace_bytes, int64_t n, int64_t c, int64_t h,
+                       int64_t w, int dtype, hipStream_t stream);
+
+/* grad_cat[n][ci][h][w] = sum_{co,ki,kj} weight[co][ci][ki][kj] *
+ *                         grad_out[n][co][h-ki+1][w-kj+1]  (zero outside the image).
+ * Replaces the cuDNN backward-data convolution of self.fuse (autograd of
+ * nn.Conv2d, triton_impl.py:294, 392). */
+int ddpm_fuse_conv_bwd_data(const void* grad_out, const void* weight, void* grad_cat,
+                            void* workspace, int64_t workspace_bytes, int64_t n, int64_t c,
+                            int64_t h, int64_t w, int dtype, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,63 @@
+"""The HIP 3x3 fuse convolution (ddpm_fuse_conv_fwd / _bwd_data) against
+float64 F.conv2d on the CPU: Conv2d(4C -> C, 3, padding 1) forward and the
+gradients of its input, weight and bias, on a non-aligned shape (C=24,
+15x17: element-wise row copies, a partial plane chunk), aligned shapes
+(W % 8 == 0: 16-byte row copies) and the full 256x256 C=64 size."""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from dynamicconvolutionoperator_amd import ops
+from tests.gpu_helpers import DEV, assert_close, randn, say
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 2e-5, torch.bfloat16: 2e-2, torch.float16: 4e-3}
+
+
+def _check(shape, dtype, seed):
+    n, c, h, w = shape
+    cat = randn((n, 4 * c, h, w), seed).to(dtype)
+    torch.manual_seed(seed + 1)
+    conv = torch.nn.Conv2d(4 * c, c, 3, 1, 1)
+    wt = conv.weight.detach().to(dtype)
+    b = conv.bias.detach().to(dtype)
+    g = randn((n, c, h, w), seed + 2).to(dtype)
+    # float64 reference on the CPU from the dtype-rounded operands
+    cr, wr, br = (t.double().requires_grad_() for t in (cat, wt, b))
+    ref = F.conv2d(cr, wr, br, padding=1)
+    ref.backward(g.double())
+    cd, wd, bd = (t.to(DEV).requires_grad_() for t in (cat, wt, b))
+    assert ops.fuse_conv_supported(cd, wd, bd)
+    out = ops.fuse_conv3x3(cd, wd, bd)
+    out.backward(g.to(DEV))
+    tol = TOL[dtype]
+    for name, a, e in (("out", out, ref), ("d cat", cd.grad, cr.grad), ("d weight", wd.grad, wr.grad),
+                       ("d bias", bd.grad, br.grad)):
+        scale = e.abs().max().item()
+        assert_close(a, e, tol * scale, tol, f"{name} {shape} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(2, 24, 15, 17), (1, 16, 12, 40), (2, 8, 5, 264)])
+def test_fuse_conv_matches_conv2d(shape, dtype):
+    say(f"fuse conv shape={shape} dtype={dtype}")
+    _check(shape, dtype, 900)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fuse_conv_full_size(dtype):
+    say(f"fuse conv 256x256 C=64 dtype={dtype}")
+    _check((1, 64, 256, 256), dtype, 910)
+
+
+def test_fuse_conv_without_bias_and_fallback():
+    cat = randn((1, 32, 9, 16), 920).to(DEV)
+    wt = randn((8, 32, 3, 3), 921, scale=0.1).to(DEV)
+    out = ops.fuse_conv3x3(cat, wt, None)
+    ref = F.conv2d(cat.cpu().double(), wt.cpu().double(), None, padding=1)
+    assert_close(out, ref, 2e-5 * ref.abs().max().item(), 2e-5, "no bias")
+    # not a 4C -> C convolution: the library path
+    wt2 = randn((8, 16, 3, 3), 922).to(DEV)
+    assert not ops.fuse_conv_supported(cat[:, :16], wt2, None)
