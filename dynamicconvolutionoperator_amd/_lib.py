@@ -47,6 +47,8 @@ SIGNATURES: dict[str, tuple[list, type]] = {
     "ddpm_fuse_conv_workspace_bytes": ([_L, _I], _L),
     "ddpm_fuse_conv_fwd": ([_P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _P], _I),
     "ddpm_fuse_conv_bwd_data": ([_P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _P], _I),
+    "ddpm_fuse_conv_bwd_weight_workspace_bytes": ([_L, _L, _L, _L, _I], _L),
+    "ddpm_fuse_conv_bwd_weight": ([_P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _P], _I),
     "ddpm_gen_bwd_w": ([_P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
 }
 

@@ -1,0 +1,525 @@
+// Weight and bias gradients of the 3x3 fuse convolution on MFMA.
+//
+//   grad_weight[co][ci][ki][kj] = sum_{n,p} grad_out[n][co][p] * cat[n][ci][p + (ki-1, kj-1)]
+//   grad_bias[co]               = sum_{n,p} grad_out[n][co][p]
+//
+// (zero padding), the backward-filter convolution the reference leaves to
+// cuDNN (triton_impl.py:294, 392).  A GEMM with M = ci, N = co, K = pixels
+// per tap, the same shape as the fused generator's weight gradient
+// (gen_bwd_w.hip) with the shifted cat rows in place of dK and grad_out in
+// place of y.  Work decomposition (CDNA4):
+//   * one workgroup per (pixel split, 16-plane block of ci): at most 16
+//     splits of at least 4 steps -- a step is one image-row segment of 128
+//     columns -- (16 splits x 16 blocks = 256 workgroups at C = 64, 256x256);
+//     their fp32 partials are summed in split order by a second kernel
+//     (deterministic, no atomics); a single split writes the gradients
+//     directly;
+//   * per step the 3 cat rows {h-1, h, h+1} of the 16 planes (128 + 16
+//     columns) and the grad_out rows of all C planes (fp32: pre-split into
+//     bf16 hi / lo planes by gen_ysplit_kernel) are copied global -> LDS by
+//     16-byte buffer loads that write LDS directly (zero outside the image),
+//     one step ahead into a second buffer;
+//   * 12 waves = 4 token segments x 3 kernel rows (three waves per SIMD); a
+//     wave accumulates its row's 3 taps x 16 ci x C co on
+//     v_mfma_f32_16x16x32_{bf16,f16} (fp32 operands as three bf16 products);
+//   * grad_bias: workgroups of the first ceil(C/16) ci blocks each add up one
+//     16-plane block of grad_out with one more MFMA per step and part (a
+//     fragment of ones times grad_out).
+
+#include "gen_common.h"
+
+#include <type_traits>
+
+namespace ddpm {
+
+constexpr int kCwSegs = 4;                  // 32-token segments per step
+constexpr int kCwTW = 32 * kCwSegs;         // columns per step
+constexpr int kCwPad = 8;                   // staged column halo (16 bytes of 2-byte values)
+constexpr int kCwLW = kCwTW + 2 * kCwPad;   // staged cat columns
+constexpr int kCwNW = 3 * kCwSegs;          // waves: segments x kernel rows
+constexpr int kCwThreads = 64 * kCwNW;
+constexpr int kCwMaxSplits = 16;
+constexpr int kCwMinSteps = 4;
+
+struct CwGeom {
+  int N, C, CI, H, W;   // C output planes (co), CI = 4C input planes (ci)
+  int cblocks;          // ceil(CI / 16)
+  int col_blocks;       // ceil(W / kCwTW)
+  int splits, steps, steps_per_split;
+  int direct;
+  int x16;              // cat rows hold whole 16-byte chunks: one 16-byte copy per row
+  int g16;              // grad_out (planes) rows 16-byte aligned with W % 8 == 0: 16-byte copies
+};
+
+// One LDS staging buffer (dwords):
+//   cat rows [3*16][kXSD]   T elements; odd pitch (the 64 lanes' reads of one
+//                           element fall at most two to a bank)
+//   gO rows  [P][MB*16][kYD] 2-byte elements (grad_out, or the bf16 hi / lo
+//                           planes of an fp32 grad_out): 16 chunks of 16
+//                           bytes, chunk k of row i at position k ^ (i & 15)
+template <typename T, int MB>
+struct CwLds {
+  static constexpr int P = Mma<T>::P;
+  static constexpr int kPerD = 4 / (int)sizeof(T);
+  static constexpr int kXD = kCwLW / kPerD;
+  static constexpr int kXSD = kXD + (sizeof(T) == 4 ? 1 : 3);
+  static constexpr int kYC = kCwTW / 8;  // 16-byte chunks per gO row (16)
+  static constexpr int kYD = 4 * kYC;
+  static constexpr int kXRows = 3 * 16;
+  static constexpr int kYRows = P * MB * 16;
+  static constexpr int kYOff = kXRows * kXSD;
+  static constexpr int kBuf = kYOff + kYRows * kYD;
+  static_assert(kXSD % 2 == 1, "odd cat-row pitch");
+  static_assert(kXD % 4 == 0, "16-byte copies move whole rows");
+  static_assert(kYC == 16, "the chunk swizzle needs 16 chunks per row");
+};
+
+template <typename T>
+__device__ __forceinline__ float cw_lds_elem(const uint32_t* __restrict__ base, int idx) {
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(base[idx]);
+  } else {
+    return to_f(reinterpret_cast<const T*>(base)[idx]);
+  }
+}
+
+struct CwPos {
+  int n, h, w0, cbk;
+  __device__ __forceinline__ void advance(const CwGeom& g) {
+    w0 += kCwTW;
+    if (++cbk == g.col_blocks) {
+      cbk = 0;
+      w0 = 0;
+      if (++h == g.H) {
+        h = 0;
+        ++n;
+      }
+    }
+  }
+};
+
+// gb: grad_out itself (2-byte types) or its bf16 hi / lo planes [n][2][C][H*W] (fp32).
+template <typename T, int MB>
+__global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
+    const T* __restrict__ cat, const uint16_t* __restrict__ gb, float* __restrict__ pw,
+    float* __restrict__ pb, T* __restrict__ dw_out, T* __restrict__ db_out, CwGeom g) {
+  typedef Mma<T> M;
+  typedef typename M::V V;
+  typedef typename M::E ME;
+  typedef CwLds<T, MB> L;
+  constexpr int P = M::P;
+  constexpr int E = (int)sizeof(T);
+  extern __shared__ __attribute__((aligned(16))) uint32_t csm[];
+
+  const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int split = logical / g.cblocks;
+  const int cb = logical - split * g.cblocks;
+  const int C = g.C, CI = g.CI, H = g.H, W = g.W;
+  const int64_t HW = (int64_t)H * W;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int col16 = lane & 15, quad = lane >> 4;
+  const int sg = wave % kCwSegs, ki = wave / kCwSegs;  // token segment, kernel row
+  // bias: workgroup cb < ceil(C/16) sums grad_out block cb (kernel-row-0 waves)
+  const bool do_bias = cb < (C + 15) / 16 && ki == 0;
+
+  const int step_beg = split * g.steps_per_split;
+  int step_end = step_beg + g.steps_per_split;
+  if (step_end > g.steps) step_end = g.steps;
+  const int steps = step_end > step_beg ? step_end - step_beg : 0;
+
+  // gO copies (16-byte lanes): the lane's byte offset within one image's
+  // planes at row 0, column 0 (kOob for planes >= C) and its chunk's column
+  constexpr int YRPC = 64 / L::kYC;  // gO rows per 1 KB copy
+  constexpr int NY = L::kYRows / YRPC;
+  constexpr int NJ = (NY + kCwNW - 1) / kCwNW;
+  uint32_t cpo[NJ];
+  int cpc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int ii = wave + kCwNW * j;
+    cpo[j] = kOob;
+    cpc[j] = 0;
+    if (ii < NY) {
+      const int row = ii * YRPC + lane / L::kYC, pos = lane % L::kYC;
+      const int part = row / (MB * 16), i = row - part * (MB * 16);
+      cpc[j] = (pos ^ (i & 15)) * 8;
+      if (i < C) cpo[j] = ((uint32_t)(part * C + i) * (uint32_t)HW + (uint32_t)cpc[j]) * 2u;
+    }
+  }
+
+  // ---- operands of step `p` -> LDS buffer `buf`
+  auto stage = [&](const CwPos& p, int buf) {
+    uint32_t* __restrict__ dstb = csm + buf * L::kBuf;
+    const BufRes xres = make_buf(cat + (int64_t)p.n * CI * HW, (uint32_t)(CI * HW * E));
+    if (g.x16) {
+      // cat rows: one copy per row, lane l < kXD/4 moving the row's 16-byte chunk l
+      const BufRes xnul = make_buf(cat, 0u);
+      const int gw = p.w0 - kCwPad + 4 * L::kPerD * lane;
+      const uint32_t colb =
+          (lane < L::kXD / 4 && (unsigned)gw < (unsigned)W) ? (uint32_t)gw * E : kOob;
+#pragma unroll
+      for (int j = 0; j < (L::kXRows + kCwNW - 1) / kCwNW; ++j) {
+        const int pr = wave + kCwNW * j;
+        if (L::kXRows % kCwNW != 0 && pr >= L::kXRows) break;
+        const int rr = pr >> 4, c = pr & 15;
+        const int ch = cb * 16 + c, hh = p.h + rr - 1;
+        const bool ok = ch < CI && (unsigned)hh < (unsigned)H;
+        const uint32_t soff = ok ? ((uint32_t)ch * (uint32_t)HW + (uint32_t)(hh * W)) * E : 0u;
+        const BufRes rs = ok ? xres : xnul;
+        if (lane < L::kXD / 4)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rs, (__attribute__((address_space(3))) void*)(dstb + pr * L::kXSD), 16, colb, soff,
+              0, 0);
+      }
+    } else {
+      // element-wise through registers (W not a multiple of a 16-byte chunk)
+      T* __restrict__ dst = reinterpret_cast<T*>(dstb);
+      for (int idx = tid; idx < L::kXRows * kCwLW; idx += kCwThreads) {
+        const int pr = idx / kCwLW, j = idx - pr * kCwLW;
+        const int rr = pr >> 4, c = pr & 15;
+        const int ch = cb * 16 + c, hh = p.h + rr - 1, gw = p.w0 - kCwPad + j;
+        const bool ok = ch < CI && (unsigned)hh < (unsigned)H && (unsigned)gw < (unsigned)W;
+        const uint32_t off = ok ? (uint32_t)(((int64_t)ch * H + hh) * W + gw) * E : kOob;
+        dst[pr * L::kXSD * L::kPerD + j] = from_f<T>(buf_load1<T>(xres, off));
+      }
+    }
+    // gO rows (P parts x MB*16 planes) in the swizzled chunk layout; planes >= C read zero
+    const BufRes yres = make_buf(gb + (int64_t)p.n * P * C * HW, (uint32_t)(P * C * HW * 2));
+    const uint32_t rowel = (uint32_t)(p.h * W);
+    if (g.g16) {
+      const uint32_t ystep = (rowel + (uint32_t)p.w0) * 2u;
+      const bool full = p.w0 + kCwTW <= W;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int ii = wave + kCwNW * j;
+        if (NY % kCwNW != 0 && ii >= NY) break;
+        uint32_t vo = cpo[j];
+        if (!full) vo = p.w0 + cpc[j] < W ? vo : kOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            yres, (__attribute__((address_space(3))) void*)(dstb + L::kYOff + ii * 256), 16, vo,
+            ystep, 0, 0);
+      }
+    } else {
+      uint16_t* __restrict__ dy = reinterpret_cast<uint16_t*>(dstb + L::kYOff);
+      constexpr int PY = L::kYRows * kCwTW;
+      for (int idx = tid; idx < PY; idx += kCwThreads) {
+        const int row = idx / kCwTW, j = idx - row * kCwTW;
+        const int part = row / (MB * 16), i = row - part * (MB * 16);
+        const int w = p.w0 + j;
+        const uint32_t off =
+            (i < C && w < W) ? ((uint32_t)(part * C + i) * (uint32_t)HW + rowel + (uint32_t)w) * 2u
+                             : kOob;
+        const int kc = (j >> 3) ^ (i & 15);
+        dy[row * L::kYD * 2 + kc * 8 + (j & 7)] =
+            (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(yres, off, 0, 0);
+      }
+    }
+  };
+
+  // A fragment of ones for the bias sums
+  V ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = (ME)1.0f;
+  f32x4 acc[3][MB], accb = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kj = 0; kj < 3; ++kj)
+#pragma unroll
+    for (int ib = 0; ib < MB; ++ib) acc[kj][ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  CwPos nxt;
+  {
+    const int row = step_beg / g.col_blocks;
+    nxt.cbk = step_beg - row * g.col_blocks;
+    nxt.w0 = nxt.cbk * kCwTW;
+    nxt.n = row / H;
+    nxt.h = row - nxt.n * H;
+  }
+  if (steps > 0) {
+    stage(nxt, 0);
+    nxt.advance(g);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const int wl = 32 * sg + 8 * quad;  // this lane's first token within the step
+  const int ky = (wl >> 3) ^ col16;   // its chunk position in rows with (row & 15) = col16
+  // element index of the lane's first cat value per tap kj (row ki, plane col16)
+  int xel[3];
+#pragma unroll
+  for (int kj = 0; kj < 3; ++kj) xel[kj] = (ki * 16 + col16) * L::kXSD * L::kPerD + kCwPad + wl + kj - 1;
+  const int bib = cb;  // the gO block this workgroup sums for the bias
+  for (int s = 0; s < steps; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < steps) {
+      stage(nxt, buf ^ 1);
+      nxt.advance(g);
+    }
+    const uint32_t* __restrict__ bb = csm + buf * L::kBuf;
+    V bfr[MB][P];
+#pragma unroll
+    for (int ib = 0; ib < MB; ++ib)
+#pragma unroll
+      for (int pp = 0; pp < P; ++pp)
+        bfr[ib][pp] = __builtin_bit_cast(
+            V, *reinterpret_cast<const u32x4*>(bb + L::kYOff + ((pp * MB + ib) * 16 + col16) * L::kYD +
+                                               4 * ky));
+    if (do_bias) {
+      // grad_bias partials: ones x gO block bib (every row of D gets the sum)
+#pragma unroll
+      for (int ib = 0; ib < MB; ++ib)
+        if (ib == bib)
+#pragma unroll
+          for (int pp = 0; pp < P; ++pp) accb = M::mac1(ones, bfr[ib][pp], accb);
+    }
+#pragma unroll
+    for (int kj = 0; kj < 3; ++kj) {
+      float xv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[e] = cw_lds_elem<T>(bb, xel[kj] + e);
+      V afr[P];
+      M::pack(xv, afr);
+#pragma unroll
+      for (int ib = 0; ib < MB; ++ib) acc[kj][ib] = M::mac(afr, bfr[ib], acc[kj][ib]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // ---- fixed-order reduction over the segments through LDS: each segment's
+  //      waves write their sums to the segment's own slice; the store loop
+  //      adds the slices in segment order
+  constexpr int NO = MB * 16;
+  constexpr int RS = NO + 1;
+  constexpr int SL = 9 * 16 * RS;                           // floats of one slice
+  float* __restrict__ red = reinterpret_cast<float*>(csm);  // [segs][9 taps][16 ci][RS]
+  float* __restrict__ rb = red + kCwSegs * SL;              // [segs][16 co]
+#pragma unroll
+  for (int kj = 0; kj < 3; ++kj) {
+    const int t = ki * 3 + kj;
+#pragma unroll
+    for (int ib = 0; ib < MB; ++ib)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        red[sg * SL + (t * 16 + 4 * quad + e) * RS + ib * 16 + col16] = acc[kj][ib][e];
+  }
+  if (do_bias && quad == 0) rb[sg * 16 + col16] = accb[0];  // row 0 of D: the column sums
+  __syncthreads();
+  // rows (tap t, ci = cb*16 + c), columns co; partial [split][9][CI][C], or
+  // grad_weight[co][ci][t] directly
+  float* __restrict__ pwb = pw + (int64_t)split * 9 * CI * C;
+  const bool v4 = C % 4 == 0 && reinterpret_cast<uintptr_t>(pw) % 16 == 0;
+  for (int idx = tid; idx < 9 * 16 * NO / 4; idx += kCwThreads) {
+    const int q = 4 * idx;
+    const int t = q / (16 * NO);
+    const int rem2 = q - t * 16 * NO;
+    const int c = rem2 / NO, i = rem2 - c * NO;
+    const int ci = cb * 16 + c;
+    if (ci >= CI || i >= C) continue;
+    const float* __restrict__ sp = red + (t * 16 + c) * RS + i;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = ((sp[e] + sp[SL + e]) + sp[2 * SL + e]) + sp[3 * SL + e];
+    if (g.direct) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (i + e < C) dw_out[((int64_t)(i + e) * CI + ci) * 9 + t] = from_f<T>(v[e]);
+    } else {
+      float* __restrict__ dst = pwb + ((int64_t)t * CI + ci) * C + i;
+      if (v4) {
+        *reinterpret_cast<f32x4*>(dst) = (f32x4){v[0], v[1], v[2], v[3]};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (i + e < C) dst[e] = v[e];
+      }
+    }
+  }
+  if (cb < (C + 15) / 16 && tid < 16) {
+    const int co = cb * 16 + tid;
+    if (co < C) {
+      const float v = ((rb[tid] + rb[16 + tid]) + rb[32 + tid]) + rb[48 + tid];
+      if (g.direct)
+        db_out[co] = from_f<T>(v);
+      else
+        pb[(int64_t)split * C + co] = v;
+    }
+  }
+}
+
+// Fixed-order sum of the split partials into grad_weight[co][ci][t] and
+// grad_bias[co]; one output element per thread (partials read with the
+// split stride, coalesced over co).
+template <typename T>
+__global__ __launch_bounds__(256) void conv_wgrad_reduce_kernel(const float* __restrict__ pw,
+                                                                const float* __restrict__ pb,
+                                                                T* __restrict__ dw_out,
+                                                                T* __restrict__ db_out, int C,
+                                                                int CI, int splits) {
+  const int64_t per = (int64_t)9 * CI * C;
+  const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (item < per) {
+    // item = (t*CI + ci)*C + co
+    float v = 0.f;
+#pragma unroll 4
+    for (int s = 0; s < splits; ++s) v += pw[(int64_t)s * per + item];
+    const int64_t tc = item / C;
+    const int co = (int)(item - tc * C);
+    const int t = (int)(tc / CI), ci = (int)(tc - (int64_t)t * CI);
+    dw_out[((int64_t)co * CI + ci) * 9 + t] = from_f<T>(v);
+  } else if (item < per + C) {
+    const int co = (int)(item - per);
+    float v = 0.f;
+    for (int s = 0; s < splits; ++s) v += pb[(int64_t)s * C + co];
+    db_out[co] = from_f<T>(v);
+  }
+}
+
+// Zero fill (a kernel rather than a memset, so the call stays valid under
+// stream capture): `count` elements of T.
+template <typename T>
+__global__ __launch_bounds__(256) void cw_zero_kernel(T* __restrict__ p, int64_t count) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < count) p[i] = from_f<T>(0.f);
+}
+
+namespace {
+
+template <typename F>
+int cw_with_type(int dt, F&& f) {
+  switch (dt) {
+    case kF32:
+      return f(float());
+    case kBF16:
+      return f(bf16());
+    case kF16:
+      return f(f16());
+    default:
+      return kBadArgument;
+  }
+}
+
+template <typename F>
+int cw_with_mb(int mb, F&& f) {
+  switch (mb) {
+    case 1:
+      return f(std::integral_constant<int, 1>());
+    case 2:
+      return f(std::integral_constant<int, 2>());
+    case 3:
+      return f(std::integral_constant<int, 3>());
+    case 4:
+      return f(std::integral_constant<int, 4>());
+    default:
+      return kUnsupported;
+  }
+}
+
+void cw_geom(CwGeom& g, int64_t n, int64_t c, int64_t h, int64_t w) {
+  g.N = (int)n;
+  g.C = (int)c;
+  g.CI = (int)(4 * c);
+  g.H = (int)h;
+  g.W = (int)w;
+  g.cblocks = (int)((4 * c + 15) / 16);
+  g.col_blocks = (int)((w + kCwTW - 1) / kCwTW);
+  const int64_t steps = n * h * g.col_blocks;
+  int64_t splits = kCwMaxSplits;
+  if (splits > (steps + kCwMinSteps - 1) / kCwMinSteps) splits = (steps + kCwMinSteps - 1) / kCwMinSteps;
+  if (splits < 1) splits = 1;
+  g.steps = (int)steps;
+  g.steps_per_split = (int)((steps + splits - 1) / splits);
+  g.splits = (int)((steps + g.steps_per_split - 1) / g.steps_per_split);
+  g.direct = g.splits == 1;
+  g.x16 = 0;
+  g.g16 = 0;
+}
+
+int64_t cw_align(int64_t v) { return (v + 255) / 256 * 256; }
+
+int64_t cw_partial_bytes(const CwGeom& g) {
+  if (g.direct) return 0;
+  return (int64_t)g.splits * ((int64_t)9 * g.CI * g.C + g.C) * (int64_t)sizeof(float);
+}
+
+}  // namespace
+}  // namespace ddpm
+
+using namespace ddpm;
+
+extern "C" int64_t ddpm_fuse_conv_bwd_weight_workspace_bytes(int64_t n, int64_t c, int64_t h,
+                                                             int64_t w, int dtype) {
+  if (n <= 0 || c <= 0 || h <= 0 || w <= 0 || dtype < kF32 || dtype > kF16) return 0;
+  if (n * h * ((w + kCwTW - 1) / kCwTW) > 0x7fffffffLL) return 0;
+  CwGeom g;
+  cw_geom(g, n, c, h, w);
+  const int64_t pbytes = cw_partial_bytes(g);
+  // fp32: the bf16 hi / lo planes of grad_out follow the partials
+  return dtype == kF32 ? cw_align(pbytes) + n * 2 * c * h * w * 2 : pbytes;
+}
+
+extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, void* grad_weight,
+                                         void* grad_bias, void* workspace, int64_t workspace_bytes,
+                                         int64_t n, int64_t c, int64_t h, int64_t w, int dtype,
+                                         hipStream_t stream) {
+  if (dtype < kF32 || dtype > kF16) return kBadArgument;
+  if (n < 0 || c < 0 || h < 0 || w < 0) return kBadArgument;
+  if (c > 64) return kUnsupported;  // grad_out rows of all output planes are staged together
+  if (c == 0) return kOk;
+  if (!grad_weight || !grad_bias) return kBadArgument;
+  const int esz = dtype == kF32 ? 4 : 2;
+  if (n == 0 || h == 0 || w == 0) {
+    // an empty batch: zero gradients
+    return cw_with_type(dtype, [&](auto tag) {
+      using T = decltype(tag);
+      const int64_t nw = c * 4 * c * 9;
+      hipLaunchKernelGGL((cw_zero_kernel<T>), dim3((unsigned)((nw + 255) / 256)), dim3(256), 0,
+                         stream, (T*)grad_weight, nw);
+      hipLaunchKernelGGL((cw_zero_kernel<T>), dim3((unsigned)((c + 255) / 256)), dim3(256), 0,
+                         stream, (T*)grad_bias, (int64_t)c);
+      return (int)hipGetLastError();
+    });
+  }
+  if (!cat || !grad_out) return kBadArgument;
+  if (n * h * ((w + kCwTW - 1) / kCwTW) > 0x7fffffffLL) return kUnsupported;
+  // 32-bit buffer offsets inside one image's planes (fp32 grad_out: two 2-byte planes)
+  if (4 * c * h * w * esz > 0x7fffffffLL || 2 * c * h * w * 2 > 0x7fffffffLL) return kUnsupported;
+  CwGeom g;
+  cw_geom(g, n, c, h, w);
+  const int64_t pbytes = cw_partial_bytes(g);
+  const int64_t need = dtype == kF32 ? cw_align(pbytes) + n * 2 * c * h * w * 2 : pbytes;
+  if (need > 0 && (!workspace || workspace_bytes < need)) return kWorkspaceTooSmall;
+  uint16_t* gs = dtype == kF32 ? (uint16_t*)((char*)workspace + cw_align(pbytes)) : nullptr;
+  const uint16_t* gsrc = dtype == kF32 ? gs : (const uint16_t*)grad_out;
+  g.x16 = (w % (16 / esz) == 0) && ((uintptr_t)cat % 16 == 0);
+  g.g16 = (w % 8 == 0) && ((uintptr_t)gsrc % 16 == 0);
+  float* pw = g.direct ? nullptr : (float*)workspace;
+  float* pb = g.direct ? nullptr : pw + (int64_t)g.splits * 9 * 4 * c * c;
+  if (dtype == kF32) {
+    const int e = launch_ysplit((const float*)grad_out, gs, c * h * w, n * c * h * w, stream);
+    if (e != 0) return e;
+  }
+  const int mb = (int)((c + 15) / 16);
+  return cw_with_type(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    return cw_with_mb(mb, [&](auto mbc) {
+      constexpr int MB = decltype(mbc)::value;
+      typedef CwLds<T, MB> L;
+      const size_t stage = (size_t)2 * L::kBuf * 4;
+      const size_t red = (size_t)(kCwSegs * 9 * 16 * (MB * 16 + 1) + kCwSegs * 16) * sizeof(float);
+      const size_t lds = stage > red ? stage : red;
+      auto kern = conv_wgrad_partial_kernel<T, MB>;
+      const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
+      if (ae != 0) return ae;
+      hipLaunchKernelGGL(kern, dim3((unsigned)(g.splits * g.cblocks)), dim3(kCwThreads), lds, stream,
+                         (const T*)cat, gsrc, pw, pb, (T*)grad_weight, (T*)grad_bias, g);
+      int e = (int)hipGetLastError();
+      if (e != 0 || g.direct) return e;
+      const int64_t items = (int64_t)9 * 4 * c * c + c;
+      hipLaunchKernelGGL((conv_wgrad_reduce_kernel<T>), dim3((unsigned)((items + 255) / 256)),
+                         dim3(256), 0, stream, (const float*)pw, (const float*)pb, (T*)grad_weight,
+                         (T*)grad_bias, (int)c, (int)(4 * c), g.splits);
+      return (int)hipGetLastError();
+    });
+  });
+}

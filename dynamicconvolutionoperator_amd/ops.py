@@ -413,9 +413,11 @@ def _fuse_conv_workspace(c, dt, device):
 
 class _FuseConv3x3(torch.autograd.Function):
     """``F.conv2d(cat, weight, bias, padding=1)`` for the DDPM fuse
-    convolution: forward and input gradient as HIP implicit-GEMM MFMA kernels
-    (``ddpm_fuse_conv_fwd`` / ``_bwd_data``); the weight and bias gradients
-    through the library convolution."""
+    convolution as HIP MFMA kernels: forward and input gradient
+    (``ddpm_fuse_conv_fwd`` / ``_bwd_data``, implicit GEMMs over the input
+    planes), weight and bias gradients (``ddpm_fuse_conv_bwd_weight``, a
+    split pixel reduction; more than 64 output channels use the library's
+    backward-filter convolution)."""
 
     @staticmethod
     def forward(ctx, cat, weight, bias):
@@ -455,9 +457,21 @@ class _FuseConv3x3(torch.autograd.Function):
         need_w = ctx.needs_input_grad[1]
         need_b = ctx.has_bias and ctx.needs_input_grad[2]
         if need_w or need_b:
-            _, gw, gb = torch.ops.aten.convolution_backward(
-                grad_out, cat, weight, [c] if ctx.has_bias else None, [1, 1], [1, 1], [1, 1], False,
-                [0, 0], 1, [False, need_w, need_b])
+            dt = _dt(cat)
+            lib = _lib.load()
+            gw = torch.empty_like(weight)
+            gb = torch.empty((c,), dtype=cat.dtype, device=cat.device)
+            with torch.cuda.device(cat.device):
+                nbytes = int(lib.ddpm_fuse_conv_bwd_weight_workspace_bytes(n, c, h, w, dt))
+                ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=cat.device)
+                code = lib.ddpm_fuse_conv_bwd_weight(_ptr(cat), _ptr(grad_out), _ptr(gw), _ptr(gb),
+                                                     _ptr(ws), nbytes, n, c, h, w, dt, _stream(cat))
+            if code == _lib.STATUS_UNSUPPORTED:
+                _, gw, gb = torch.ops.aten.convolution_backward(
+                    grad_out, cat, weight, [c] if ctx.has_bias else None, [1, 1], [1, 1], [1, 1],
+                    False, [0, 0], 1, [False, need_w, need_b])
+            else:
+                _lib.check(code, "ddpm_fuse_conv_bwd_weight")
             grad_w = gw if need_w else None
             grad_b = gb if need_b else None
         return grad_cat, grad_w, grad_b

@@ -222,6 +222,23 @@ int ddpm_fuse_conv_bwd_data(const void* grad_out, const void* weight, void* grad
                             void* workspace, int64_t workspace_bytes, int64_t n, int64_t c,
                             int64_t h, int64_t w, int dtype, hipStream_t stream);
 
+/* Bytes of workspace ddpm_fuse_conv_bwd_weight needs for `dtype`: fp32
+ * split partials of the weight and bias gradients (none with one split),
+ * then for fp32 the bf16 hi / lo planes of grad_out. */
+int64_t ddpm_fuse_conv_bwd_weight_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w,
+                                                  int dtype);
+
+/* grad_weight[co][ci][ki][kj] = sum_{n,h,w} grad_out[n][co][h][w] *
+ *                               cat[n][ci][h+ki-1][w+kj-1]  (zero padding),
+ * grad_bias[co] = sum grad_out[n][co][h][w]; fp32 accumulation in at most 16
+ * pixel splits summed in split order (deterministic), rounded once to
+ * `dtype`; an empty batch writes zeros.  c <= 64 (kUnsupported beyond).
+ * Replaces the cuDNN backward-filter convolution of self.fuse (autograd of
+ * nn.Conv2d, triton_impl.py:294, 392). */
+int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, void* grad_weight,
+                              void* grad_bias, void* workspace, int64_t workspace_bytes, int64_t n,
+                              int64_t c, int64_t h, int64_t w, int dtype, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

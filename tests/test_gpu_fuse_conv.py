@@ -61,3 +61,22 @@ def test_fuse_conv_without_bias_and_fallback():
     # not a 4C -> C convolution: the library path
     wt2 = randn((8, 16, 3, 3), 922).to(DEV)
     assert not ops.fuse_conv_supported(cat[:, :16], wt2, None)
+
+
+def test_fuse_conv_weight_gradient_empty_batch_and_determinism():
+    """An empty batch gives zero weight / bias gradients; two runs of the split
+    weight gradient are bit-identical (fixed-order reduction)."""
+    wt = randn((8, 32, 3, 3), 930, scale=0.1).to(DEV).requires_grad_()
+    b = randn((8,), 931).to(DEV).requires_grad_()
+    cat = torch.zeros((0, 32, 9, 16), device=DEV, requires_grad=True)
+    ops.fuse_conv3x3(cat, wt, b).sum().backward()
+    assert wt.grad is not None and not wt.grad.any() and not b.grad.any()
+    cat = randn((2, 256, 64, 64), 932).to(DEV)
+    g = randn((2, 64, 64, 64), 933).to(DEV)
+    wt = randn((64, 256, 3, 3), 934, scale=0.02).to(DEV)
+    grads = []
+    for _ in range(2):
+        w2, b2 = wt.clone().requires_grad_(), torch.zeros(64, device=DEV, requires_grad=True)
+        ops.fuse_conv3x3(cat, w2, b2).backward(g)
+        grads.append((w2.grad.clone(), b2.grad.clone()))
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
