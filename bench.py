@@ -13,7 +13,8 @@ Also reported on the same line (``extra``):
   * bf16 training, fused inference (fp32 / bf16) at 256x256;
   * a per-entry-point breakdown of the fp32 and bf16 steps (HIP events around
     each C-ABI launch on its stream, in a separate pass after the headline
-    loop) and the ``roofline`` entry of the dominant HIP kernel;
+    loop: the fused generator entry points and the 3x3 fuse convolution's) and
+    the ``roofline`` entry of the dominant HIP kernel;
   * the dynamic filter's HBM bandwidth (forward, dX, dK; fp32 and bf16, K=3
     256x256, rotating buffer sets so repeats do not run out of the MALL);
   * 128x128 C=64 K=3 fp32 inference: filter-only ms and GB/s and fused
@@ -185,11 +186,16 @@ def work_per_launch(name, esize):
     E = B * C * H * W
     G = 3 * C * K * K
     gemm = 2.0 * B * H * W * C * G  # the generator contraction C -> 3CK^2
+    conv = 2.0 * B * H * W * C * 4 * C * 9
     table = {
         "ddpm_gen_fwd": ((6 * E + G * (C + 1)) * esize, gemm),  # x, y in; cat (4E) out
         "ddpm_gen_bwd_x": ((6 * E + G * (C + 1)) * esize, gemm),  # y, gO (4E) in; dX out
         "ddpm_gen_bwd_y": ((5 * E + G * C) * esize, gemm),  # x, gO branches (3E) in; dY out
         "ddpm_gen_bwd_w": ((5 * E) * esize + G * (C + 1) * esize, gemm),  # x, y, gO branches in
+        # the 3x3 fuse convolution 4C -> C: GEMMs of 2*N*H*W*C*4C*9 flops
+        "ddpm_fuse_conv_fwd": ((5 * E + 36 * C * C) * esize, conv),  # cat (4E) in, out (E)
+        "ddpm_fuse_conv_bwd_data": ((5 * E + 36 * C * C) * esize, conv),  # gO (E) in, d cat (4E)
+        "ddpm_fuse_conv_bwd_weight": ((5 * E + 36 * C * C) * esize, conv),  # cat, gO in
         "ddpm_filter_fwd": ((3 * K * K + 5) * E * esize, 0.0),
         "ddpm_filter_bwd_x": ((3 * K * K + 5) * E * esize, 0.0),
         "ddpm_filter_bwd_k": ((3 * K * K + 4) * E * esize, 0.0),
@@ -446,7 +452,12 @@ def kernel_mode(args):
     dw, db = torch.empty_like(wt), torch.empty_like(bs)
     wsb = max(int(lib.ddpm_gen_bwd_w_workspace_bytes(B, C, hw, hw, k, code)),
               int(lib.ddpm_gen_bwd_y_workspace_bytes(C, k)),
-              int(lib.ddpm_gen_bwd_x_workspace_bytes(B, C, hw, hw, k, *DIL)), 1)
+              int(lib.ddpm_gen_bwd_x_workspace_bytes(B, C, hw, hw, k, *DIL)),
+              int(lib.ddpm_fuse_conv_workspace_bytes(C, code)),
+              int(lib.ddpm_fuse_conv_bwd_weight_workspace_bytes(B, C, hw, hw, code)), 1)
+    cw = rnd(C, 4 * C, 3, 3) * 0.02
+    cb, dcw, dcb = rnd(C), torch.empty(C, 4 * C, 3, 3, device="cuda", dtype=dt), torch.empty(C, device="cuda", dtype=dt)
+    cout = torch.empty(B, C, hw, hw, device="cuda", dtype=dt)
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
@@ -467,6 +478,15 @@ def kernel_mode(args):
                                                              code, code, s),
         "ddpm_filter_bwd_k": lambda t: lib.ddpm_filter_bwd_k(ptr(t["x"]), ptr(t["go"]), ptr(dk), *shp, code,
                                                              code, s),
+        # the fuse convolution: the 4C-plane tensor go stands in for the concat
+        "ddpm_fuse_conv_fwd": lambda t: lib.ddpm_fuse_conv_fwd(ptr(t["go"]), ptr(cw), ptr(cb), ptr(cout),
+                                                               ptr(ws), wsb, B, C, hw, hw, code, s),
+        "ddpm_fuse_conv_bwd_data": lambda t: lib.ddpm_fuse_conv_bwd_data(ptr(t["x"]), ptr(cw), ptr(out),
+                                                                         ptr(ws), wsb, B, C, hw, hw,
+                                                                         code, s),
+        "ddpm_fuse_conv_bwd_weight": lambda t: lib.ddpm_fuse_conv_bwd_weight(ptr(t["go"]), ptr(t["x"]),
+                                                                             ptr(dcw), ptr(dcb), ptr(ws),
+                                                                             wsb, B, C, hw, hw, code, s),
         "copy": lambda t: (dst.copy_(src), 0)[1],
     }
     names = args.kernel.split(",")
@@ -531,7 +551,7 @@ def main():
     from dynamicconvolutionoperator_amd import _lib
 
     lib = _lib.load()
-    entries = [n for n in _lib.SIGNATURES if n.startswith(("ddpm_gen_fwd", "ddpm_gen_bwd_x", "ddpm_gen_bwd_y", "ddpm_gen_bwd_w", "ddpm_filter_", "ddpm_gen_kernels"))]
+    entries = [n for n in _lib.SIGNATURES if n.startswith(("ddpm_gen_fwd", "ddpm_gen_bwd_x", "ddpm_gen_bwd_y", "ddpm_gen_bwd_w", "ddpm_filter_", "ddpm_gen_kernels", "ddpm_fuse_conv"))]
     entries = [n for n in entries if not n.endswith(("_workspace_bytes", "_supported", "_scratch_bytes"))]
 
     # ---- headline: fp32 fused recompute training step, uninstrumented
@@ -675,7 +695,7 @@ def main():
             "kernel_size": K,
             "height": H,
             "width": W,
-            "route": "fused generator (HIP) + 3x3 fuse conv (MIOpen)",
+            "route": "fused generator + 3x3 fuse convolution, all HIP kernels",
             "parallelism": "single GPU",
         },
         "roofline": roofline,
