@@ -21,9 +21,10 @@ Also reported on the same line (``extra``):
     end-to-end ms (gpu_bench.py:94-118);
   * K=5 128x128 C=64 bf16 on the materialized route: inference and
     forward+backward ms (gpu_bench.py:265-345);
-  * peak temporary memory of the fused and Unfold training steps, each route
-    in its own child process started before this process uses the GPU, with
-    gradients released before the baseline is read (gpu_memory_bench.py:47-76);
+  * peak temporary memory of the fused and Unfold training steps (C = 64 fp32
+    and bf16, C = 128 fp32), each route in its own child process started
+    before this process uses the GPU, with gradients released before the
+    baseline is read (gpu_memory_bench.py:47-76);
   * the Unfold route's GPU step time.
 ``cpu_baseline``: the reference's CPU path, timed on this host's cores in
 the same run -- the CPU branch of the drop-in module (streaming with
@@ -73,28 +74,29 @@ def parse_args():
     p.add_argument("--peak-mem", nargs=2, metavar=("ROUTE", "DTYPE"),
                    help="child mode: peak temporary memory of one training step of ROUTE "
                    "(fused|unfold) in DTYPE (float32|bfloat16); prints one JSON line")
+    p.add_argument("--channels", type=int, default=C, help="with --peak-mem: C")
     p.add_argument("--cpu-budget", type=float, default=12.0,
                    help="seconds per CPU-baseline leg at most (after its warm-up)")
     return p.parse_args()
 
 
 # --------------------------------------------------------------------------- helpers
-def make_inputs(dtype, seed=21, grad=True):
+def make_inputs(dtype, seed=21, grad=True, channels=C):
     import torch
 
     torch.manual_seed(seed)
-    x = torch.randn(B, C, H, W, device="cuda", dtype=dtype, requires_grad=grad)
-    y = torch.randn(B, C, H, W, device="cuda", dtype=dtype, requires_grad=grad)
+    x = torch.randn(B, channels, H, W, device="cuda", dtype=dtype, requires_grad=grad)
+    y = torch.randn(B, channels, H, W, device="cuda", dtype=dtype, requires_grad=grad)
     return x, y
 
 
-def make_module(dtype, fused=True):
+def make_module(dtype, fused=True, channels=C):
     import torch
 
     from dynamicconvolutionoperator_amd import DDPM
 
     torch.manual_seed(21)
-    return DDPM(C, K, fused_generator_training=fused).cuda().to(dtype).train()
+    return DDPM(channels, K, fused_generator_training=fused).cuda().to(dtype).train()
 
 
 def train_step(module, x, y):
@@ -284,15 +286,15 @@ def unfold_route_step(params, x, y):
     return F.conv2d(torch.cat(outs, 1), fw, fb, padding=1)
 
 
-def peak_mem_child(route, dtype_name, warmup=2):
+def peak_mem_child(route, dtype_name, channels=C, warmup=2):
     """Child mode: one route's peak temporary memory, measured as the
     reference's gpu_memory_bench.py:47-76 does (warm-up, gradients released,
     empty cache, reset peak, baseline, one step)."""
     import torch
 
     dtype = {"float32": torch.float32, "bfloat16": torch.bfloat16}[dtype_name]
-    module = make_module(dtype)
-    x, y = make_inputs(dtype)
+    module = make_module(dtype, channels=channels)
+    x, y = make_inputs(dtype, channels=channels)
     params = list(module.parameters())
 
     def step():
@@ -314,20 +316,24 @@ def peak_mem_child(route, dtype_name, warmup=2):
     step()
     torch.cuda.synchronize()
     peak = torch.cuda.max_memory_allocated()
-    print(json.dumps({"route": route, "dtype": dtype_name, "baseline_mib": base / 2**20,
+    print(json.dumps({"route": route, "dtype": dtype_name, "channels": channels,
+                      "baseline_mib": base / 2**20,
                       "peak_mib": peak / 2**20, "temporary_peak_mib": (peak - base) / 2**20}))
 
 
 def peak_memory_children():
-    """Runs peak_mem_child for each (route, dtype) in its own process."""
+    """Runs peak_mem_child for each (route, dtype) in its own process: C = 64
+    in fp32 and bf16, and C = 128 in fp32 (the widest fused channel count)."""
     import subprocess
 
     out = {}
-    for dtype_name, key in (("float32", "fp32"), ("bfloat16", "bf16")):
+    for dtype_name, key, channels in (("float32", "fp32", C), ("bfloat16", "bf16", C),
+                                      ("float32", "fp32_c128", 128)):
         res = {}
         for route in ("fused", "unfold"):
             proc = subprocess.run(
-                [sys.executable, os.path.abspath(__file__), "--peak-mem", route, dtype_name],
+                [sys.executable, os.path.abspath(__file__), "--peak-mem", route, dtype_name,
+                 "--channels", str(channels)],
                 capture_output=True, text=True, timeout=300,
             )
             if proc.returncode != 0:
@@ -533,7 +539,7 @@ def main():
     import torch
 
     if args.peak_mem:
-        peak_mem_child(*args.peak_mem)
+        peak_mem_child(*args.peak_mem, channels=args.channels)
         return
     # device_count() does not initialise the GPU: the peak-memory children
     # below start before this process uses it

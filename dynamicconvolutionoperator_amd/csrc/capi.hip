@@ -1,6 +1,6 @@
 // Library-level C-ABI helpers: status strings, ABI version, support queries,
 // and the host-side launch helper shared by every entry point.
-#include "gen_common.h"
+#include "gen_tile.h"
 
 #include <map>
 #include <mutex>
@@ -52,14 +52,17 @@ extern "C" const char* ddpm_status_string(int code) {
 // this channel count, kernel size and largest dilation, else 0 (the caller
 // then materializes the dynamic kernels and uses the ddpm_filter_* entry
 // points).  The backward kernels stage a column halo of kGenMaxDil pixels,
-// and the forward's halo tile (16+2R) x (32+2R) pixels x 16 channels, R =
-// (K/2)*max_dilation, must fit the 160 KB of LDS of one workgroup.
+// and the 32-column tile's halo tile (16+2R) x (32+2R) pixels x 16 channels
+// (fp32 entries, R = (K/2)*max_dilation) must fit the LDS of one workgroup
+// next to two fp32 weight slices.
 extern "C" int ddpm_gen_supported(int64_t c, int kernel_size, int max_dilation) {
-  if (c < 1 || c > 64 || !(kernel_size == 1 || kernel_size == 3) || max_dilation < 1) return 0;
+  if (c < 1 || c > 128 || !(kernel_size == 1 || kernel_size == 3) || max_dilation < 1) return 0;
   if (kernel_size == 1) return 1;
   if (max_dilation > kGenMaxDil) return 0;
-  const int64_t r = (int64_t)(kernel_size / 2) * max_dilation;
-  const int64_t plane = ((16 + 2 * r) * (32 + 2 * r) * 4 * 4 + 255) / 256 * 256;
-  const int64_t lds = 4 * plane + 2 * 2 * 2 * 64 * 16 + 3 * kernel_size * kernel_size * 16 * 4;
-  return lds <= 160 * 1024 ? 1 : 0;
+  GenGeom gg;
+  if (gen_make_geom(gg, 1, c, 1, 1, kernel_size, max_dilation, max_dilation, max_dilation) != kOk)
+    return 0;
+  TileGeom g;
+  size_t lds = 0;
+  return tile_geom(g, gg, 16, 2, 2, lds) == kOk ? 1 : 0;
 }

@@ -9,7 +9,7 @@
 //   db[(b,c,t)]    = sum_p dK[(b,c,t), p]
 //
 // Work decomposition (CDNA4): one workgroup per (token split, branch b,
-// 16-channel block of c).  Splits are equal ranges of steps -- one step is
+// 16-channel block of c, and above 64 channels half of the input channels i).  Splits are equal ranges of steps -- one step is
 // one row segment of 128 columns -- at most 16 of them (the reference's
 // bound, :1001-1005) and at least 4 steps each (16 splits x 3 branches x 4
 // channel blocks = 192 workgroups at C = 64, 256x256); they write fp32
@@ -46,6 +46,7 @@ struct WGradGeom {
   int N, C, H, W;
   int d0, d1, d2;
   int cblocks;         // ceil(C / 16)
+  int ihalves;         // 1, or 2 when C > 64: a workgroup covers 16*MB input channels i
   int col_blocks;      // ceil(W / kWgTW)
   int splits;
   int steps;           // N * H * col_blocks
@@ -175,11 +176,14 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
   extern __shared__ __attribute__((aligned(16))) uint32_t wsm[];
 
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int ih = logical % g.ihalves;
+  const int lg = logical / g.ihalves;
   const int per_split = 3 * g.cblocks;
-  const int split = logical / per_split;
-  const int rem = logical - split * per_split;
+  const int split = lg / per_split;
+  const int rem = lg - split * per_split;
   const int b = rem / g.cblocks;
   const int cb = rem - b * g.cblocks;
+  const int i0 = ih * MB * 16;  // first input channel of this workgroup
   const int d = dil_of(b, g.d0, g.d1, g.d2);
   const int C = g.C, H = g.H, W = g.W;
   const int64_t HW = (int64_t)H * W;
@@ -223,7 +227,8 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
       const int row = ii * YRPC + lane / L::kYC, pos = lane % L::kYC;
       const int part = row / (MB * 16), i = row - part * (MB * 16);
       cpc[j] = (pos ^ (i & 15)) * 8;
-      if (i < C) cpo[j] = ((uint32_t)(part * C + i) * (uint32_t)HW + (uint32_t)cpc[j]) * 2u;
+      if (i0 + i < C)
+        cpo[j] = ((uint32_t)(part * C + i0 + i) * (uint32_t)HW + (uint32_t)cpc[j]) * 2u;
     } else if (ii < NY + NG) {
       const int row = (ii - NY) * GRPC + lane / L::kGC, pos = lane % L::kGC;
       cpc[j] = (pos ^ (row & 15)) * PC;
@@ -349,8 +354,9 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
           const int part = row / (MB * 16), i = row - part * (MB * 16);
           const int w = p.w0 + j;
           const uint32_t off =
-              (i < C && w < W) ? ((uint32_t)(part * C + i) * (uint32_t)HW + rowel + (uint32_t)w) * 2u
-                               : kOob;
+              (i0 + i < C && w < W)
+                  ? ((uint32_t)(part * C + i0 + i) * (uint32_t)HW + rowel + (uint32_t)w) * 2u
+                  : kOob;
           const int kc = (j >> 3) ^ (i & 15);
           dy[row * L::kYD * 2 + kc * 8 + (j & 7)] =
               (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(yres, off, 0, 0);
@@ -521,10 +527,10 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
     const int q = 4 * idx;
     const int t = q / (16 * NO);
     const int rem2 = q - t * 16 * NO;
-    const int c = rem2 / NO, i = rem2 - c * NO;
-    const int ch = cb * 16 + c;
+    const int c = rem2 / NO, il = rem2 - c * NO;
+    const int ch = cb * 16 + c, i = i0 + il;
     if (ch >= C || i >= C) continue;
-    const float* __restrict__ sp = red + (t * 16 + c) * RS + i;
+    const float* __restrict__ sp = red + (t * 16 + c) * RS + il;
     float v[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = ((sp[e] + sp[SL + e]) + sp[2 * SL + e]) + sp[3 * SL + e];
@@ -544,7 +550,8 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
       }
     }
   }
-  for (int idx = tid; idx < KK * 16; idx += NT) {
+  // the bias gradient: once, by the first input-channel half
+  for (int idx = tid; idx < (ih == 0 ? KK * 16 : 0); idx += NT) {
     const int t = idx >> 4, c = idx & 15;
     const int ch = cb * 16 + c;
     if (ch >= C) continue;
@@ -663,6 +670,7 @@ void wgrad_geom(WGradGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int d0
   g.d1 = d1;
   g.d2 = d2;
   g.cblocks = (int)((c + 15) / 16);
+  g.ihalves = c > 64 ? 2 : 1;
   g.col_blocks = (int)((w + kWgTW - 1) / kWgTW);
   const int64_t steps = n * h * g.col_blocks;
   int64_t splits = kWgMaxSplits;
@@ -731,7 +739,7 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
   g.xdma = (esz == 4) || ((w % 2 == 0) && ((uintptr_t)x % 4 == 0));
   g.x16 = (w % (16 / esz) == 0) && ((uintptr_t)x % 16 == 0);
   g.x4 = (w % 8 == 0) && ((uintptr_t)ysrc % 16 == 0) && ((uintptr_t)grad_out % 16 == 0);
-  const int mb = (int)((c + 15) / 16);
+  const int mb = c > 64 ? 4 : (int)((c + 15) / 16);  // 16-channel blocks of i per workgroup
   const int kk = kernel_size * kernel_size;
   float* pw = g.direct ? nullptr : (float*)workspace;
   float* pb = g.direct ? nullptr : pw + (int64_t)g.splits * 3 * kk * c * c;
@@ -749,7 +757,7 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
       const size_t stage = (size_t)2 * L::kBuf * 4;
       const size_t red = (size_t)(kWgSegs * KKc * 16 * (MB * 16 + 1) + KKc * kWgSegs * 16) * sizeof(float);
       const size_t lds = stage > red ? stage : red;
-      const dim3 grid((unsigned)(g.splits * 3 * g.cblocks));
+      const dim3 grid((unsigned)(g.splits * 3 * g.cblocks * g.ihalves));
       const int ae = allow_dynamic_lds(
           reinterpret_cast<const void*>(&gen_bwd_w_partial_kernel<T, KS, MB>), lds);
       if (ae != 0) return ae;

@@ -28,7 +28,7 @@
 namespace ddpm {
 
 template <typename T, int KS, int NK, int CB>
-__global__ __launch_bounds__(kGtThreads) __attribute__((amdgpu_waves_per_eu(CB == 4 ? 2 : 4))) void gen_bwd_x_tile_kernel(
+__global__ __launch_bounds__(kGtThreads) __attribute__((amdgpu_waves_per_eu(gt_waves_per_eu<T, NK, CB>()))) void gen_bwd_x_tile_kernel(
     const T* __restrict__ gout, const T* __restrict__ y, const T* __restrict__ wt,
     const T* __restrict__ bias, float* __restrict__ part, TileGeom g) {
   gen_tile_body<T, KS, NK, CB, true>(gout, y, wt, bias, nullptr, part, g);
@@ -112,12 +112,13 @@ int xt_with_type(int dt, F&& f) {
 
 // Tiling of the scatter kernel: 64-column tiles when the fp32 accumulator
 // tile (16 bytes per 4-channel pixel) fits the LDS next to fp32 weight
-// slices, else 32 columns.  The choice ignores the dtype so that the
-// workspace size depends on the shape alone.
+// slices and the fp32 y operand fits the registers, else 32 columns.  The
+// choice ignores the dtype so that the workspace size depends on the shape
+// alone.
 int bx_geom(TileGeom& g, const GenGeom& gg, int& cb, size_t& lds) {
-  cb = 4;
+  cb = gt_first_cb(gt_nk(gg.C));
   int st = tile_geom(g, gg, 16, 2, cb, lds);
-  if (st == kUnsupported) {
+  if (st == kUnsupported && cb == 4) {
     cb = 2;
     st = tile_geom(g, gg, 16, 2, cb, lds);
   }
@@ -171,7 +172,7 @@ extern "C" int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bia
   if (st != kOk) return st;
   if (!workspace || workspace_bytes < bx_part_bytes(g)) return kWorkspaceTooSmall;
   float* part = (float*)workspace;
-  const int nk = (int)((c + 31) / 32);
+  const int nk = gt_nk((int)c);
   return xt_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
     auto launch = [&](auto kern) {
@@ -191,8 +192,11 @@ extern "C" int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bia
                            (const float*)part, (const T*)grad_out, (T*)grad_x, g);
       return (int)hipGetLastError();
     };
+    // 1 or 2 chunks of 32 input channels, or 4 (65..128 channels, always
+    // 32-column tiles; chunks past C read zeros)
     auto pick = [&](auto ks) {
       constexpr int KS = decltype(ks)::value;
+      if (nk > 2) return launch(gen_bwd_x_tile_kernel<T, KS, 4, 2>);
       if (cb == 4)
         return nk == 1 ? launch(gen_bwd_x_tile_kernel<T, KS, 1, 4>)
                        : launch(gen_bwd_x_tile_kernel<T, KS, 2, 4>);

@@ -8,8 +8,10 @@
 //
 // A GEMM with M = i, N = pixels and K = (b, t, c) whose B operand dK is
 // formed on chip and never stored.  Work decomposition (CDNA4):
-//   * one workgroup per image-row segment of 256 pixels; 8 waves, two per
-//     SIMD, each owning 32 pixels (two MFMA column blocks) x all C i;
+//   * one workgroup per image-row segment of 256 pixels (and, above 64
+//     channels, per half of the output channels i); 8 waves, two per SIMD,
+//     each owning 32 pixels (two MFMA column blocks) x all C i (x the
+//     workgroup's 64 i);
 //   * the K loop runs in stages (branch b, 32-channel chunk, tap row ki): a
 //     stage needs one x row (h + dh) of 32 channels, 256 + 16 columns, and
 //     the K-slice of the weight for its K taps; both are copied global -> LDS
@@ -45,12 +47,14 @@ struct YGeom {
   int d0, d1, d2;
   int col_tiles;  // ceil(W / kYtTW)
   int nc32;       // ceil(C / 32)
+  int ihalves;    // 1, or 2 when C > 64: workgroups per segment, 16*MB output channels each
   int x4;         // x rows can be copied in 16-byte lanes (W % 8 == 0, aligned base)
 };
 
 // Packed weight for the A fragments: 16-byte units
-//   [b][cc][t][ib][part][lane]   lane (i = ib*16 + (lane & 15), q = lane >> 4)
-// holding W[(b*C + c)*KK + t][i] for c = cc*32 + 4*e + q, e = 0..7.
+//   [ih][b][cc][t][ib][part][lane]   lane (i = (ih*MB + ib)*16 + (lane & 15),
+//   q = lane >> 4) holding W[(b*C + c)*KK + t][i] for c = cc*32 + 4*e + q,
+//   e = 0..7 (ih: the output-channel half of a workgroup; ib < MB).
 template <typename T>
 __host__ __device__ constexpr int yt_parts() {
   return sizeof(T) == 4 ? 2 : 1;
@@ -59,10 +63,10 @@ __host__ __device__ constexpr int yt_parts() {
 template <typename T, int KS, int MB>
 __global__ __launch_bounds__(256) void gen_pack_wt_kernel(const T* __restrict__ wt,
                                                           uint32_t* __restrict__ pk, int C,
-                                                          int nc32) {
+                                                          int nc32, int ihalves) {
   constexpr int KK = KS * KS;
   constexpr int P = yt_parts<T>();
-  const int total = 3 * nc32 * KK * MB * 64;
+  const int total = ihalves * 3 * nc32 * KK * MB * 64;
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= total) return;
   const int lane = idx & 63;
@@ -72,8 +76,10 @@ __global__ __launch_bounds__(256) void gen_pack_wt_kernel(const T* __restrict__ 
   const int t = rest % KK;
   rest /= KK;
   const int cc = rest % nc32;
-  const int b = rest / nc32;
-  const int i = ib * 16 + (lane & 15), q = lane >> 4;
+  rest /= nc32;
+  const int b = rest % 3;
+  const int ih = rest / 3;
+  const int i = (ih * MB + ib) * 16 + (lane & 15), q = lane >> 4;
   float v[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -83,7 +89,7 @@ __global__ __launch_bounds__(256) void gen_pack_wt_kernel(const T* __restrict__ 
   typename Mma<T>::V o[P];
   Mma<T>::pack(v, o);
   u32x4* __restrict__ dst = reinterpret_cast<u32x4*>(pk);
-  const int64_t unit = ((((int64_t)(b * nc32 + cc) * KK + t) * MB + ib) * P) * 64 + lane;
+  const int64_t unit = (((((int64_t)ih * 3 + b) * nc32 + cc) * KK + t) * MB + ib) * P * 64 + lane;
 #pragma unroll
   for (int part = 0; part < P; ++part) dst[unit + part * 64] = __builtin_bit_cast(u32x4, o[part]);
 }
@@ -119,7 +125,9 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
   constexpr int E = (int)sizeof(T);
   extern __shared__ __attribute__((aligned(16))) uint32_t ysm[];
 
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int ih = logical % g.ihalves;  // output channels (ih*MB + ib)*16 + ...
+  const int tile = logical / g.ihalves;
   const int row = tile / g.col_tiles;  // image row n*H + h
   const int w0 = (tile - row * g.col_tiles) * kYtTW;
   const int n = row / g.H, h = row - n * g.H;
@@ -177,7 +185,7 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
       }
     }
     // weight slice of the stage's K taps: contiguous in the packed weight
-    const uint32_t* src = pk + (int64_t)((bc * KK + ki * KS) * MB * P * 64) * 4;
+    const uint32_t* src = pk + (int64_t)(((ih * 3 * g.nc32 + bc) * KK + ki * KS) * MB * P * 64) * 4;
     const BufRes pres = make_buf(src, (uint32_t)(L::kAUnits * 16));
 #pragma unroll
     for (int j = 0; j < (L::kAUnits / 64 + kYtWaves - 1) / kYtWaves; ++j) {
@@ -275,7 +283,7 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
       for (int ib = 0; ib < MB; ++ib)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int i = ib * 16 + 4 * quad + e;
+          const int i = (ih * MB + ib) * 16 + 4 * quad + e;
           if (i < C) yo[(int64_t)i * HW] = from_f<T>(acc[blk][ib][e]);
         }
     }
@@ -314,9 +322,17 @@ int yt_with_mb(int mb, F&& f) {
   }
 }
 
+// Output-channel halves per row segment and 16-channel blocks per half.
+void yt_split(int64_t c, int& ihalves, int& mb) {
+  ihalves = c > 64 ? 2 : 1;
+  mb = c > 64 ? 4 : (int)((c + 15) / 16);
+}
+
 int64_t yt_pack_bytes(int64_t c, int k, int dtype) {
-  const int64_t nc32 = (c + 31) / 32, mb = (c + 15) / 16;
-  return 3 * nc32 * (int64_t)k * k * mb * (dtype == kF32 ? 2 : 1) * 64 * 16;
+  int ih, mb;
+  yt_split(c, ih, mb);
+  const int64_t nc32 = (c + 31) / 32;
+  return (int64_t)ih * 3 * nc32 * k * k * mb * (dtype == kF32 ? 2 : 1) * 64 * 16;
 }
 
 // Validates the arguments of both dY entry points; kOk, an error, or
@@ -336,7 +352,7 @@ int yt_check(const void* x, const void* weight, const void* grad_out, void* grad
   if (gg.d0 > kYtMaxDil || gg.d1 > kYtMaxDil || gg.d2 > kYtMaxDil) return kUnsupported;
   // 32-bit buffer offsets inside one image's [C][H][W] planes
   if (c * h * w * (dtype == kF32 ? 4 : 2) > 0x7fffffffLL) return kUnsupported;
-  if (n * h * ((w + kYtTW - 1) / kYtTW) > 0x7fffffffLL) return kUnsupported;
+  if (2 * n * h * ((w + kYtTW - 1) / kYtTW) > 0x7fffffffLL) return kUnsupported;
   return kOk;
 }
 
@@ -389,7 +405,7 @@ int scratch_address(void** out) {
 using namespace ddpm;
 
 extern "C" int64_t ddpm_gen_bwd_y_workspace_bytes(int64_t c, int kernel_size) {
-  if (c <= 0 || c > 64 || kernel_size < 1) return 0;
+  if (c <= 0 || c > 128 || kernel_size < 1) return 0;
   return yt_pack_bytes(c, kernel_size, kF32);
 }
 
@@ -444,8 +460,9 @@ int yt_launch(const void* x, const void* weight, const void* grad_out, void* gra
   g.col_tiles = (int)((w + kYtTW - 1) / kYtTW);
   g.nc32 = (int)((c + 31) / 32);
   g.x4 = (w % 8 == 0) && ((uintptr_t)x % 16 == 0);
-  const int64_t tiles = n * h * g.col_tiles;  // below 2^31 (yt_check)
-  const int mb = (int)((c + 15) / 16);
+  int mb;
+  yt_split(c, g.ihalves, mb);
+  const int64_t tiles = n * h * g.col_tiles * g.ihalves;  // below 2^31 (yt_check)
   return yt_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
     return yt_with_mb(mb, [&](auto mbc) {
@@ -453,9 +470,10 @@ int yt_launch(const void* x, const void* weight, const void* grad_out, void* gra
       auto launch = [&](auto ks) {
         constexpr int KS = decltype(ks)::value;
         typedef YtLds<T, KS, MB> L;
-        const int units = 3 * g.nc32 * KS * KS * MB * 64;
+        const int units = g.ihalves * 3 * g.nc32 * KS * KS * MB * 64;
         hipLaunchKernelGGL((gen_pack_wt_kernel<T, KS, MB>), dim3((units + 255) / 256), dim3(256), 0,
-                           stream, (const T*)weight, (uint32_t*)workspace, (int)c, g.nc32);
+                           stream, (const T*)weight, (uint32_t*)workspace, (int)c, g.nc32,
+                           g.ihalves);
         int e = (int)hipGetLastError();
         if (e != 0) return e;
         const size_t lds = (size_t)2 * L::kBuf * 4;

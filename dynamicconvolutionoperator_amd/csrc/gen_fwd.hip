@@ -19,9 +19,10 @@
 namespace ddpm {
 
 // CB = 4: 256 registers per lane (one 8-wave workgroup per CU, whose 133 KB
-// halo tile fills the LDS anyway); CB = 2: 128 registers, two workgroups per CU.
+// halo tile fills the LDS anyway); CB = 2: 128 registers, two workgroups per
+// CU, unless the y operand needs more (gt_waves_per_eu).
 template <typename T, int KS, int NK, int CB>
-__global__ __launch_bounds__(kGtThreads) __attribute__((amdgpu_waves_per_eu(CB == 4 ? 2 : 4))) void gen_fwd_kernel(
+__global__ __launch_bounds__(kGtThreads) __attribute__((amdgpu_waves_per_eu(gt_waves_per_eu<T, NK, CB>()))) void gen_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ wt,
     const T* __restrict__ bias, T* __restrict__ out, TileGeom g) {
   gen_tile_body<T, KS, NK, CB, false>(x, y, wt, bias, out, nullptr, g);
@@ -50,7 +51,7 @@ int gen_make_geom(GenGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int k,
                   int d2) {
   if (n < 0 || c < 0 || h < 0 || w < 0) return kBadArgument;
   if (k < 1 || (k % 2) == 0 || d0 < 1 || d1 < 1 || d2 < 1) return kBadArgument;
-  if (k > 3 || c > 64) return kUnsupported;
+  if (k > 3 || c > 128) return kUnsupported;
   if (h > (1 << 20) || w > (1 << 20) || h * w > ((int64_t)1 << 31)) return kUnsupported;
   if (k == 1) d0 = d1 = d2 = 1;  // a 1x1 tap has no neighbour to dilate
   g.N = (int)n;
@@ -85,18 +86,19 @@ extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, co
   // 32-bit buffer offsets inside one image's [C][H][W] planes (and 16 planes
   // past a channel block's first one)
   if (c * h * w * esz > 0x7fffffffLL || 16 * h * w * esz > 0x7fffffffLL) return kUnsupported;
-  // 64-column tiles when their halo tile fits the LDS, else 32 columns
+  // 64-column tiles when their halo tile fits the LDS (and the y operand the
+  // registers), else 32 columns
   TileGeom g;
   size_t lds = 0;
   const int parts = esz == 4 ? 2 : 1;
-  int cb = 4;
+  const int nk = gt_nk((int)c);
+  int cb = gt_first_cb(nk);
   st = tile_geom(g, gg, 4 * esz, parts, cb, lds);
-  if (st == kUnsupported) {
+  if (st == kUnsupported && cb == 4) {
     cb = 2;
     st = tile_geom(g, gg, 4 * esz, parts, cb, lds);
   }
   if (st != kOk) return st;
-  const int nk = (int)((c + 31) / 32);
   return with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
     auto launch = [&](auto kern) {
@@ -107,8 +109,13 @@ extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, co
                          (const T*)weight, (const T*)bias, (T*)out, g);
       return (int)hipGetLastError();
     };
+    // 1 or 2 chunks of 32 input channels, or 4 (65..128 channels; chunks
+    // past C read zeros)
     auto pick = [&](auto ks) {
       constexpr int KS = decltype(ks)::value;
+      if (nk > 2) {
+        return launch(gen_fwd_kernel<T, KS, 4, 2>);  // 32-column tiles
+      }
       if (cb == 4)
         return nk == 1 ? launch(gen_fwd_kernel<T, KS, 1, 4>) : launch(gen_fwd_kernel<T, KS, 2, 4>);
       return nk == 1 ? launch(gen_fwd_kernel<T, KS, 1, 2>) : launch(gen_fwd_kernel<T, KS, 2, 2>);

@@ -55,6 +55,24 @@ struct TileGeom {
   int vec;      // W % 4 == 0: 4-column groups at positions 4k are whole inside or outside the image
 };
 
+// Waves per SIMD the tile kernels are compiled for: two (256 registers per
+// lane) for the 64-column tile and for 65..128 input channels (NK = 4: the y
+// operand alone takes 64 registers per 2-byte column block pair, 128 for
+// fp32), else four.
+template <typename T, int NK, int CB>
+constexpr int gt_waves_per_eu() {
+  return (CB == 4 || NK == 4) ? 2 : 4;
+}
+
+// Column blocks of 16 pixels per tile row the tile kernels try first: the y
+// operand of the 64-column tile with more than 64 input channels (NK = 4)
+// would not fit the registers, so those use 32 columns.
+inline int gt_first_cb(int nk) { return nk > 2 ? 2 : 4; }
+
+// Chunks of 32 input channels the tile kernels are instantiated for: 1, 2,
+// or 4 for 65..128 channels (chunks past C hold zeros).
+inline int gt_nk(int c) { return c <= 32 ? 1 : (c <= 64 ? 2 : 4); }
+
 // Tiling and LDS bytes for a tile of 16 x 16*cb pixels whose LDS tile holds
 // `entry` bytes per 4-channel pixel and whose weight slices have `parts`
 // parts; kUnsupported when it does not fit the LDS.
@@ -80,7 +98,7 @@ inline int tile_geom(TileGeom& f, const GenGeom& g, int entry, int parts, int cb
   // planes start on 256-byte boundaries: the four quads of a wave then read
   // their 4-channel entries with the fewest LDS bank conflicts (measured)
   f.plane = (f.npix * entry + 255) / 256 * 256;
-  const int nk = (g.C + 31) / 32;
+  const int nk = gt_nk(g.C);
   lds = (size_t)4 * f.plane + (size_t)2 * nk * parts * 64 * 16 + (size_t)3 * g.K * g.K * 16 * 4;
   if (lds > (size_t)kGtMaxLds) return kUnsupported;
   if ((int64_t)f.tiles * g.cblocks * g.N > 0x7fffffffLL) return kUnsupported;
@@ -177,34 +195,42 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
   const int c0 = cb * 16;
   const int nch = C - c0 < 16 ? C - c0 : 16;
 
-  // ---- weight slices: thread -> (row m, input channels i, i+1); the slice
-  //      of step bt is loaded during step bt-2 and written to LDS in step bt-1.
-  //      Wave (kk, q) = (wave/4, wave%4), lane (m, e/2) = (lane%16, lane/16):
-  //      the 64 lanes of a wave write 64 different LDS banks.
-  const int wm = lane & 15, wi = (wave >> 2) * 32 + 8 * (wave & 3) + 2 * (lane >> 4);
-  const bool wlive = (wave >> 2) < NK;
+  // ---- weight slices: thread -> (row m, input channels i, i+1) of every
+  //      second 32-channel chunk; the slice of step bt is loaded during step
+  //      bt-2 and written to LDS in step bt-1.  Wave (kk0, q) = (wave/4,
+  //      wave%4), lane (m, e/2) = (lane%16, lane/16): the 64 lanes of a wave
+  //      write 64 different LDS banks.
+  constexpr int JW = (NK + 1) / 2;  // 32-channel chunks per thread
+  const int wm = lane & 15, wsub = 8 * (wave & 3) + 2 * (lane >> 4), wk0 = wave >> 2;
   const BufRes wres = make_buf(wt, (uint32_t)(3 * C * KK * C * E));
-  uint32_t wraw[2];
+  uint32_t wraw[JW][2];
   auto wload = [&](int bt) {
     const int b = bt / KK, t = bt - b * KK;
     const int c = c0 + wm;
     const uint32_t row = (uint32_t)(((b * C + c) * KK + t) * C);
-    wraw[0] = gf_load_raw<E>(wres, (c < C && wi < C) ? (row + wi) * E : kOob);
-    wraw[1] = gf_load_raw<E>(wres, (c < C && wi + 1 < C) ? (row + wi + 1) * E : kOob);
+#pragma unroll
+    for (int j = 0; j < JW; ++j) {
+      const int wi = (wk0 + 2 * j) * 32 + wsub;
+      wraw[j][0] = gf_load_raw<E>(wres, (c < C && wi < C) ? (row + wi) * E : kOob);
+      wraw[j][1] = gf_load_raw<E>(wres, (c < C && wi + 1 < C) ? (row + wi + 1) * E : kOob);
+    }
   };
   auto wput = [&](int buf) {
-    if (!wlive) return;
-    // unit (kk, part, lane = m + 16*q) holds W[m][kk*32 + 8*q + e], e = 0..7
-    uint32_t* __restrict__ dst = reinterpret_cast<uint32_t*>(abuf + buf * AU * 16) +
-                                 ((wi >> 5) * P * 64 + wm + 16 * ((wi & 31) >> 3)) * 4 +
-                                 ((wi & 7) >> 1);
-    if constexpr (E == 4) {
-      uint32_t hi, lo;
-      split_bf16x2(__uint_as_float(wraw[0]), __uint_as_float(wraw[1]), hi, lo);
-      dst[0] = hi;
-      dst[64 * 4] = lo;
-    } else {
-      dst[0] = wraw[0] | (wraw[1] << 16);
+#pragma unroll
+    for (int j = 0; j < JW; ++j) {
+      const int kk = wk0 + 2 * j;  // wave-uniform
+      if (kk >= NK) break;
+      // unit (kk, part, lane = m + 16*q) holds W[m][kk*32 + 8*q + e], e = 0..7
+      uint32_t* __restrict__ dst = reinterpret_cast<uint32_t*>(abuf + buf * AU * 16) +
+                                   (kk * P * 64 + wm + 16 * (wsub >> 3)) * 4 + ((wsub & 7) >> 1);
+      if constexpr (E == 4) {
+        uint32_t hi, lo;
+        split_bf16x2(__uint_as_float(wraw[j][0]), __uint_as_float(wraw[j][1]), hi, lo);
+        dst[0] = hi;
+        dst[64 * 4] = lo;
+      } else {
+        dst[0] = wraw[j][0] | (wraw[j][1] << 16);
+      }
     }
   };
   wload(0);

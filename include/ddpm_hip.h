@@ -45,10 +45,10 @@ int ddpm_abi_version(void);
 const char* ddpm_status_string(int code);
 
 /* 1 when the fused generator entry points (ddpm_gen_*) accept this channel
- * count, kernel size and largest dilation (C <= 64, K in {1, 3}, and for
+ * count, kernel size and largest dilation (C <= 128, K in {1, 3}, and for
  * K = 3 max_dilation <= 8, the column halo the backward kernels stage; a 1x1
- * tap ignores the dilation), else 0.  The reference's fused path has no such
- * limit; callers route other shapes to the materialized entry points
+ * tap ignores the dilation), else 0.  The reference's fused path has no
+ * channel limit; callers route other shapes to the materialized entry points
  * (ddpm_filter_*), with identical results. */
 int ddpm_gen_supported(int64_t c, int kernel_size, int max_dilation);
 

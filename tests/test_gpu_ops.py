@@ -131,6 +131,42 @@ def test_generator_matches_oracle(shape, K, dtype):
 
 
 @pytest.mark.parametrize(
+    "shape",
+    [
+        (1, 72, 13, 21),   # 65..96 channels: four K steps, the last one partly zero
+        (2, 128, 16, 40),  # the largest fused channel count, W % 4 == 0
+    ],
+)
+@pytest.mark.parametrize("K", [1, 3])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_generator_wide_channels_match_oracle(shape, K, dtype):
+    """65..128 channels on the fused kernels: 32-column tiles, dY and dW over two
+    halves of the output / input channels."""
+    n, c, h, w = shape
+    say(f"generator wide shape={shape} K={K} dtype={dtype}")
+    assert ops.generator_supported(c, K, DIL)
+    x = randn(shape, 38, dtype)
+    y = randn(shape, 39, dtype)
+    wt, b = default_generator_params(c, K, 40, dtype)
+    g = randn((n, 4 * c, h, w), 41, dtype)
+    xd, yd = x.to(DEV).requires_grad_(), y.to(DEV).requires_grad_()
+    wd, bd = wt.to(DEV).requires_grad_(), b.to(DEV).requires_grad_()
+    out = ops.fused_generator_dynamic_cat(xd, yd, wd, bd, K, DIL)
+    out.backward(g.to(DEV))
+    x64, y64, w64, b64, g64 = (v.double() for v in (x, y, wt, b, g))
+    kern = ref.generated_kernels(y64, w64, b64, K)
+    if dtype != torch.float32:
+        kern = kern.to(dtype).double()
+    atol, rtol = TOL["gen_fwd"][dtype]
+    assert_close(out, ref.dynamic_cat(x64, kern, K), atol, rtol, "gen out")
+    dx, dy, dw, db = ref.generator_dynamic_cat_backward(x64, y64, w64, b64, g64, K)
+    atol, rtol = TOL["gen_bwd"][dtype]
+    for name, a, e in (("dx", xd.grad, dx), ("dy", yd.grad, dy), ("dw", wd.grad, dw), ("db", bd.grad, db)):
+        scale = max(1.0, e.abs().max().item())
+        assert_close(a, e, atol * scale, rtol, f"gen {name}")
+
+
+@pytest.mark.parametrize(
     "K,dil,fused",
     [
         (3, (2, 7, 8), True),    # largest dilation the fused kernels stage
@@ -250,6 +286,8 @@ def test_generator_inference_has_no_autograd_graph():
         (1, 10, 24, 40),     # C % 4 != 0, 24 steps -> 6 splits, scalar split reduction
         (2, 64, 128, 136),   # 512 steps -> 16 splits, a partial 128-column block per row
         (1, 24, 150, 130),   # W % 8 != 0 (element-wise y / gradient copies), 16 splits
+        (1, 96, 40, 64),     # two input-channel halves (the second partly zero), 10 splits
+        (1, 128, 4, 20),     # two halves, one split writes the gradients directly
     ],
 )
 def test_generator_weight_gradient_splits(shape):

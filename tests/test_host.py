@@ -35,7 +35,12 @@ def test_host_only_queries():
     assert lib.ddpm_abi_version() == _lib.ABI_VERSION == 2
     assert b"invalid argument" in lib.ddpm_status_string(10001)
     assert lib.ddpm_gen_supported(64, 3, 5) == 1
-    assert lib.ddpm_gen_supported(65, 3, 5) == 0
+    # up to 128 channels (four 32-channel K steps, 32-column tiles above 64)
+    assert lib.ddpm_gen_supported(65, 3, 5) == 1
+    assert lib.ddpm_gen_supported(128, 3, 5) == 1
+    assert lib.ddpm_gen_supported(128, 3, 8) == 1
+    assert lib.ddpm_gen_supported(129, 3, 5) == 0
+    assert lib.ddpm_gen_supported(129, 1, 1) == 0
     assert lib.ddpm_gen_supported(64, 5, 5) == 0
     # the backward kernels stage a column halo of 8 pixels; 1x1 taps ignore dilation
     assert lib.ddpm_gen_supported(64, 3, 8) == 1
@@ -62,6 +67,18 @@ def test_host_only_queries():
     # ... and 16x32 tiles when the R = 8 accumulator tile does not fit the LDS
     assert lib.ddpm_gen_bwd_x_workspace_bytes(1, 64, 256, 256, 3, 1, 3, 8) == 128 * 4 * 16 * 32 * 48 * 4
     assert lib.ddpm_gen_bwd_x_workspace_bytes(1, 64, 256, 256, 5, 1, 3, 5) == 0  # unsupported
+    # above 64 channels always 16x32 tiles (8 x 16 of them), 8 channel blocks; R = 5:
+    # 32+2R = 42 columns padded (shift 3) to 48
+    assert lib.ddpm_gen_bwd_x_workspace_bytes(1, 128, 256, 256, 3, 1, 3, 5) == 128 * 8 * 16 * 26 * 48 * 4
+    assert lib.ddpm_gen_bwd_x_workspace_bytes(1, 129, 256, 256, 3, 1, 3, 5) == 0  # unsupported
+    # dY's packed weight: [output-channel halves][3 branches][32-channel chunks][K*K]
+    # [16-channel blocks per half][hi, lo][64 lanes] x 16 bytes
+    assert lib.ddpm_gen_bwd_y_workspace_bytes(64, 3) == 1 * 3 * 2 * 9 * 4 * 2 * 64 * 16
+    assert lib.ddpm_gen_bwd_y_workspace_bytes(96, 3) == 2 * 3 * 3 * 9 * 4 * 2 * 64 * 16
+    assert lib.ddpm_gen_bwd_y_workspace_bytes(128, 3) == 2 * 3 * 4 * 9 * 4 * 2 * 64 * 16
+    assert lib.ddpm_gen_bwd_y_workspace_bytes(129, 3) == 0
+    # the weight gradient at 128 channels: the same 16 splits of C x (C + 1) partials
+    assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 128, 256, 256, 3, 1) == 16 * 27 * 128 * 129 * 4
     # generator convolution weight gradient at 128x128, C = 64, K = 5: 4800 rows in
     # 75 tiles of 64, 6 splits (450 workgroups for 512 slots) of (4800 x 64 + 4800)
     # fp32 partials, then the bf16 hi / lo planes of an fp32 y
@@ -87,7 +104,8 @@ def test_entry_points_validate_arguments_before_touching_the_device():
     assert lib.ddpm_filter_fwd(null, null, null, 1, 1, 4, 4, 2, 1, 3, 5, 0, 0, null) == 10001
     assert lib.ddpm_filter_fwd(null, null, null, 1, 1, 4, 4, 3, 1, 3, 5, 7, 0, null) == 10001
     assert lib.ddpm_filter_fwd(null, null, null, 1, 1, 4, 4, 3, 1, 3, 5, 0, 0, null) == 10001
-    assert lib.ddpm_gen_fwd(null, null, null, null, null, 1, 65, 4, 4, 3, 1, 3, 5, 0, null) == 10002
+    assert lib.ddpm_gen_fwd(null, null, null, null, null, 1, 129, 4, 4, 3, 1, 3, 5, 0, null) == 10002
+    assert lib.ddpm_gen_fwd(null, null, null, null, null, 1, 128, 4, 4, 3, 1, 3, 5, 0, null) == 10001
     assert lib.ddpm_gen_bwd_w(null, null, null, null, null, null, 0, 1, 64, 256, 256, 3, 1, 3, 5, 0, null) != 0
     # the generator 1x1 convolution: even kernel size, more than 128 channels
     assert lib.ddpm_gen_kernels(null, null, null, null, 1, 64, 8, 8, 4, 1, null) == 10001

@@ -52,8 +52,9 @@ def test_noalloc_bwd_y_matches_workspace_entry_point():
     lib = _lib.load()
     noalloc, scratch_bytes = _bind(lib)
     # the fixed buffer covers the largest packed weight the fused kernels take
-    assert scratch_bytes() >= lib.ddpm_gen_bwd_y_workspace_bytes(64, 3)
+    assert scratch_bytes() >= lib.ddpm_gen_bwd_y_workspace_bytes(128, 3)
     cases = [
+        ((1, 128, 16, 40), 3, torch.float32),  # the largest packed weight
         ((1, 64, 48, 96), 3, torch.float32),
         ((2, 24, 15, 17), 3, torch.float32),  # smaller: the buffer holds the last call's weight
         ((1, 40, 20, 32), 1, torch.bfloat16),
