@@ -13,15 +13,19 @@
 //                   rotated kernel), out = grad_cat [N][4C][H][W], no bias
 //
 // with zero padding outside the image.  Work decomposition (CDNA4):
-//   * one workgroup per (image-row segment of 256 pixels, group of 64 output
-//     planes m); 8 waves, two per SIMD, each owning 32 pixels (two MFMA
-//     column blocks) x the group's 64 planes;
+//   * one workgroup per (segment of 256 pixels, group of 16*MB output planes
+//     m); a segment is RS image rows x SW = 256/RS columns (SW = 256 for wide
+//     images, down to 32, so narrow images do not leave lanes idle); 8 waves,
+//     two per SIMD, each owning 32 pixels of one row (two MFMA column blocks)
+//     x the group's planes; MB = 4, halved while the grid has fewer
+//     workgroups than the chip has CUs (at 128x128 the forward's 64 output
+//     planes go to 4 workgroups of 16);
 //   * the K loop runs in stages (32-plane chunk of `in`, kernel row ki): a
-//     stage needs one row h + ki - 1 of 32 input planes, 256 + 16 columns,
-//     and the group's A slice for the 3 taps of that row; both are copied
-//     global -> LDS by buffer loads that write LDS directly (16-byte lanes;
-//     reads outside the image return zero), one stage ahead into a second
-//     buffer;
+//     stage needs the RS rows h + ki - 1 of 32 input planes, SW + 16 columns
+//     each, and the group's A slice for the 3 taps of that kernel row; both
+//     are copied global -> LDS by buffer loads that write LDS directly
+//     (16-byte lanes; reads outside the image return zero), one stage ahead
+//     into a second buffer;
 //   * A is packed once per call by a small kernel into MFMA A-fragment order
 //     (fp32: split into bf16 hi / lo), so a fragment is one 16-byte LDS read;
 //   * MFMA slot k = 8*quad + e of a 32-plane chunk holds plane 4*e + quad (A
@@ -38,16 +42,19 @@ namespace ddpm {
 
 constexpr int kCvWaves = 8;
 constexpr int kCvThreads = 64 * kCvWaves;
-constexpr int kCvTW = 32 * kCvWaves;       // output columns per workgroup
+constexpr int kCvPix = 32 * kCvWaves;      // output pixels per workgroup (RS rows x SW columns)
 constexpr int kCvPad = 8;                  // staged column halo (one chunk of 2-byte values)
-constexpr int kCvLW = kCvTW + 2 * kCvPad;  // staged columns (272)
-constexpr int kCvMB = 4;                   // 16-plane blocks of m per workgroup
+constexpr int kCvMaxMB = 4;                // 16-plane blocks of m per workgroup, at most
+constexpr int kCvFillWGs = 256;            // workgroups to aim for (the CU count of an MI355X)
 
 struct ConvGeom {
   int N, K, M, H, W;  // K input planes, M output planes
-  int col_tiles;      // ceil(W / kCvTW)
+  int rs, sw;         // segment rows and columns (rs * sw = kCvPix)
+  int tiles_h, tiles_w;
   int nc32;           // ceil(K / 32)
-  int mgroups;        // ceil(M / (kCvMB * 16))
+  int mb;             // 16-plane blocks of m per workgroup
+  int mgroups;        // ceil(M / (mb * 16))
+  int seg;            // staged elements per segment row (sw + 2 * kCvPad)
   int x4;             // input rows copied in 16-byte lanes (W % 8 == 0, aligned base)
 };
 
@@ -56,27 +63,29 @@ __host__ __device__ constexpr int cv_parts() {
   return sizeof(T) == 4 ? 2 : 1;
 }
 
-// Packed A: 16-byte units [mg][cc][ki][kj][ib][part][lane], lane (m = mg*64 +
-// ib*16 + (lane & 15), q = lane >> 4) holding A[m][cc*32 + 4e + q][ki][kj],
-// e = 0..7.  `rot` selects the input-gradient form (transposed, rotated).
-template <typename T>
+// Packed A: 16-byte units [mg][cc][ki][kj][ib][part][lane] (ib < g.mb), lane
+// (m = (mg*mb + ib)*16 + (lane & 15), q = lane >> 4) holding
+// A[m][cc*32 + 4e + q][ki][kj], e = 0..7.  `rot` selects the input-gradient
+// form (transposed, rotated).
+template <typename T, int MB>
 __global__ __launch_bounds__(256) void conv3x3_pack_kernel(const T* __restrict__ wt,
                                                            uint32_t* __restrict__ pk, ConvGeom g,
                                                            int rot) {
   constexpr int P = cv_parts<T>();
-  const int64_t total = (int64_t)g.mgroups * g.nc32 * 9 * kCvMB * 64;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  // 32-bit indices: the host bounds the packed units below 2^31
+  const int total = g.mgroups * g.nc32 * 9 * MB * 64;
+  const int idx = (int)(blockIdx.x * blockDim.x + threadIdx.x);
   if (idx >= total) return;
-  const int lane = (int)(idx & 63);
-  int64_t rest = idx >> 6;
-  const int ib = (int)(rest % kCvMB);
-  rest /= kCvMB;
-  const int tap = (int)(rest % 9);
+  const int lane = idx & 63;
+  int rest = idx >> 6;
+  const int ib = rest % MB;
+  rest /= MB;
+  const int tap = rest % 9;
   rest /= 9;
-  const int cc = (int)(rest % g.nc32);
-  const int mg = (int)(rest / g.nc32);
+  const int cc = rest % g.nc32;
+  const int mg = rest / g.nc32;
   const int ki = tap / 3, kj = tap - 3 * ki;
-  const int m = mg * kCvMB * 16 + ib * 16 + (lane & 15), q = lane >> 4;
+  const int m = (mg * MB + ib) * 16 + (lane & 15), q = lane >> 4;
   float v[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -93,34 +102,39 @@ __global__ __launch_bounds__(256) void conv3x3_pack_kernel(const T* __restrict__
   typename Mma<T>::V o[P];
   Mma<T>::pack(v, o);
   u32x4* __restrict__ dst = reinterpret_cast<u32x4*>(pk);
-  const int64_t unit = (((((int64_t)mg * g.nc32 + cc) * 9 + tap) * kCvMB + ib) * P) * 64 + lane;
+  const int64_t unit = (((((int64_t)mg * g.nc32 + cc) * 9 + tap) * MB + ib) * P) * 64 + lane;
 #pragma unroll
   for (int part = 0; part < P; ++part) dst[unit + part * 64] = __builtin_bit_cast(u32x4, o[part]);
 }
 
-// One LDS staging buffer (dwords): input rows [32 planes][kXS] then the A
-// slice [3 taps][kCvMB][P][64 lanes][4 dwords].
-template <typename T>
+// One LDS staging buffer (dwords): input rows [32 planes][kXS] -- a plane
+// holds its RS segment rows back to back, g.seg elements each -- then the A
+// slice [3 taps][MB][P][64 lanes][4 dwords].  The plane pitch is a
+// compile-time constant, so that the operand reads take their plane offsets
+// as immediates: the staged plane of one-row segments (WIDE: 272 elements)
+// or the largest over the segment shapes (8 rows x 48 columns), rounded to
+// 16 (mod 64) dwords so that a lane's 8 plane reads hit distinct banks.
+template <typename T, int MB, bool WIDE>
 struct CvLds {
   static constexpr int kE = (int)sizeof(T);
   static constexpr int kPerD = 4 / kE;
-  static constexpr int kXD = kCvLW / kPerD;  // dwords per staged row
-  // pitch = 16 (mod 64) dwords: the 8 plane reads of a lane fall on distinct banks
+  static constexpr int kPC = 16 / kE;  // elements per 16-byte chunk
+  static constexpr int kXD = (WIDE ? kCvPix + 2 * kCvPad : 8 * (32 + 2 * kCvPad)) / kPerD;
   static constexpr int kXS = kXD + ((16 - kXD % 64) + 64) % 64;
-  static constexpr int kXChunks = kXD / 4;  // 16-byte chunks per row
   static constexpr int kAOff = 32 * kXS;
-  static constexpr int kAUnits = 3 * kCvMB * cv_parts<T>() * 64;  // 16-byte units
+  static constexpr int kAUnits = 3 * MB * cv_parts<T>() * 64;  // 16-byte units
   static constexpr int kBuf = kAOff + 4 * kAUnits;
+  static_assert(kCvPix == 256, "segments hold at most kXD dwords per plane");
 };
 
-template <typename T, bool BIAS>
+template <typename T, bool BIAS, int MB, bool WIDE>
 __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict__ in,
                                                              const uint32_t* __restrict__ pk,
                                                              const T* __restrict__ bias,
                                                              T* __restrict__ out, ConvGeom g) {
   typedef Mma<T> M;
   typedef typename M::V V;
-  typedef CvLds<T> L;
+  typedef CvLds<T, MB, WIDE> L;
   constexpr int P = M::P;
   constexpr int E = (int)sizeof(T);
   extern __shared__ __attribute__((aligned(16))) uint32_t csm[];
@@ -128,9 +142,11 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int mg = bid % g.mgroups;
   const int tile = bid / g.mgroups;
-  const int row = tile / g.col_tiles;  // image row n*H + h
-  const int w0 = (tile - row * g.col_tiles) * kCvTW;
-  const int n = row / g.H, h = row - n * g.H;
+  const int tiles_img = g.tiles_h * g.tiles_w;
+  const int n = tile / tiles_img;
+  const int trem = tile - n * tiles_img;
+  const int ty = trem / g.tiles_w;
+  const int h0 = ty * g.rs, w0 = (trem - ty * g.tiles_w) * g.sw;
   const int H = g.H, W = g.W;
   const int64_t HW = (int64_t)H * W;
   const int tid = threadIdx.x;
@@ -138,13 +154,31 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
   const int lane = tid & 63;
   const int col16 = lane & 15, quad = lane >> 4;
   const int nstage = 3 * g.nc32;  // (cc, ki)
+  // this wave's 32 pixels: segment row wseg (wave-uniform), columns pcol0 ..
+  const int wseg = (32 * wave) / g.sw;
+  const int pcol0 = 32 * wave - wseg * g.sw;
 
   const BufRes xres = make_buf(in + (int64_t)n * g.K * HW, (uint32_t)(g.K * HW * (int64_t)E));
+  // 16-byte copies of a staged plane: chunk ci = pc + lane of copy `part`
+  // (the last copy ends at the plane's end and may overlap the previous one)
+  // is column chunk cw of segment row sgr; both are stage-invariant
+  const int cps = g.seg / L::kPC;  // chunks per segment row
+  const int cpp = g.rs * cps;      // chunks per staged plane (at most 96)
+  constexpr int kParts = 2;
+  int cpos[kParts], crow[kParts], ccol[kParts];
+#pragma unroll
+  for (int part = 0; part < kParts; ++part) {
+    const int pc = 64 * part < cpp - 64 ? 64 * part : (cpp > 64 ? cpp - 64 : 0);
+    const int ci = pc + lane;
+    crow[part] = ci / cps;
+    ccol[part] = (ci - crow[part] * cps) * L::kPC - kCvPad;  // column relative to w0
+    cpos[part] = 4 * pc;                                     // dword offset in the plane
+  }
+  const int nparts = (cpp + 63) / 64;
   // ---- stage s = cc * 3 + ki -> LDS buffer `buf`
   auto stage = [&](int s, int buf) {
     const int ki = s % 3;
     const int cc = s / 3;
-    const int hh = h + ki - 1;
     uint32_t* __restrict__ dstb = csm + buf * L::kBuf;
     if (g.x4) {
       // one resource for the image; a chunk outside the image (column, row or
@@ -153,35 +187,36 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
       for (int j = 0; j < 32 / kCvWaves; ++j) {
         const int cr = wave + kCvWaves * j;
         const int ch = cc * 32 + cr;
-        const bool ok = ch < g.K && (unsigned)hh < (unsigned)H;
-        const uint32_t rowel = (uint32_t)ch * (uint32_t)HW + (uint32_t)(hh * W);
 #pragma unroll
-        for (int part = 0; part < (L::kXChunks + 63) / 64; ++part) {
-          // the last copy ends at the row end (it may overlap the previous one)
-          const int pc = 64 * part < L::kXChunks - 64 ? 64 * part
-                                                      : (L::kXChunks > 64 ? L::kXChunks - 64 : 0);
-          const int gw = w0 - kCvPad + (pc + lane) * 4 * L::kPerD;
+        for (int part = 0; part < kParts; ++part) {
+          if (part >= nparts) break;
+          // one-row segments: the row is uniform over the wave
+          const int hh = h0 + (WIDE ? 0 : crow[part]) + ki - 1;
+          const int gw = w0 + ccol[part];
+          const bool ok = ch < g.K && (unsigned)hh < (unsigned)H && (unsigned)gw < (unsigned)W;
           const uint32_t off =
-              (ok && (unsigned)gw < (unsigned)W) ? (rowel + (uint32_t)gw) * (uint32_t)E : kOob;
-          if (L::kXChunks >= 64 || lane < L::kXChunks)
+              ok ? ((uint32_t)ch * (uint32_t)HW + (uint32_t)(hh * W + gw)) * (uint32_t)E : kOob;
+          if (cpp >= 64 || lane < cpp)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                xres, (__attribute__((address_space(3))) void*)(dstb + cr * L::kXS + 4 * pc), 16,
+                xres, (__attribute__((address_space(3))) void*)(dstb + cr * L::kXS + cpos[part]), 16,
                 off, 0, 0, 0);
         }
       }
     } else {
       // element-wise copy through registers (W % 8 != 0 or unaligned input)
       T* __restrict__ dst = reinterpret_cast<T*>(dstb);
-      for (int idx = tid; idx < 32 * kCvLW; idx += kCvThreads) {
-        const int cr = idx / kCvLW, j = idx - cr * kCvLW;
-        const int ch = cc * 32 + cr, gw = w0 - kCvPad + j;
+      const int plen = g.rs * g.seg;
+      for (int idx = tid; idx < 32 * plen; idx += kCvThreads) {
+        const int cr = idx / plen, j = idx - cr * plen;
+        const int sgr = j / g.seg, col = j - sgr * g.seg;
+        const int ch = cc * 32 + cr, hh = h0 + sgr + ki - 1, gw = w0 - kCvPad + col;
         const bool ok = ch < g.K && (unsigned)hh < (unsigned)H && (unsigned)gw < (unsigned)W;
         const uint32_t off = ok ? ((uint32_t)ch * (uint32_t)HW + (uint32_t)(hh * W + gw)) * E : kOob;
         dst[cr * L::kXS * L::kPerD + j] = from_f<T>(buf_load1<T>(xres, off));
       }
     }
     // A slice of the stage's 3 taps: contiguous in the packed weight
-    const uint32_t* src = pk + ((((int64_t)mg * g.nc32 + cc) * 9 + ki * 3) * kCvMB * P * 64) * 4;
+    const uint32_t* src = pk + ((((int64_t)mg * g.nc32 + cc) * 9 + ki * 3) * MB * P * 64) * 4;
     const BufRes pres = make_buf(src, (uint32_t)(L::kAUnits * 16));
 #pragma unroll
     for (int j = 0; j < (L::kAUnits / 64 + kCvWaves - 1) / kCvWaves; ++j) {
@@ -193,13 +228,15 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
     }
   };
 
-  f32x4 acc[2][kCvMB];
+  f32x4 acc[2][MB];
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-    for (int ib = 0; ib < kCvMB; ++ib) acc[blk][ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ib = 0; ib < MB; ++ib) acc[blk][ib] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int px0 = 32 * wave + col16;  // pixel of block 0 within the tile; block 1 is +16
+  // staged element of this lane's block-0 pixel at tap column 0: segment row
+  // wseg, column pad + pcol0 + col16
+  const int el0 = wseg * g.seg + kCvPad + pcol0 + col16;
   stage(0, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -207,22 +244,22 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
     const int buf = s & 1;
     if (s + 1 < nstage) stage(s + 1, buf ^ 1);
     const uint32_t* __restrict__ bb = csm + buf * L::kBuf;
-    // this lane's input elements: plane 4e + quad, column pad + px + dw
+    // this lane's input elements: plane 4e + quad, element el0 + 16 blk + dw
     const uint32_t* __restrict__ xq = bb + quad * L::kXS;
 #pragma unroll
     for (int kj = 0; kj < 3; ++kj) {
       const int dw = kj - 1;
-      V afr[kCvMB][P];
+      V afr[MB][P];
 #pragma unroll
-      for (int ib = 0; ib < kCvMB; ++ib)
+      for (int ib = 0; ib < MB; ++ib)
 #pragma unroll
         for (int pp = 0; pp < P; ++pp)
           afr[ib][pp] = __builtin_bit_cast(
               V, *reinterpret_cast<const u32x4*>(bb + L::kAOff +
-                                                 4 * ((((kj * kCvMB) + ib) * P + pp) * 64 + lane)));
+                                                 4 * ((((kj * MB) + ib) * P + pp) * 64 + lane)));
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk) {
-        const int col = kCvPad + px0 + 16 * blk + dw;
+        const int col = el0 + 16 * blk + dw;
         float bv[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -234,30 +271,33 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
         V bfr[P];
         M::pack(bv, bfr);
 #pragma unroll
-        for (int ib = 0; ib < kCvMB; ++ib) acc[blk][ib] = M::mac(afr[ib], bfr, acc[blk][ib]);
+        for (int ib = 0; ib < MB; ++ib) acc[blk][ib] = M::mac(afr[ib], bfr, acc[blk][ib]);
       }
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
 
-  // ---- store: lane holds out[m = mg*64 + ib*16 + 4*quad + e][pixel col16 of block]
+  // ---- store: lane holds out[m = (mg*MB + ib)*16 + 4*quad + e][pixel col16 of block]
+  const int h = h0 + wseg;
+  if (h < H) {
 #pragma unroll
-  for (int blk = 0; blk < 2; ++blk) {
-    const int w = w0 + px0 + 16 * blk;
-    if (w < W) {
-      T* __restrict__ yo = out + (int64_t)n * g.M * HW + (int64_t)h * W + w;
+    for (int blk = 0; blk < 2; ++blk) {
+      const int w = w0 + pcol0 + col16 + 16 * blk;
+      if (w < W) {
+        T* __restrict__ yo = out + (int64_t)n * g.M * HW + (int64_t)h * W + w;
 #pragma unroll
-      for (int ib = 0; ib < kCvMB; ++ib)
+        for (int ib = 0; ib < MB; ++ib)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int m = mg * kCvMB * 16 + ib * 16 + 4 * quad + e;
-          if (m < g.M) {
-            float v = acc[blk][ib][e];
-            if constexpr (BIAS) v += to_f(bias[m]);
-            yo[(int64_t)m * HW] = from_f<T>(v);
+          for (int e = 0; e < 4; ++e) {
+            const int m = (mg * MB + ib) * 16 + 4 * quad + e;
+            if (m < g.M) {
+              float v = acc[blk][ib][e];
+              if constexpr (BIAS) v += to_f(bias[m]);
+              yo[(int64_t)m * HW] = from_f<T>(v);
+            }
           }
-        }
+      }
     }
   }
 }
@@ -278,20 +318,39 @@ int cv_with_type(int dt, F&& f) {
   }
 }
 
-void cv_geom(ConvGeom& g, int64_t n, int64_t k, int64_t m, int64_t h, int64_t w) {
+int cv_pow2ceil(int64_t v) {
+  int p = 1;
+  while (p < v && p < (1 << 30)) p <<= 1;
+  return p;
+}
+
+// Segment shape and m-block count for a shape: SW = the image width rounded
+// up to a power of two within [32, 256]; MB = 4, halved while the grid has
+// fewer than kCvFillWGs workgroups.  `esz` sizes the LDS staging buffers.
+void cv_geom(ConvGeom& g, int64_t n, int64_t k, int64_t m, int64_t h, int64_t w, int esz) {
   g.N = (int)n;
   g.K = (int)k;
   g.M = (int)m;
   g.H = (int)h;
   g.W = (int)w;
-  g.col_tiles = (int)((w + kCvTW - 1) / kCvTW);
+  int sw = cv_pow2ceil(w);
+  sw = sw < 32 ? 32 : (sw > kCvPix ? kCvPix : sw);
+  g.sw = sw;
+  g.rs = kCvPix / sw;
+  g.tiles_h = (int)((h + g.rs - 1) / g.rs);
+  g.tiles_w = (int)((w + sw - 1) / sw);
   g.nc32 = (int)((k + 31) / 32);
-  g.mgroups = (int)((m + kCvMB * 16 - 1) / (kCvMB * 16));
+  g.mb = kCvMaxMB;
+  const int64_t tiles = n * g.tiles_h * g.tiles_w;
+  while (g.mb > 1 && tiles * ((m + g.mb * 16 - 1) / (g.mb * 16)) < kCvFillWGs) g.mb /= 2;
+  g.mgroups = (int)((m + g.mb * 16 - 1) / (g.mb * 16));
+  g.seg = sw + 2 * kCvPad;
+  (void)esz;
   g.x4 = 0;
 }
 
 int64_t cv_pack_bytes(const ConvGeom& g, int dtype) {
-  return (int64_t)g.mgroups * g.nc32 * 9 * kCvMB * (dtype == kF32 ? 2 : 1) * 64 * 16;
+  return (int64_t)g.mgroups * g.nc32 * 9 * g.mb * (dtype == kF32 ? 2 : 1) * 64 * 16;
 }
 
 // Shape checks shared by both directions: K input planes, M output planes.
@@ -302,41 +361,60 @@ int cv_check(int64_t n, int64_t k, int64_t m, int64_t h, int64_t w, int dtype) {
   // 32-bit buffer offsets inside one image's input and output planes
   if (k * h * w * esz > 0x7fffffffLL || m * h * w * esz > 0x7fffffffLL) return kUnsupported;
   if (h > (1 << 20) || w > (1 << 20)) return kUnsupported;
-  const int64_t groups = n * h * ((w + kCvTW - 1) / kCvTW) * ((m + kCvMB * 16 - 1) / (kCvMB * 16));
+  // the grid at its largest (32-column segments of 8 rows, single m blocks)
+  const int64_t groups = n * ((h + 7) / 8) * ((w + 31) / 32) * ((m + 15) / 16);
   if (groups > 0x7fffffffLL) return kUnsupported;
+  // 32-bit indices of the weight packing: (m/16 + 4) blocks x 9 taps x 64 lanes per 32 planes
+  if (((m + 15) / 16 + 4) * ((k + 31) / 32) * 9 * 64 > 0x7fffffffLL) return kUnsupported;
   return kOk;
 }
 
 int cv_run(const void* in, const void* wt, const void* bias, void* out, void* workspace,
            int64_t workspace_bytes, int64_t n, int64_t k, int64_t m, int64_t h, int64_t w, int rot,
            int dtype, hipStream_t stream) {
+  const int esz = dtype == kF32 ? 4 : 2;
   ConvGeom g;
-  cv_geom(g, n, k, m, h, w);
+  cv_geom(g, n, k, m, h, w, esz);
   const int64_t need = cv_pack_bytes(g, dtype);
   if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 16 != 0)
     return kWorkspaceTooSmall;
-  const int esz = dtype == kF32 ? 4 : 2;
   g.x4 = (w % 8 == 0) && ((uintptr_t)in % 16 == 0);
-  (void)esz;
   return cv_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
-    typedef CvLds<T> L;
-    const int64_t units = (int64_t)g.mgroups * g.nc32 * 9 * kCvMB * 64;
-    hipLaunchKernelGGL((conv3x3_pack_kernel<T>), dim3((unsigned)((units + 255) / 256)), dim3(256), 0,
-                       stream, (const T*)wt, (uint32_t*)workspace, g, rot);
+    const int64_t units = (int64_t)g.mgroups * g.nc32 * 9 * g.mb * 64;
+    const dim3 pgrid((unsigned)((units + 255) / 256));
+    if (g.mb == 4)
+      hipLaunchKernelGGL((conv3x3_pack_kernel<T, 4>), pgrid, dim3(256), 0, stream, (const T*)wt,
+                         (uint32_t*)workspace, g, rot);
+    else if (g.mb == 2)
+      hipLaunchKernelGGL((conv3x3_pack_kernel<T, 2>), pgrid, dim3(256), 0, stream, (const T*)wt,
+                         (uint32_t*)workspace, g, rot);
+    else
+      hipLaunchKernelGGL((conv3x3_pack_kernel<T, 1>), pgrid, dim3(256), 0, stream, (const T*)wt,
+                         (uint32_t*)workspace, g, rot);
     int e = (int)hipGetLastError();
     if (e != 0) return e;
-    const size_t lds = (size_t)2 * L::kBuf * 4;
-    const dim3 grid((unsigned)((int64_t)n * h * g.col_tiles * g.mgroups));
-    auto launch = [&](auto kern) {
+    const dim3 grid((unsigned)((int64_t)n * g.tiles_h * g.tiles_w * g.mgroups));
+    auto launch = [&](auto kern, size_t lds) {
       const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
       if (ae != 0) return ae;
       hipLaunchKernelGGL(kern, grid, dim3(kCvThreads), lds, stream, (const T*)in,
                          (const uint32_t*)workspace, (const T*)bias, (T*)out, g);
       return (int)hipGetLastError();
     };
-    if (bias) return launch(conv3x3_kernel<T, true>);
-    return launch(conv3x3_kernel<T, false>);
+    auto pick = [&](auto b) {
+      constexpr bool B = decltype(b)::value;
+      // one-row segments (wide images) with the narrower staging pitch
+      if (g.mb == 4 && g.rs == 1)
+        return launch(conv3x3_kernel<T, B, 4, true>, (size_t)2 * CvLds<T, 4, true>::kBuf * 4);
+      if (g.mb == 4)
+        return launch(conv3x3_kernel<T, B, 4, false>, (size_t)2 * CvLds<T, 4, false>::kBuf * 4);
+      if (g.mb == 2)
+        return launch(conv3x3_kernel<T, B, 2, false>, (size_t)2 * CvLds<T, 2, false>::kBuf * 4);
+      return launch(conv3x3_kernel<T, B, 1, false>, (size_t)2 * CvLds<T, 1, false>::kBuf * 4);
+    };
+    if (bias) return pick(std::true_type());
+    return pick(std::false_type());
   });
 }
 
@@ -347,9 +425,11 @@ using namespace ddpm;
 
 extern "C" int64_t ddpm_fuse_conv_workspace_bytes(int64_t c, int dtype) {
   if (c <= 0 || dtype < kF32 || dtype > kF16) return 0;
+  // the largest packed weight over the shapes: four-block m groups (fewer
+  // blocks per group pack no more bytes)
   ConvGeom gf, gd;
-  cv_geom(gf, 1, 4 * c, c, 1, 1);  // forward: K = 4C input planes, M = C
-  cv_geom(gd, 1, c, 4 * c, 1, 1);  // input gradient: K = C, M = 4C
+  cv_geom(gf, 1 << 20, 4 * c, c, 1, 1, dtype == kF32 ? 4 : 2);  // forward: K = 4C, M = C
+  cv_geom(gd, 1 << 20, c, 4 * c, 1, 1, dtype == kF32 ? 4 : 2);  // input gradient: K = C, M = 4C
   const int64_t a = cv_pack_bytes(gf, dtype), b = cv_pack_bytes(gd, dtype);
   return a > b ? a : b;
 }

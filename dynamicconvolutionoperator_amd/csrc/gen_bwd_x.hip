@@ -110,19 +110,11 @@ int xt_with_type(int dt, F&& f) {
   }
 }
 
-// Tiling of the scatter kernel: 64-column tiles when the fp32 accumulator
-// tile (16 bytes per 4-channel pixel) fits the LDS next to fp32 weight
-// slices and the fp32 y operand fits the registers, else 32 columns.  The
-// choice ignores the dtype so that the workspace size depends on the shape
-// alone.
+// Tiling of the scatter kernel (tile_geom_for) with 16-byte accumulator
+// entries and fp32 weight slices whatever the dtype, so that the workspace
+// size depends on the shape alone.
 int bx_geom(TileGeom& g, const GenGeom& gg, int& cb, size_t& lds) {
-  cb = gt_first_cb(gt_nk(gg.C));
-  int st = tile_geom(g, gg, 16, 2, cb, lds);
-  if (st == kUnsupported && cb == 4) {
-    cb = 2;
-    st = tile_geom(g, gg, 16, 2, cb, lds);
-  }
-  return st;
+  return tile_geom_for(g, gg, 16, 2, cb, lds);
 }
 
 int64_t bx_part_bytes(const TileGeom& g) {
@@ -200,6 +192,9 @@ extern "C" int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bia
       if (cb == 4)
         return nk == 1 ? launch(gen_bwd_x_tile_kernel<T, KS, 1, 4>)
                        : launch(gen_bwd_x_tile_kernel<T, KS, 2, 4>);
+      if (cb == 1)
+        return nk == 1 ? launch(gen_bwd_x_tile_kernel<T, KS, 1, 1>)
+                       : launch(gen_bwd_x_tile_kernel<T, KS, 2, 1>);
       return nk == 1 ? launch(gen_bwd_x_tile_kernel<T, KS, 1, 2>)
                      : launch(gen_bwd_x_tile_kernel<T, KS, 2, 2>);
     };

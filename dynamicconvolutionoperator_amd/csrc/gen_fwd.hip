@@ -86,18 +86,12 @@ extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, co
   // 32-bit buffer offsets inside one image's [C][H][W] planes (and 16 planes
   // past a channel block's first one)
   if (c * h * w * esz > 0x7fffffffLL || 16 * h * w * esz > 0x7fffffffLL) return kUnsupported;
-  // 64-column tiles when their halo tile fits the LDS (and the y operand the
-  // registers), else 32 columns
   TileGeom g;
   size_t lds = 0;
   const int parts = esz == 4 ? 2 : 1;
   const int nk = gt_nk((int)c);
-  int cb = gt_first_cb(nk);
-  st = tile_geom(g, gg, 4 * esz, parts, cb, lds);
-  if (st == kUnsupported && cb == 4) {
-    cb = 2;
-    st = tile_geom(g, gg, 4 * esz, parts, cb, lds);
-  }
+  int cb = 4;
+  st = tile_geom_for(g, gg, 4 * esz, parts, cb, lds);
   if (st != kOk) return st;
   return with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
@@ -118,6 +112,8 @@ extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, co
       }
       if (cb == 4)
         return nk == 1 ? launch(gen_fwd_kernel<T, KS, 1, 4>) : launch(gen_fwd_kernel<T, KS, 2, 4>);
+      if (cb == 1)
+        return nk == 1 ? launch(gen_fwd_kernel<T, KS, 1, 1>) : launch(gen_fwd_kernel<T, KS, 2, 1>);
       return nk == 1 ? launch(gen_fwd_kernel<T, KS, 1, 2>) : launch(gen_fwd_kernel<T, KS, 2, 2>);
     };
     if (kernel_size == 1) return pick(std::integral_constant<int, 1>());

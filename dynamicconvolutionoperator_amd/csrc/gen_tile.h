@@ -105,6 +105,38 @@ inline int tile_geom(TileGeom& f, const GenGeom& g, int entry, int parts, int cb
   return kOk;
 }
 
+// Workgroups the tile kernels aim to launch at least: the CU count of an
+// MI355X (a fixed number, so that a workspace query made without a device
+// agrees with the launch).
+constexpr int kGtFillWGs = 256;
+
+// Tiling of the tile kernels for a shape: 64-column tiles (32 for 65..128
+// channels), 32 columns when the 64-column halo tile does not fit the LDS,
+// then, for 1 or 2 input-channel chunks, narrower tiles (32, then 16
+// columns) while the grid has fewer than kGtFillWGs workgroups -- at
+// 128x128, C = 64 the 64-column tiles give 64 workgroups for 256 CUs
+// (measured fp32 forward 43.5 -> 26.3 us with 16-column tiles).  Returns
+// kOk with `cb` (16-column blocks per tile row), `f` and `lds` set.
+inline int tile_geom_for(TileGeom& f, const GenGeom& g, int entry, int parts, int& cb, size_t& lds) {
+  const int nk = gt_nk(g.C);
+  cb = gt_first_cb(nk);
+  int st = tile_geom(f, g, entry, parts, cb, lds);
+  if (st == kUnsupported && cb == 4) {
+    cb = 2;
+    st = tile_geom(f, g, entry, parts, cb, lds);
+  }
+  if (st != kOk) return st;
+  while (nk <= 2 && cb > 1 && (int64_t)f.N * f.tiles * f.cblocks < kGtFillWGs) {
+    TileGeom f2;
+    size_t lds2 = 0;
+    if (tile_geom(f2, g, entry, parts, cb / 2, lds2) != kOk) break;
+    f = f2;
+    lds = lds2;
+    cb /= 2;
+  }
+  return kOk;
+}
+
 // Raw element bits through a buffer resource (no conversion).
 template <int E>
 __device__ __forceinline__ uint32_t gf_load_raw(BufRes r, uint32_t off) {

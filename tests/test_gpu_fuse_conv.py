@@ -1,8 +1,10 @@
 """The HIP 3x3 fuse convolution (ddpm_fuse_conv_fwd / _bwd_data) against
 float64 F.conv2d on the CPU: Conv2d(4C -> C, 3, padding 1) forward and the
 gradients of its input, weight and bias, on a non-aligned shape (C=24,
-15x17: element-wise row copies, a partial plane chunk), aligned shapes
-(W % 8 == 0: 16-byte row copies) and the full 256x256 C=64 size."""
+15x17: element-wise row copies, a partial plane chunk, 8-row segments of 32
+columns), aligned shapes (W % 8 == 0: 16-byte row copies; segments of 4 rows
+x 64 columns and 2 rows x 128 columns, the last one partly outside the image)
+and the 256x256 and 128x128 C=64 sizes."""
 
 import pytest
 import torch
@@ -40,16 +42,19 @@ def _check(shape, dtype, seed):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("shape", [(2, 24, 15, 17), (1, 16, 12, 40), (2, 8, 5, 264)])
+@pytest.mark.parametrize("shape", [(2, 24, 15, 17), (1, 16, 12, 40), (2, 8, 5, 264), (1, 32, 19, 96)])
 def test_fuse_conv_matches_conv2d(shape, dtype):
     say(f"fuse conv shape={shape} dtype={dtype}")
     _check(shape, dtype, 900)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_fuse_conv_full_size(dtype):
-    say(f"fuse conv 256x256 C=64 dtype={dtype}")
-    _check((1, 64, 256, 256), dtype, 910)
+@pytest.mark.parametrize("hw", [256, 128])
+def test_fuse_conv_full_size(dtype, hw):
+    """256x256 (one-row segments, four-block m groups) and 128x128 (two-row
+    segments; the forward's 64 output planes in four single-block groups)."""
+    say(f"fuse conv {hw}x{hw} C=64 dtype={dtype}")
+    _check((1, 64, hw, hw), dtype, 910)
 
 
 def test_fuse_conv_without_bias_and_fallback():
