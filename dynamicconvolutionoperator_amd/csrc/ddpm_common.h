@@ -53,11 +53,31 @@ __device__ __forceinline__ float quant<float>(float v) {
   return v;
 }
 
+// quant() of four values: for bf16 two v_cvt_pk_bf16_f32 and four widening
+// shifts / masks (6 instructions where four separate roundings take 8).
+template <typename T>
+__device__ __forceinline__ void quant4(const f32x4& v, float (&q)[4]);
+
 // Two fp32 values rounded to nearest-even bf16, packed low/high
 // (one v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   const bf16x2 r = __builtin_convertvector((f32x2){a, b}, bf16x2);
   return __builtin_bit_cast(uint32_t, r);
+}
+
+template <typename T>
+__device__ __forceinline__ void quant4(const f32x4& v, float (&q)[4]) {
+  if constexpr (__is_same(T, bf16)) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t p = pack_bf16x2(v[2 * h], v[2 * h + 1]);
+      q[2 * h] = __uint_as_float(p << 16);
+      q[2 * h + 1] = __uint_as_float(p & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] = quant<T>(v[e]);
+  }
 }
 
 // Splits two fp32 values into bf16 pairs hi + lo with a ~= hi_a + lo_a:

@@ -179,6 +179,134 @@ __device__ __forceinline__ void gf_store4_raw(BufRes r, uint32_t off, const uint
   }
 }
 
+// Halo tile of x (zero outside the image) -> the 4 LDS planes of 4-channel
+// entries (XB bytes each) for the workgroup's 16-channel block starting at
+// channel c0 (nch of them), tile rows h0.., columns w0..; the tile's own
+// pixels also go to the identity channels of the concat `out`.
+template <typename T, int XB>
+__device__ __forceinline__ void gt_stage_x(const T* __restrict__ a, T* __restrict__ out,
+                                           unsigned char* __restrict__ xs, const TileGeom& g,
+                                           int n, int c0, int nch, int h0, int w0, int TW,
+                                           int tid) {
+  constexpr int E = (int)sizeof(T);
+  typedef uint32_t XQ __attribute__((ext_vector_type(E)));  // one 4-channel x entry
+  const int C = g.C, H = g.H, W = g.W, R = g.R, LW = g.LW;
+  const int64_t HW = (int64_t)H * W;
+  const uint32_t HWE = (uint32_t)HW * (uint32_t)E;
+  // ---- halo tile of x (zero outside the image) -> LDS planes; the tile's
+  //      own pixels also go to the identity channels of the output
+  const BufRes xres = make_buf(a + ((int64_t)n * C + c0) * HW, (uint32_t)nch * HWE);
+  const BufRes ores = make_buf(out + ((int64_t)n * 4 * C + c0) * HW, (uint32_t)nch * HWE);
+  if (g.vec) {
+    // a task = (4-channel plane, halo row, 4 image columns a multiple of 4
+    // apart from column 0): one 16-byte (8-byte) access per channel, the
+    // 4 x 4 block transposed in registers into four 4-channel entries
+    const int gpr = g.LWp / 4, cpos = R + g.pad;
+    const int tasks = 4 * g.LH * gpr;
+    for (int task = tid; task < tasks; task += kGtThreads) {
+      const int k = task % gpr, rest = task / gpr;
+      const int i = rest % g.LH, grp = rest / g.LH;
+      const int gh = h0 - R + i, gc = w0 - cpos + 4 * k;
+      const bool in = (unsigned)gh < (unsigned)H && (unsigned)gc < (unsigned)W;
+      const uint32_t off = in ? (uint32_t)(gh * W + gc) * (uint32_t)E : kOob;
+      uint32_t v[4][4];  // [channel][column]
+#pragma unroll
+      for (int e = 0; e < 4; ++e) gf_load4_raw<E>(xres, off + (uint32_t)(4 * grp + e) * HWE, v[e]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int j = 4 * k + m - g.pad;
+        if (j < 0 || j >= LW) continue;
+        XQ q;
+        if constexpr (E == 4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) q[e] = v[e][m];
+        } else {
+          q[0] = v[0][m] | (v[1][m] << 16);
+          q[1] = v[2][m] | (v[3][m] << 16);
+        }
+        *reinterpret_cast<XQ*>(xs + grp * g.plane + (i * LW + j) * XB) = q;
+      }
+      if (i >= R && i < R + kGtTH && 4 * k >= cpos && 4 * k < cpos + TW) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gf_store4_raw<E>(ores, off + (uint32_t)(4 * grp + e) * HWE, v[e]);
+      }
+    }
+  } else {
+    // element-wise: two pixels per thread and batch, 32 loads in flight
+    // before any LDS write
+    for (int p0 = tid; p0 < g.npix; p0 += 2 * kGtThreads) {
+      uint32_t lo[2], so[2];
+      int pix[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        pix[s] = p0 + s * kGtThreads;
+        const int i = pix[s] / LW, j = pix[s] - i * LW;
+        const int gh = h0 - R + i, gw = w0 - R + j;
+        const bool in =
+            pix[s] < g.npix && (unsigned)gh < (unsigned)H && (unsigned)gw < (unsigned)W;
+        const bool inner = i >= R && i < R + kGtTH && j >= R && j < R + TW;
+        lo[s] = in ? (uint32_t)(gh * W + gw) * (uint32_t)E : kOob;
+        so[s] = (in && inner) ? lo[s] : kOob;
+      }
+      uint32_t v[2][16];
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int ch = 0; ch < 16; ++ch) v[s][ch] = gf_load_raw<E>(xres, lo[s] + ch * HWE);
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int ch = 0; ch < 16; ++ch) gf_store_raw<E>(ores, so[s] + ch * HWE, v[s][ch]);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (pix[s] >= g.npix) continue;
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp) {
+          XQ q;
+          if constexpr (E == 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[e] = v[s][4 * grp + e];
+          } else {
+            q[0] = v[s][4 * grp] | (v[s][4 * grp + 1] << 16);
+            q[1] = v[s][4 * grp + 2] | (v[s][4 * grp + 3] << 16);
+          }
+          *reinterpret_cast<XQ*>(xs + grp * g.plane + pix[s] * XB) = q;
+        }
+      }
+    }
+  }
+}
+
+// The y operand (B fragments, unshifted pixels) of this wave's NBW = 2*CB
+// blocks of 16 pixels: 8 input channels per lane and 32-channel chunk.
+template <typename T, int NK, int CB>
+__device__ __forceinline__ void gt_load_y(const T* __restrict__ y,
+                                          typename Mma<T>::V (&bfr)[2 * CB][NK][Mma<T>::P],
+                                          const TileGeom& g, int n, int h0, int w0, int wave,
+                                          int col16, int quad) {
+  typedef Mma<T> M;
+  constexpr int E = (int)sizeof(T);
+  const int C = g.C, H = g.H, W = g.W;
+  const int64_t HW = (int64_t)H * W;
+  const uint32_t HWE = (uint32_t)HW * (uint32_t)E;
+  const BufRes yres = make_buf(y + (int64_t)n * C * HW, (uint32_t)C * HWE);
+#pragma unroll
+  for (int blk = 0; blk < 2 * CB; ++blk) {
+    const int gh = h0 + 2 * wave + blk / CB, gw = w0 + 16 * (blk % CB) + col16;
+    const uint32_t po = (gh < H && gw < W) ? (uint32_t)(gh * W + gw) * (uint32_t)E : kOob;
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = 32 * kk + 8 * quad + e;
+        v[e] = buf_load1<T>(yres, i < C ? po + (uint32_t)i * HWE : kOob);
+      }
+      M::pack(v, bfr[blk][kk]);
+    }
+  }
+}
+
 // a: x (forward) or grad_cat (BX); out: the concat (forward); part: the
 // per-workgroup partials (BX), [N][tiles][cblocks][16][LH][LWp] fp32, halo
 // column j at position j + pad and zero at the positions no column maps to:
@@ -272,88 +400,7 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
     for (int i = tid; i < g.plane / 4; i += kGtThreads)
       reinterpret_cast<f32x4*>(xs)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   } else {
-    // ---- halo tile of x (zero outside the image) -> LDS planes; the tile's
-    //      own pixels also go to the identity channels of the output
-    const BufRes xres = make_buf(a + ((int64_t)n * C + c0) * HW, (uint32_t)nch * HWE);
-    const BufRes ores = make_buf(out + ((int64_t)n * 4 * C + c0) * HW, (uint32_t)nch * HWE);
-    if (g.vec) {
-      // a task = (4-channel plane, halo row, 4 image columns a multiple of 4
-      // apart from column 0): one 16-byte (8-byte) access per channel, the
-      // 4 x 4 block transposed in registers into four 4-channel entries
-      const int gpr = g.LWp / 4, cpos = R + g.pad;
-      const int tasks = 4 * g.LH * gpr;
-      for (int task = tid; task < tasks; task += kGtThreads) {
-        const int k = task % gpr, rest = task / gpr;
-        const int i = rest % g.LH, grp = rest / g.LH;
-        const int gh = h0 - R + i, gc = w0 - cpos + 4 * k;
-        const bool in = (unsigned)gh < (unsigned)H && (unsigned)gc < (unsigned)W;
-        const uint32_t off = in ? (uint32_t)(gh * W + gc) * (uint32_t)E : kOob;
-        uint32_t v[4][4];  // [channel][column]
-#pragma unroll
-        for (int e = 0; e < 4; ++e) gf_load4_raw<E>(xres, off + (uint32_t)(4 * grp + e) * HWE, v[e]);
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const int j = 4 * k + m - g.pad;
-          if (j < 0 || j >= LW) continue;
-          XQ q;
-          if constexpr (E == 4) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) q[e] = v[e][m];
-          } else {
-            q[0] = v[0][m] | (v[1][m] << 16);
-            q[1] = v[2][m] | (v[3][m] << 16);
-          }
-          *reinterpret_cast<XQ*>(xs + grp * g.plane + (i * LW + j) * XB) = q;
-        }
-        if (i >= R && i < R + kGtTH && 4 * k >= cpos && 4 * k < cpos + TW) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) gf_store4_raw<E>(ores, off + (uint32_t)(4 * grp + e) * HWE, v[e]);
-        }
-      }
-    } else {
-      // element-wise: two pixels per thread and batch, 32 loads in flight
-      // before any LDS write
-      for (int p0 = tid; p0 < g.npix; p0 += 2 * kGtThreads) {
-        uint32_t lo[2], so[2];
-        int pix[2];
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          pix[s] = p0 + s * kGtThreads;
-          const int i = pix[s] / LW, j = pix[s] - i * LW;
-          const int gh = h0 - R + i, gw = w0 - R + j;
-          const bool in =
-              pix[s] < g.npix && (unsigned)gh < (unsigned)H && (unsigned)gw < (unsigned)W;
-          const bool inner = i >= R && i < R + kGtTH && j >= R && j < R + TW;
-          lo[s] = in ? (uint32_t)(gh * W + gw) * (uint32_t)E : kOob;
-          so[s] = (in && inner) ? lo[s] : kOob;
-        }
-        uint32_t v[2][16];
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-#pragma unroll
-          for (int ch = 0; ch < 16; ++ch) v[s][ch] = gf_load_raw<E>(xres, lo[s] + ch * HWE);
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-#pragma unroll
-          for (int ch = 0; ch < 16; ++ch) gf_store_raw<E>(ores, so[s] + ch * HWE, v[s][ch]);
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          if (pix[s] >= g.npix) continue;
-#pragma unroll
-          for (int grp = 0; grp < 4; ++grp) {
-            XQ q;
-            if constexpr (E == 4) {
-#pragma unroll
-              for (int e = 0; e < 4; ++e) q[e] = v[s][4 * grp + e];
-            } else {
-              q[0] = v[s][4 * grp] | (v[s][4 * grp + 1] << 16);
-              q[1] = v[s][4 * grp + 2] | (v[s][4 * grp + 3] << 16);
-            }
-            *reinterpret_cast<XQ*>(xs + grp * g.plane + pix[s] * XB) = q;
-          }
-        }
-      }
-    }
+    gt_stage_x<T, XB>(a, out, xs, g, n, c0, nch, h0, w0, TW, tid);
   }
 
   // ---- bias rows of this channel block, [bt][16]
@@ -367,27 +414,7 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
 
   // ---- y operand (unshifted pixels) of this wave's blocks
   V bfr[NBW][NK][P];
-  auto pix_off = [&](int blk) {  // byte offset of this lane's pixel in a plane
-    const int gh = h0 + 2 * wave + blk / CB, gw = w0 + 16 * (blk % CB) + col16;
-    return (gh < H && gw < W) ? (uint32_t)(gh * W + gw) * (uint32_t)E : kOob;
-  };
-  {
-    const BufRes yres = make_buf(y + (int64_t)n * C * HW, (uint32_t)C * HWE);
-#pragma unroll
-    for (int blk = 0; blk < NBW; ++blk) {
-      const uint32_t po = pix_off(blk);
-#pragma unroll
-      for (int kk = 0; kk < NK; ++kk) {
-        float v[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int i = 32 * kk + 8 * quad + e;
-          v[e] = buf_load1<T>(yres, i < C ? po + (uint32_t)i * HWE : kOob);
-        }
-        M::pack(v, bfr[blk][kk]);
-      }
-    }
-  }
+  gt_load_y<T, NK, CB>(y, bfr, g, n, h0, w0, wave, col16, quad);
   __syncthreads();
 
   // Addresses inside the loop are a lane part, kept in a few registers, plus
@@ -473,8 +500,10 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
       for (int blk = 0; blk < NBW; ++blk) {
         f32x4* __restrict__ pa = reinterpret_cast<f32x4*>(xs + lb + ebase(blk) + shift);
         f32x4 s = *pa;
+        float q[4];
+        quant4<T>(dacc[blk], q);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) s[e] = fmaf(quant<T>(dacc[blk][e]), go[blk][e], s[e]);
+        for (int e = 0; e < 4; ++e) s[e] = fmaf(q[e], go[blk][e], s[e]);
         *pa = s;
       }
     } else {
@@ -490,8 +519,10 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
           for (int e = 0; e < 4; ++e)
             xv[e] = to_f(__builtin_bit_cast(T, (unsigned short)(xq[e >> 1] >> (16 * (e & 1)))));
         }
+        float q[4];
+        quant4<T>(dacc[blk], q);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[blk][e] = fmaf(quant<T>(dacc[blk][e]), xv[e], acc[blk][e]);
+        for (int e = 0; e < 4; ++e) acc[blk][e] = fmaf(q[e], xv[e], acc[blk][e]);
       }
       if (t == KK - 1) {
         // ---- branch b: channels c0 + 4*quad + e of output block b+1
