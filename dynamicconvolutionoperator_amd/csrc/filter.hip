@@ -23,6 +23,8 @@
 
 #include "ddpm_common.h"
 
+#include <type_traits>
+
 namespace ddpm {
 
 struct FilterGeom {
@@ -78,12 +80,13 @@ __device__ __forceinline__ void buf_loadv(BufRes r, uint32_t off, float (&v)[V])
 }
 
 // Stage plane[h0 - R .. h0 + TH + R) x [w0 - CP .. w0 + TW + CP) into LDS as
-// fp32 (zero outside the image), phase-split by V.  Items are (row, V-wide
+// TS (fp32, or the plane's own 2-byte type: half the LDS; zero outside the
+// image), phase-split by V.  Items are (row, V-wide
 // column group); W % V == 0 so a group is inside or outside the image as a
 // whole.  Each thread issues a batch of branch-free buffer loads before
 // writing any of them, so the loads are in flight together.
-template <typename T, int V>
-__device__ __forceinline__ void stage_plane(float* __restrict__ s, const T* __restrict__ plane,
+template <typename T, int V, typename TS = float>
+__device__ __forceinline__ void stage_plane(TS* __restrict__ s, const T* __restrict__ plane,
                                             const FilterGeom& g, int h0, int w0) {
   constexpr int NB = 8;
   const int groups = (g.TW + 2 * g.CP) / V;
@@ -105,20 +108,20 @@ __device__ __forceinline__ void stage_plane(float* __restrict__ s, const T* __re
     for (int k = 0; k < NB; ++k) {
       if (dst[k] >= 0) {
 #pragma unroll
-        for (int e = 0; e < V; ++e) s[dst[k] + e * g.PS] = v[k][e];
+        for (int e = 0; e < V; ++e) s[dst[k] + e * g.PS] = from_f<TS>(v[k][e]);
       }
     }
   }
 }
 
 // Staged value at tile row `lrow` (0 = first staged row) and staged column j.
-template <int V>
-__device__ __forceinline__ float staged(const float* __restrict__ s, const FilterGeom& g, int lrow,
+template <int V, typename TS = float>
+__device__ __forceinline__ float staged(const TS* __restrict__ s, const FilterGeom& g, int lrow,
                                         int j) {
   if constexpr (V == 1) {
-    return s[lrow * g.RS + j];
+    return to_f(s[lrow * g.RS + j]);
   } else {
-    return s[lrow * g.RS + (j & (V - 1)) * g.PS + (j / V)];
+    return to_f(s[lrow * g.RS + (j & (V - 1)) * g.PS + (j / V)]);
   }
 }
 
@@ -446,7 +449,12 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_vec_kernel(const 
   static_assert(KS >= 1 && V * sizeof(TK) == 16, "16-byte kernel chunks, fixed K");
   constexpr int KK = KS * KS, r = KS / 2;
   constexpr uint32_t E = sizeof(TK);
-  extern __shared__ float gs[];
+  // the gradient planes are staged in their own type: 2-byte planes take
+  // half the LDS of fp32 ones (more workgroups per CU; the tall K = 5 tiles
+  // fit two per CU)
+  typedef typename std::conditional<sizeof(TK) == 2, TK, float>::type TS;
+  extern __shared__ __attribute__((aligned(16))) unsigned char gsm[];
+  TS* __restrict__ gs = reinterpret_cast<TS*>(gsm);
   const int bid = blockIdx.x;
   const int plane = bid / g.tiles;
   const int tile = bid - plane * g.tiles;
@@ -493,7 +501,7 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_vec_kernel(const 
   u32x4 nxt[KS][2];
   load_row(0, 0, nxt);
 #pragma unroll
-  for (int b = 0; b < 3; ++b) stage_plane<TK, V>(gs + b * lplane, gp + (b + 1) * gstride, g, h0, w0);
+  for (int b = 0; b < 3; ++b) stage_plane<TK, V, TS>(gs + b * lplane, gp + (b + 1) * gstride, g, h0, w0);
   __syncthreads();
   if (!active) return;  // no barrier below
 
@@ -515,7 +523,7 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_vec_kernel(const 
     }
     if (it + 1 < 3 * KS) load_row((it + 1) / KS, (it + 1) % KS, nxt);
     const int d = dil_of(b, g.d0, g.d1, g.d2);
-    const float* __restrict__ gb = gs + b * lplane;
+    const TS* __restrict__ gb = gs + b * lplane;
     const int lrow = trow + g.R - (ki - r) * d;
 #pragma unroll
     for (int kj = 0; kj < KS; ++kj) {
@@ -525,7 +533,7 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_vec_kernel(const 
       realign<TK, V>(cur[kj][0], cur[kj][1], s, kv);
       const int j0 = jc - dw;
 #pragma unroll
-      for (int v = 0; v < V; ++v) acc[v] = fmaf(kv[v], staged<V>(gb, g, lrow, j0 + v), acc[v]);
+      for (int v = 0; v < V; ++v) acc[v] = fmaf(kv[v], staged<V, TS>(gb, g, lrow, j0 + v), acc[v]);
     }
   }
   VecIO<TX, V>::store(gx + (int64_t)plane * HW + (int64_t)gh * g.W + gw, acc);
@@ -641,7 +649,9 @@ int launch_ks(FilterOp op, const void* a, const void* b, void* o, const FilterGe
       if constexpr (KS >= 1 && 16 % sizeof(TK) == 0) {
         constexpr int VK = 16 / (int)sizeof(TK);
         if (vec == VK)
-          return launch_kernel(filter_bwd_x_vec_kernel<TX, TK, KS, VK>, g, 3 * lds1, stream, (const TK*)a, (const TK*)b, (TX*)o, g);
+          return launch_kernel(filter_bwd_x_vec_kernel<TX, TK, KS, VK>, g,
+                               (size_t)3 * g.LH * g.RS * (sizeof(TK) == 2 ? 2 : 4), stream,
+                               (const TK*)a, (const TK*)b, (TX*)o, g);
       }
       // 4 pixels per lane only for K <= 3 (larger K would not keep the
       // in-flight kernel values in registers)
@@ -689,11 +699,12 @@ int run_filter(FilterOp op, const void* a, const void* b, void* o, int64_t n, in
     const bool kvec = (k == 1 || k == 3 || k == 5) && w % v == 0 && aligned(a, 16) &&
                       aligned(b, 16) && aligned(o, 16) &&
                       (int64_t)k * k * h * w * (int64_t)esize(k_dtype) <= 0x7fffffffLL;
-    // ... and the three staged tiles leave room for two workgroups per CU
-    // (measured: at K = 5 with 2-byte kernels the tall halo tiles, ~90 KB,
-    // made the vector gather 30% slower than the one-pixel-per-lane one)
+    // ... and the three staged tiles (fp32, or 2-byte for 2-byte gradients)
+    // leave room for two workgroups per CU (measured: at K = 5 with fp32
+    // tiles of ~90 KB the vector gather was 30% slower than the
+    // one-pixel-per-lane one)
     if (kvec && make_geom(g, n, c, h, w, k, d0, d1, d2, v, v, 3, true) == kOk &&
-        (size_t)3 * g.LH * g.RS * sizeof(float) <= kFilterMaxLds / 2) {
+        (size_t)3 * g.LH * g.RS * esize(k_dtype) <= kFilterMaxLds / 2) {
       return with_type(x_dtype, [&](auto tx) {
         using TX = decltype(tx);
         return with_type(k_dtype, [&](auto tk) {
