@@ -191,6 +191,17 @@ struct VecIO {
       for (int e = 0; e < VEC; ++e) v[e] = to_f(t[e]);
     }
   }
+  static __device__ __forceinline__ void store_nt(T* p, const float (&v)[VEC]) {
+    if constexpr (VEC == 1) {
+      __builtin_nontemporal_store(from_f<T>(v[0]), p);
+    } else {
+      typedef T TV __attribute__((ext_vector_type(VEC)));
+      TV t;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) t[e] = from_f<T>(v[e]);
+      __builtin_nontemporal_store(t, reinterpret_cast<TV*>(p));
+    }
+  }
   static __device__ __forceinline__ void store(T* p, const float (&v)[VEC]) {
     if constexpr (VEC == 1) {
       p[0] = from_f<T>(v[0]);
@@ -213,6 +224,11 @@ struct VecIO {
 typedef __amdgpu_buffer_rsrc_t BufRes;
 constexpr uint32_t kOob = 0x80000000u;
 
+// Cache-policy operand of the raw buffer store builtins selecting a
+// non-temporal (streaming) store on gfx950: for output planes that a kernel
+// writes once and does not read back.
+constexpr int kNtStore = 2;
+
 __device__ __forceinline__ BufRes make_buf(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
@@ -230,13 +246,13 @@ __device__ __forceinline__ float buf_load1(BufRes r, uint32_t off) {
 
 // Buffer stores follow the same rule: a store at or beyond num_records is
 // dropped, so masked lanes write nothing without a branch.
-template <typename T>
+template <typename T, int AUX = 0>
 __device__ __forceinline__ void buf_store1(BufRes r, uint32_t off, float v) {
   if constexpr (sizeof(T) == 4) {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, AUX);
   } else {
     __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, from_f<T>(v)), r, off,
-                                          0, 0);
+                                          0, AUX);
   }
 }
 

@@ -9,7 +9,7 @@
 //     LDS as fp32, zero outside the image, so all dilations read it there;
 //   * forward / dK: a lane owns V consecutive pixels (16 bytes of kernel
 //     plane: V = 4 for fp32, 8 for 2-byte types; 8 bytes, V = 4, for the
-//     2-byte forward at K <= 3) and streams its 3*K*K kernel planes with
+//     2-byte forward at K <= 5) and streams its 3*K*K kernel planes with
 //     non-temporal vector loads issued before the x tile is staged (2-byte
 //     forward: one branch's ahead); the LDS tile is stored phase-split (column j at phase j % V,
 //     index j / V) so each of a lane's V shifted reads is bank-conflict free;
@@ -19,7 +19,8 @@
 //     wave-uniform shift) where the staged tiles fit two workgroups per CU;
 //     otherwise one pixel in each of U column blocks of 64, so every load of
 //     a kernel plane is 64 consecutive elements;
-//   * FP32 accumulation; outputs written once, no Unfold buffers.
+//   * FP32 accumulation; outputs written once with non-temporal vector
+//     stores (streamed, not read back by the kernel), no Unfold buffers.
 
 #include "ddpm_common.h"
 
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(kFilterThreads) void filter_fwd_kernel(const TX* __
     float xv[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) xv[v] = staged<V>(xs, g, trow + g.R, jc + v);
-    VecIO<TK, V>::store(op, xv);
+    VecIO<TK, V>::store_nt(op, xv);
   }
 #pragma unroll
   for (int b = 0; b < 3; ++b) {
@@ -216,7 +217,7 @@ __global__ __launch_bounds__(kFilterThreads) void filter_fwd_kernel(const TX* __
         for (int v = 0; v < V; ++v) acc[v] = fmaf(to_f(kv[v]), staged<V>(xs, g, lrow, j0 + v), acc[v]);
       }
     }
-    VecIO<TK, V>::store(op + (b + 1) * ostride, acc);
+    VecIO<TK, V>::store_nt(op + (b + 1) * ostride, acc);
     if constexpr (ROLL) {
 #pragma unroll
       for (int t = 0; t < KS * KS; ++t) kpre[t] = knx[t];
@@ -272,7 +273,9 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_k_kernel(const TX* 
         float prod[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) prod[v] = go[b][v] * staged<V>(xs, g, lrow, j0 + v);
-        VecIO<TK, V>::store(kp + b * bstride + (int64_t)(ki * K + kj) * HW, prod);
+        // non-temporal: the 3*K*K planes are written once and not read back
+        // here (measured 17% faster than plain stores at 256x256)
+        VecIO<TK, V>::store_nt(kp + b * bstride + (int64_t)(ki * K + kj) * HW, prod);
       }
     }
   }
@@ -536,7 +539,7 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_vec_kernel(const 
       for (int v = 0; v < V; ++v) acc[v] = fmaf(kv[v], staged<V, TS>(gb, g, lrow, j0 + v), acc[v]);
     }
   }
-  VecIO<TX, V>::store(gx + (int64_t)plane * HW + (int64_t)gh * g.W + gw, acc);
+  VecIO<TX, V>::store_nt(gx + (int64_t)plane * HW + (int64_t)gh * g.W + gw, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -719,9 +722,10 @@ int run_filter(FilterOp op, const void* a, const void* b, void* o, int64_t n, in
     lw = (w >= 256 && k <= 3) ? 4 : 1;
   } else {
     // 16 bytes of kernel plane per lane where rows and bases allow it; the
-    // 2-byte forward at K <= 3 uses 8 (measured 4% faster at 256x256: fewer
-    // registers for the kernel vectors in flight, more waves per SIMD)
-    const int v = (k_dtype == kF32 || (op == FilterOp::kFwd && k <= 3)) ? 4 : 8;
+    // 2-byte forward at K <= 5 uses 8 (fewer registers for the kernel vectors
+    // in flight, more waves per SIMD: measured 4% faster at 256x256 K=3, 19%
+    // at 128x128 K=5)
+    const int v = (k_dtype == kF32 || (op == FilterOp::kFwd && k <= 5)) ? 4 : 8;
     // `a` is x for both; its V-wide groups are read as one vector
     const bool ok = (w % v == 0) && aligned(b, 16) && aligned(o, 16) &&
                     aligned(a, (size_t)v * esize(x_dtype));
