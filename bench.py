@@ -481,6 +481,9 @@ def kernel_mode(args):
                                                        wsb, *shp, code, s),
         "ddpm_gen_bwd_w": lambda t: lib.ddpm_gen_bwd_w(ptr(t["x"]), ptr(t["y"]), ptr(t["go"]), ptr(dw),
                                                        ptr(db), ptr(ws), wsb, *shp, code, s),
+        # the generator 1x1 convolution of the materialized route writes the kernel tensor
+        "ddpm_gen_kernels": lambda t: lib.ddpm_gen_kernels(ptr(t["y"]), ptr(wt), ptr(bs), ptr(t["kern"]), B, C,
+                                                           hw, hw, k, code, s),
         "ddpm_filter_fwd": lambda t: lib.ddpm_filter_fwd(ptr(t["x"]), ptr(t["kern"]), ptr(out), *shp, code,
                                                          code, s),
         "ddpm_filter_bwd_x": lambda t: lib.ddpm_filter_bwd_x(ptr(t["go"]), ptr(t["kern"]), ptr(dx), *shp,

@@ -226,7 +226,9 @@ constexpr uint32_t kOob = 0x80000000u;
 
 // Cache-policy operand of the raw buffer store builtins selecting a
 // non-temporal (streaming) store on gfx950: for output planes that a kernel
-// writes once and does not read back.
+// writes once, in whole 128-byte lines, and does not read back (stores of
+// partial lines -- the 64- and 32-byte pixel runs of the fused forward's
+// fragment-shaped stores -- measured 25-37% more HBM write bytes with it).
 constexpr int kNtStore = 2;
 
 __device__ __forceinline__ BufRes make_buf(const void* base, uint32_t bytes) {

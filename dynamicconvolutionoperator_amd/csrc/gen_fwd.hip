@@ -211,7 +211,7 @@ __global__ __launch_bounds__(kGtThreads) __attribute__((amdgpu_waves_per_eu(gt_w
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-          for (int e = 0; e < 2; ++e) buf_store1<T, kNtStore>(bres, goff(blk, mb, e), acc[blk][mb][e]);
+          for (int e = 0; e < 2; ++e) buf_store1<T>(bres, goff(blk, mb, e), acc[blk][mb][e]);
     }
   }
 }

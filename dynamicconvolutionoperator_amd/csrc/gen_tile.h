@@ -171,11 +171,11 @@ __device__ __forceinline__ void gf_load4_raw(BufRes r, uint32_t off, uint32_t (&
 template <int E>
 __device__ __forceinline__ void gf_store4_raw(BufRes r, uint32_t off, const uint32_t (&v)[4]) {
   if constexpr (E == 4) {
-    __builtin_amdgcn_raw_buffer_store_b128((u32x4){v[0], v[1], v[2], v[3]}, r, off, 0, kNtStore);
+    __builtin_amdgcn_raw_buffer_store_b128((u32x4){v[0], v[1], v[2], v[3]}, r, off, 0, 0);
   } else {
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     __builtin_amdgcn_raw_buffer_store_b64((u32x2){v[0] | (v[1] << 16), v[2] | (v[3] << 16)}, r,
-                                          off, 0, kNtStore);
+                                          off, 0, 0);
   }
 }
 
@@ -537,7 +537,7 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
 #pragma unroll
         for (int blk = 0; blk < NBW; ++blk)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) buf_store1<T, kNtStore>(bres, goff(lo, blk, e), acc[blk][e]);
+          for (int e = 0; e < 4; ++e) buf_store1<T>(bres, goff(lo, blk, e), acc[blk][e]);
       }
     }
     lds_barrier();
