@@ -101,6 +101,22 @@ __global__ __launch_bounds__(kGtThreads) __attribute__((amdgpu_waves_per_eu(gt_w
   const int c0 = cb * 16;
   const int nch = C - c0 < 16 ? C - c0 : 16;
 
+  // x halo tile first (its loads are consumed here); then the bias rows, the
+  // weight slices and the y operand, all in flight together
+  gt_stage_x<T, XB, CB>(x, out, xs, g, n, c0, nch, h0, w0, TW, tid);
+  // ---- bias rows [ps][mb*16 + m], written to LDS at the end of the prologue
+  static_assert(NPS * 32 <= kGtThreads, "one bias value per thread");
+  uint32_t bv;
+  {
+    const int ps = tid >> 5, rr = tid & 31;
+    const int mb = rr >> 4, m = rr & 15;
+    const int b = ps / NPB, j = ps - b * NPB;
+    const int c = c0 + 8 * mb + (m >> 1), t = 2 * j + (m & 1);
+    const BufRes bres = make_buf(bias, (uint32_t)(3 * C * KK * E));
+    bv = gf_load_raw<E>(bres, (tid < NPS * 32 && c < C && t < KK)
+                                  ? (uint32_t)((b * C + c) * KK + t) * (uint32_t)E
+                                  : kOob);
+  }
   // ---- every pair step's weight slice -> LDS: unit (ps, mb, kk, lane) holds
   //      the 16 bytes W[(b, c0 + 8mb + m/2, 2j + m%2)][kk*32 + 8q .. +7],
   //      m = lane & 15, q = lane >> 4 (zero for tap 9 and channels >= C)
@@ -119,17 +135,9 @@ __global__ __launch_bounds__(kGtThreads) __attribute__((amdgpu_waves_per_eu(gt_w
           0);
     }
   }
-  // ---- bias rows [ps][mb*16 + m]
-  for (int idx = tid; idx < NPS * 32; idx += kGtThreads) {
-    const int ps = idx >> 5, rr = idx & 31;
-    const int mb = rr >> 4, m = rr & 15;
-    const int b = ps / NPB, j = ps - b * NPB;
-    const int c = c0 + 8 * mb + (m >> 1), t = 2 * j + (m & 1);
-    bs[idx] = (c < C && t < KK) ? to_f(bias[(int64_t)(b * C + c) * KK + t]) : 0.f;
-  }
-  gt_stage_x<T, XB>(x, out, xs, g, n, c0, nch, h0, w0, TW, tid);
   V bfr[NBW][NK][1];
   gt_load_y<T, NK, CB>(y, bfr, g, n, h0, w0, wave, col16, quad);
+  if (tid < NPS * 32) bs[tid] = gf_raw_to_f<T>(bv);
   __builtin_amdgcn_s_waitcnt(0);  // the LDS-direct weight copies
   __syncthreads();
 
@@ -139,9 +147,9 @@ __global__ __launch_bounds__(kGtThreads) __attribute__((amdgpu_waves_per_eu(gt_w
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
     lb[mb] = (uint32_t)((2 * mb + (quad >> 1)) * g.plane + col16 * XB + 4 * (quad & 1));
-  auto ebase = [&](int blk) {
-    return (uint32_t)(((2 * wave + blk / CB + R) * LW + 16 * (blk % CB) + R) * XB);
-  };
+  // byte offset of row rr (0, 1) of this wave's blocks at zero shift; block
+  // blk sits at row blk / CB, 16 * (blk % CB) entries to the right
+  auto rbase = [&](int rr) { return (uint32_t)(((2 * wave + rr + R) * LW + R) * XB); };
   // global byte offset of channel c0 + 8mb + 2q + e at this lane's pixel of
   // block blk (kOob outside the image or the channel block)
   auto goff = [&](int blk, int mb, int e) {
@@ -191,11 +199,14 @@ __global__ __launch_bounds__(kGtThreads) __attribute__((amdgpu_waves_per_eu(gt_w
     for (int mb = 0; mb < 2; ++mb) {
       uint32_t l = lb[mb];
       asm volatile("" : "+v"(l));
+      // one base per (row, shift); the block's column is the reads' immediate offset
+      const unsigned char* __restrict__ p0[2] = {xs + l + (rbase(0) + sh0), xs + l + (rbase(1) + sh0)};
+      const unsigned char* __restrict__ p1[2] = {xs + l + (rbase(0) + sh1), xs + l + (rbase(1) + sh1)};
 #pragma unroll
       for (int blk = 0; blk < NBW; ++blk) {
-        const unsigned char* px = xs + l + ebase(blk);
-        const uint32_t x0 = *reinterpret_cast<const uint32_t*>(px + sh0);
-        const uint32_t x1 = *reinterpret_cast<const uint32_t*>(px + sh1);
+        const int co = 16 * (blk % CB) * XB;
+        const uint32_t x0 = *reinterpret_cast<const uint32_t*>(p0[blk / CB] + co);
+        const uint32_t x1 = *reinterpret_cast<const uint32_t*>(p1[blk / CB] + co);
         const uint32_t qa = pack2<T>(dacc[mb][blk][0], dacc[mb][blk][1]);
         const uint32_t qb = pack2<T>(dacc[mb][blk][2], dacc[mb][blk][3]);
         acc[blk][mb][0] = dot2<T>(qa, __builtin_amdgcn_perm(x1, x0, sela), acc[blk][mb][0]);

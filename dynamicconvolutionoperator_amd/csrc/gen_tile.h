@@ -145,6 +145,14 @@ __device__ __forceinline__ uint32_t gf_load_raw(BufRes r, uint32_t off) {
   else
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
 }
+// The value of a raw element loaded by gf_load_raw<sizeof(T)>.
+template <typename T>
+__device__ __forceinline__ float gf_raw_to_f(uint32_t r) {
+  if constexpr (sizeof(T) == 4)
+    return __uint_as_float(r);
+  else
+    return to_f(__builtin_bit_cast(T, (unsigned short)r));
+}
 template <int E>
 __device__ __forceinline__ void gf_store_raw(BufRes r, uint32_t off, uint32_t v) {
   if constexpr (E == 4)
@@ -156,34 +164,11 @@ __device__ __forceinline__ void gf_store_raw(BufRes r, uint32_t off, uint32_t v)
 // 4 consecutive elements at byte offset `off` (16-byte aligned for fp32,
 // 8-byte for 2-byte types) as raw bits, one element per dword, and the
 // matching store.
-template <int E>
-__device__ __forceinline__ void gf_load4_raw(BufRes r, uint32_t off, uint32_t (&v)[4]) {
-  if constexpr (E == 4) {
-    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) v[m] = a[m];
-  } else {
-    const auto a = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) v[m] = (a[m >> 1] >> (16 * (m & 1))) & 0xffffu;
-  }
-}
-template <int E>
-__device__ __forceinline__ void gf_store4_raw(BufRes r, uint32_t off, const uint32_t (&v)[4]) {
-  if constexpr (E == 4) {
-    __builtin_amdgcn_raw_buffer_store_b128((u32x4){v[0], v[1], v[2], v[3]}, r, off, 0, 0);
-  } else {
-    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    __builtin_amdgcn_raw_buffer_store_b64((u32x2){v[0] | (v[1] << 16), v[2] | (v[3] << 16)}, r,
-                                          off, 0, 0);
-  }
-}
-
 // Halo tile of x (zero outside the image) -> the 4 LDS planes of 4-channel
 // entries (XB bytes each) for the workgroup's 16-channel block starting at
 // channel c0 (nch of them), tile rows h0.., columns w0..; the tile's own
 // pixels also go to the identity channels of the concat `out`.
-template <typename T, int XB>
+template <typename T, int XB, int CB>
 __device__ __forceinline__ void gt_stage_x(const T* __restrict__ a, T* __restrict__ out,
                                            unsigned char* __restrict__ xs, const TileGeom& g,
                                            int n, int c0, int nch, int h0, int w0, int TW,
@@ -203,32 +188,67 @@ __device__ __forceinline__ void gt_stage_x(const T* __restrict__ a, T* __restric
     // 4 x 4 block transposed in registers into four 4-channel entries
     const int gpr = g.LWp / 4, cpos = R + g.pad;
     const int tasks = 4 * g.LH * gpr;
-    for (int task = tid; task < tasks; task += kGtThreads) {
-      const int k = task % gpr, rest = task / gpr;
-      const int i = rest % g.LH, grp = rest / g.LH;
-      const int gh = h0 - R + i, gc = w0 - cpos + 4 * k;
-      const bool in = (unsigned)gh < (unsigned)H && (unsigned)gc < (unsigned)W;
-      const uint32_t off = in ? (uint32_t)(gh * W + gc) * (uint32_t)E : kOob;
-      uint32_t v[4][4];  // [channel][column]
+    // up to U tasks per thread with their loads in flight together: one
+    // memory round trip for the whole halo tile up to R = 8 (at most 5, 3
+    // and 2 tasks per thread for 64-, 32- and 16-column tiles); the elements
+    // stay packed as loaded
+    constexpr int U = CB == 4 ? 5 : CB == 2 ? 3 : 2;
+    constexpr int ND = E == 4 ? 4 : 2;  // dwords of one channel's 4 columns
+    typedef uint32_t VD __attribute__((ext_vector_type(ND)));
+    for (int t0 = tid; t0 < tasks; t0 += U * kGtThreads) {
+      VD v[U][4];  // [task][channel]
+      uint32_t off[U];
+      int ti[U], tk[U], tg[U];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) gf_load4_raw<E>(xres, off + (uint32_t)(4 * grp + e) * HWE, v[e]);
+      for (int u = 0; u < U; ++u) {
+        const int task = t0 + u * kGtThreads;
+        const int k = task % gpr, rest = task / gpr;
+        const int i = rest % g.LH, grp = task < tasks ? rest / g.LH : 0;
+        const int gh = h0 - R + i, gc = w0 - cpos + 4 * k;
+        const bool in = task < tasks && (unsigned)gh < (unsigned)H && (unsigned)gc < (unsigned)W;
+        off[u] = in ? (uint32_t)(gh * W + gc) * (uint32_t)E : kOob;
+        ti[u] = i;
+        tk[u] = k;
+        tg[u] = grp;
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const int j = 4 * k + m - g.pad;
-        if (j < 0 || j >= LW) continue;
-        XQ q;
-        if constexpr (E == 4) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) q[e] = v[e][m];
-        } else {
-          q[0] = v[0][m] | (v[1][m] << 16);
-          q[1] = v[2][m] | (v[3][m] << 16);
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t o = off[u] + (uint32_t)(4 * grp + e) * HWE;
+          if constexpr (E == 4)
+            v[u][e] = __builtin_amdgcn_raw_buffer_load_b128(xres, o, 0, 0);
+          else
+            v[u][e] = __builtin_amdgcn_raw_buffer_load_b64(xres, o, 0, 0);
         }
-        *reinterpret_cast<XQ*>(xs + grp * g.plane + (i * LW + j) * XB) = q;
       }
-      if (i >= R && i < R + kGtTH && 4 * k >= cpos && 4 * k < cpos + TW) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) gf_store4_raw<E>(ores, off + (uint32_t)(4 * grp + e) * HWE, v[e]);
+      for (int u = 0; u < U; ++u) {
+        if (t0 + u * kGtThreads >= tasks) break;
+        const int i = ti[u], k = tk[u], grp = tg[u];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int j = 4 * k + m - g.pad;
+          if (j < 0 || j >= LW) continue;
+          XQ q;
+          if constexpr (E == 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[e] = v[u][e][m];
+          } else {
+            // channels (0, 1) and (2, 3) of column m: halves m & 1 of dword m >> 1
+            const uint32_t sel = (m & 1) ? 0x07060302u : 0x05040100u;
+            q[0] = __builtin_amdgcn_perm(v[u][1][m >> 1], v[u][0][m >> 1], sel);
+            q[1] = __builtin_amdgcn_perm(v[u][3][m >> 1], v[u][2][m >> 1], sel);
+          }
+          *reinterpret_cast<XQ*>(xs + grp * g.plane + (i * LW + j) * XB) = q;
+        }
+        if (i >= R && i < R + kGtTH && 4 * k >= cpos && 4 * k < cpos + TW) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t o = off[u] + (uint32_t)(4 * grp + e) * HWE;
+            if constexpr (E == 4)
+              __builtin_amdgcn_raw_buffer_store_b128(v[u][e], ores, o, 0, 0);
+            else
+              __builtin_amdgcn_raw_buffer_store_b64(v[u][e], ores, o, 0, 0);
+          }
+        }
       }
     }
   } else {
@@ -393,28 +413,50 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
       }
     }
   };
-  wload(0);
-
+  // ---- bias rows of this channel block, [bt][16] (raw buffer loads, kOob
+  //      for the padding: no branch around them)
+  constexpr int NBI = (NBT * 16 + kGtThreads - 1) / kGtThreads;
+  uint32_t bv[NBI];
+  auto bias_load = [&]() {
+    const BufRes bres = make_buf(bias, (uint32_t)(3 * C * KK * E));
+#pragma unroll
+    for (int q = 0; q < NBI; ++q) {
+      const int idx = tid + q * kGtThreads;
+      const int m = idx & 15, bt = idx >> 4;
+      const int b = bt / KK, t = bt - b * KK;
+      bv[q] = gf_load_raw<E>(bres, (idx < NBT * 16 && m < nch)
+                                       ? (uint32_t)((b * C + c0 + m) * KK + t) * (uint32_t)E
+                                       : kOob);
+    }
+  };
+  auto bias_put = [&]() {
+#pragma unroll
+    for (int q = 0; q < NBI; ++q)
+      if (tid + q * kGtThreads < NBT * 16) bs[tid + q * kGtThreads] = gf_raw_to_f<T>(bv[q]);
+  };
+  V bfr[NBW][NK][P];  // y operand (unshifted pixels) of this wave's blocks
   if constexpr (BX) {
+    bias_load();
+    wload(0);
     // ---- accumulator tile = 0
     for (int i = tid; i < g.plane / 4; i += kGtThreads)
       reinterpret_cast<f32x4*>(xs)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    bias_put();
+    wput(0);
+    if (NBT > 1) wload(1);
+    gt_load_y<T, NK, CB>(y, bfr, g, n, h0, w0, wave, col16, quad);
   } else {
-    gt_stage_x<T, XB>(a, out, xs, g, n, c0, nch, h0, w0, TW, tid);
+    // the x halo tile first (its loads are consumed there), then the bias
+    // rows, the first weight slice and the y operand with their loads in
+    // flight together
+    gt_stage_x<T, XB, CB>(a, out, xs, g, n, c0, nch, h0, w0, TW, tid);
+    bias_load();
+    wload(0);
+    gt_load_y<T, NK, CB>(y, bfr, g, n, h0, w0, wave, col16, quad);
+    bias_put();
+    wput(0);
+    if (NBT > 1) wload(1);
   }
-
-  // ---- bias rows of this channel block, [bt][16]
-  for (int idx = tid; idx < NBT * 16; idx += kGtThreads) {
-    const int m = idx & 15, bt = idx >> 4;
-    const int b = bt / KK, t = bt - b * KK;
-    bs[idx] = m < nch ? to_f(bias[(int64_t)(b * C + c0 + m) * KK + t]) : 0.f;
-  }
-  wput(0);
-  if (NBT > 1) wload(1);
-
-  // ---- y operand (unshifted pixels) of this wave's blocks
-  V bfr[NBW][NK][P];
-  gt_load_y<T, NK, CB>(y, bfr, g, n, h0, w0, wave, col16, quad);
   __syncthreads();
 
   // Addresses inside the loop are a lane part, kept in a few registers, plus
@@ -422,11 +464,11 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
   // from hoisting their per-(block, channel) sums out of the loop, which
   // would hold one register each.
   //   LDS entry of this lane's pixel in block blk at zero shift:
-  //     lbase + ebase(blk)
+  //     lbase + rbase(blk / CB) + 16 * (blk % CB) * XB, the last term the
+  //     immediate offset of the LDS access
   const uint32_t lbase = (uint32_t)(quad * g.plane + col16 * XB);
-  auto ebase = [&](int blk) {
-    return (uint32_t)(((2 * wave + blk / CB + R) * LW + 16 * (blk % CB) + R) * XB);
-  };
+  auto rbase = [&](int rr) { return (uint32_t)(((2 * wave + rr + R) * LW + R) * XB); };
+  auto ebase = [&](int blk) { return rbase(blk / CB) + (uint32_t)(16 * (blk % CB) * XB); };
   //   global byte offset of channel 4*quad + e at this lane's pixel of block
   //   blk within a channel block's planes: lofs[blk % CB] + row and channel
   //   parts (kOob outside the image or the channel block)
@@ -472,6 +514,11 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
     const int shift = ((ki - r) * d * LW + (kj - r) * d) * XB;
     uint32_t lb = lbase;
     asm volatile("" : "+v"(lb));
+    // forward: this lane's shifted entry in block rows 0 and 1 (the block's
+    // column is the read's immediate offset); the read-modify-write of BX
+    // measured 1-2% faster with one sum per block
+    const unsigned char* __restrict__ px[2] = {xs + lb + (rbase(0) + shift),
+                                               xs + lb + (rbase(1) + shift)};
     const unsigned char* __restrict__ ab = abuf + (bt & 1) * AU * 16;
     V afr[NK][P];
 #pragma unroll
@@ -509,7 +556,7 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
     } else {
 #pragma unroll
       for (int blk = 0; blk < NBW; ++blk) {
-        const XQ xq = *reinterpret_cast<const XQ*>(xs + lb + ebase(blk) + shift);
+        const XQ xq = *reinterpret_cast<const XQ*>(px[blk / CB] + 16 * (blk % CB) * XB);
         float xv[4];
         if constexpr (E == 4) {
 #pragma unroll
