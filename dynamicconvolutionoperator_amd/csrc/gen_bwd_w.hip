@@ -26,8 +26,10 @@
 // accumulates taps x 16 c x C i with v_mfma_f32_16x16x32_{bf16,f16} (M = c,
 // N = i, K = tokens; fp32 operands run as three bf16 products).  db is one
 // more MFMA per tap and part against a column of ones.  For fp32, y is split
-// into bf16 hi/lo planes once per call by a small kernel, so every B fragment
-// is a plain 16-byte LDS read.
+// into bf16 hi / lo rows while it is staged: each thread loads its 4-column
+// pieces of the next step's y rows into registers at the start of a step and
+// writes their split to LDS after the step's MFMAs (no pre-pass over y, no
+// workspace planes), so every B fragment is a plain 16-byte LDS read.
 
 #include "gen_common.h"
 #include <type_traits>
@@ -55,6 +57,7 @@ struct WGradGeom {
   int xdma;            // x rows start on dword boundaries: LDS-direct dword copies
   int x16;             // x rows hold whole 16-byte chunks (W % (16/E) == 0, aligned): 16-byte copies
   int x4;              // y and gradient rows 16-byte aligned (W % 8 == 0): 16-byte copies
+  int y4;              // fp32 y rows 16-byte aligned (W % 4 == 0): 16-byte register loads
 };
 
 // Tap groups per kernel size: the K = 3 taps are split over three waves of 3
@@ -154,10 +157,9 @@ __global__ __launch_bounds__(256) void gen_ysplit_kernel(const float* __restrict
   }
 }
 
-// yb: y itself (2-byte types) or its bf16 hi / lo planes [n][2][C][H*W] (fp32).
 template <typename T, int KS, int MB>
 __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_partial_kernel(
-    const T* __restrict__ x, const uint16_t* __restrict__ yb, const T* __restrict__ gout,
+    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ gout,
     float* __restrict__ pw, float* __restrict__ pb, T* __restrict__ dw_out, T* __restrict__ db_out,
     WGradGeom g) {
   typedef Mma<T> M;
@@ -173,6 +175,13 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
   constexpr int NT = 64 * NW;
   constexpr int E = (int)sizeof(T);
   constexpr int PC = 16 / E;  // T elements per 16-byte chunk
+  // fp32: y goes through registers and is split into its bf16 hi / lo rows on
+  // the way to LDS; 2-byte types copy y global -> LDS directly
+  constexpr bool kYReg = E == 4;
+  // fp32: db sums the fp32 products on the VALU (frees the registers of the
+  // bias MFMA's accumulators and column of ones); 2-byte types add the
+  // bf16-rounded products with one more MFMA per tap against a column of ones
+  constexpr bool kVBias = E == 4;
   extern __shared__ __attribute__((aligned(16))) uint32_t wsm[];
 
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
@@ -208,7 +217,7 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
   //     column of its chunk.
   constexpr int YRPC = 64 / L::kYC;  // y rows per 1 KB copy
   constexpr int GRPC = 64 / L::kGC;  // gradient rows per 1 KB copy
-  constexpr int NY = L::kYRows / YRPC, NG = 16 / GRPC;
+  constexpr int NY = kYReg ? 0 : L::kYRows / YRPC, NG = 16 / GRPC;
   constexpr int NJ = (NY + NG + NW - 1) / NW;
   int xlo[L::kXI];
 #pragma unroll
@@ -314,7 +323,7 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
     }
     // y rows (P parts x MB*16 channels) and branch-gradient rows (16
     // channels) in the swizzled chunk layout; channels >= C read zero
-    const BufRes yres = make_buf(yb + (int64_t)p.n * P * CHW, (uint32_t)(P * CHW * 2));
+    const BufRes yres = make_buf(y + (int64_t)p.n * CHW, (uint32_t)(CHW * E));
     const BufRes gres = make_buf(gbase + (int64_t)p.n * 4 * CHW, (uint32_t)(CHW * E));
     if (g.x4) {
       // 1 KB copies: lane l moves one 16-byte chunk; the step's byte offset
@@ -347,16 +356,15 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
       // element-wise through registers
       uint16_t* __restrict__ dy = reinterpret_cast<uint16_t*>(dstb + L::kYOff);
       T* __restrict__ dg = reinterpret_cast<T*>(dstb + L::kGOff);
-      constexpr int PY = L::kYRows * kWgTW, PG = 16 * kWgTW;
+      constexpr int PY = kYReg ? 0 : L::kYRows * kWgTW, PG = 16 * kWgTW;
       for (int idx = tid; idx < PY + PG; idx += NT) {
         if (idx < PY) {
           const int row = idx / kWgTW, j = idx - row * kWgTW;
-          const int part = row / (MB * 16), i = row - part * (MB * 16);
+          const int i = row;
           const int w = p.w0 + j;
           const uint32_t off =
-              (i0 + i < C && w < W)
-                  ? ((uint32_t)(part * C + i0 + i) * (uint32_t)HW + rowel + (uint32_t)w) * 2u
-                  : kOob;
+              (i0 + i < C && w < W) ? ((uint32_t)(i0 + i) * (uint32_t)HW + rowel + (uint32_t)w) * 2u
+                                    : kOob;
           const int kc = (j >> 3) ^ (i & 15);
           dy[row * L::kYD * 2 + kc * 8 + (j & 7)] =
               (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(yres, off, 0, 0);
@@ -373,17 +381,70 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
     }
   };
 
+  // ---- fp32 y rows of step `p`: thread tid loads the 4-column pieces u = tid
+  //      + NT*j (row u / 32, columns 4*(u % 32) .. +3) into registers
+  //      (yload, issued before a step's MFMAs) and writes their bf16 hi / lo
+  //      split to the y rows of LDS buffer `buf` (ystore, after them): the
+  //      two 8-byte halves of the row's chunk (u % 32) / 2, swizzled as the
+  //      LDS-direct copies place them.  Columns past the image and channels
+  //      >= C read zero.
+  constexpr int YU = kYReg ? MB * 16 * (kWgTW / 4) : 1;  // 4-column pieces per step
+  constexpr int YUT = (YU + NT - 1) / NT;
+  f32x4 yreg[YUT];
+  auto yload = [&](const WgPos& p) {
+    if constexpr (kYReg) {
+      const BufRes yres = make_buf(y + (int64_t)p.n * CHW, (uint32_t)(CHW * E));
+      const uint32_t rowel = (uint32_t)(p.h * W);
+#pragma unroll
+      for (int j = 0; j < YUT; ++j) {
+        const int u = tid + NT * j;
+        if (YU % NT != 0 && u >= YU) break;  // wave-uniform (NT and YU are multiples of 64)
+        const int i = u >> 5, w = p.w0 + 4 * (u & 31);
+        const bool okc = i0 + i < C;
+        const uint32_t base = ((uint32_t)(i0 + i) * (uint32_t)HW + rowel + (uint32_t)w) * 4u;
+        if (g.y4) {
+          yreg[j] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(yres, okc && w < W ? base : kOob, 0, 0));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            yreg[j][e] = buf_load1<float>(yres, okc && w + e < W ? base + 4u * e : kOob);
+        }
+      }
+    }
+  };
+  auto ystore = [&](int buf) {
+    if constexpr (kYReg) {
+      uint32_t* __restrict__ yl = wsm + buf * L::kBuf + L::kYOff;
+#pragma unroll
+      for (int j = 0; j < YUT; ++j) {
+        const int u = tid + NT * j;
+        if (YU % NT != 0 && u >= YU) break;
+        const int i = u >> 5, q = u & 31;
+        const int dw = i * L::kYD + 4 * ((q >> 1) ^ (i & 15)) + 2 * (q & 1);
+        uint32_t h0, l0, h1, l1;
+        split_bf16x2(yreg[j][0], yreg[j][1], h0, l0);
+        split_bf16x2(yreg[j][2], yreg[j][3], h1, l1);
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<u32x2*>(yl + dw) = (u32x2){h0, h1};
+        *reinterpret_cast<u32x2*>(yl + MB * 16 * L::kYD + dw) = (u32x2){l0, l1};
+      }
+    }
+  };
+
   // B fragment of the bias column: B[k][n] = (n == 0) for every k
   V ones;
-  {
+  if constexpr (!kVBias) {
     const ME one = col16 == 0 ? (ME)1.0f : (ME)0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ones[e] = one;
   }
   f32x4 acc[TPH][MB], accb[TPH];
+  float dbs[TPH];  // kVBias: sum of the lane's products per tap
 #pragma unroll
   for (int tt = 0; tt < TPH; ++tt) {
     accb[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dbs[tt] = 0.f;
 #pragma unroll
     for (int ib = 0; ib < MB; ++ib) acc[tt][ib] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -397,8 +458,10 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
     nxt.h = row - nxt.n * H;
   }
   if (steps > 0) {
+    yload(nxt);
     stage(nxt, 0);
     nxt.advance(g);
+    ystore(0);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -414,7 +477,9 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
   }
   for (int s = 0; s < steps; ++s) {
     const int buf = s & 1;
-    if (s + 1 < steps) {
+    const bool more = s + 1 < steps;
+    if (more) {
+      yload(nxt);
       stage(nxt, buf ^ 1);
       nxt.advance(g);
     }
@@ -457,6 +522,8 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
 #pragma unroll
       for (int e = 0; e < 8; ++e) dk[e] = gv[e] * lds_elem<T>(bb, xel[tt] + e);
       M::pack(dk, af);
+      if constexpr (kVBias)
+        dbs[tt] += ((dk[0] + dk[1]) + (dk[2] + dk[3])) + ((dk[4] + dk[5]) + (dk[6] + dk[7]));
     };
     V afc[P];
     make_afr(0, afc);
@@ -468,12 +535,14 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
       if (tt + 1 < TPH) make_afr(tt + 1, afn);
 #pragma unroll
       for (int ib = 0; ib < MB; ++ib) acc[tt][ib] = M::mac(afc, bfr[ib], acc[tt][ib]);
+      if constexpr (!kVBias) {
 #pragma unroll
-      for (int pp = 0; pp < P; ++pp) accb[tt] = M::mac1(afc[pp], ones, accb[tt]);
+        for (int pp = 0; pp < P; ++pp) accb[tt] = M::mac1(afc[pp], ones, accb[tt]);
+      }
       if (tt + 1 < TPH) {
         __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // LDS reads
 #pragma unroll
-        for (int i = 0; i < MB * (P == 2 ? 3 : 1) + P; ++i) {
+        for (int i = 0; i < MB * (P == 2 ? 3 : 1) + (kVBias ? 0 : P); ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
           __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
         }
@@ -481,6 +550,7 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
 #pragma unroll
       for (int pp = 0; pp < P; ++pp) afc[pp] = afn[pp];
     }
+    if (more) ystore(buf ^ 1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
@@ -498,7 +568,19 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
   static_assert(kWgSegs == 4, "the slice sum below adds four segments");
   float* __restrict__ red = reinterpret_cast<float*>(wsm);  // [segs][KK][16 c][RS]
   float* __restrict__ rb = red + kWgSegs * SL;              // [KK][segs][16 c]
-  if (col16 == 0) {
+  if constexpr (kVBias) {
+    // lanes col16 + 16*quad hold channel col16's sums over their 8 tokens:
+    // added across the quads in a fixed order ((q0 + q1) + (q2 + q3))
+#pragma unroll
+    for (int tt = 0; tt < TPH; ++tt) {
+      const int t = th * TPH + tt;
+      if (t >= KK) break;
+      float v = dbs[tt];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      if (quad == 0) rb[(t * kWgSegs + sg) * 16 + col16] = v;
+    }
+  } else if (col16 == 0) {
 #pragma unroll
     for (int tt = 0; tt < TPH; ++tt) {
       const int t = th * TPH + tt;
@@ -683,15 +765,14 @@ void wgrad_geom(WGradGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int d0
   g.xdma = 0;
   g.x16 = 0;
   g.x4 = 0;
+  g.y4 = 0;
 }
 
-// Workspace: the fp32 split partials (none with one split), then, for fp32,
-// y's bf16 hi / lo planes (256-byte aligned).
+// Workspace: the fp32 split partials (none with one split).
 int64_t wg_partial_bytes(const WGradGeom& g, int64_t c, int k) {
   if (g.direct) return 0;
   return (int64_t)g.splits * 3 * k * k * c * (c + 1) * (int64_t)sizeof(float);
 }
-int64_t wg_align(int64_t v) { return (v + 255) / 256 * 256; }
 
 }  // namespace
 }  // namespace ddpm
@@ -705,9 +786,7 @@ extern "C" int64_t ddpm_gen_bwd_w_workspace_bytes(int64_t n, int64_t c, int64_t 
   if (n * h * ((w + kWgTW - 1) / kWgTW) > 0x7fffffffLL) return 0;
   WGradGeom g;
   wgrad_geom(g, n, c, h, w, 1, 1, 1);
-  const int64_t pbytes = wg_partial_bytes(g, c, kernel_size);
-  // fp32: the bf16 hi / lo planes of y follow the partials
-  return dtype == kF32 ? wg_align(pbytes) + n * 2 * c * h * w * 2 : pbytes;
+  return wg_partial_bytes(g, c, kernel_size);
 }
 
 extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out,
@@ -724,29 +803,24 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
   if (gg.d0 > kWgMaxDil || gg.d1 > kWgMaxDil || gg.d2 > kWgMaxDil) return kUnsupported;
   if (n * h * ((w + kWgTW - 1) / kWgTW) > 0x7fffffffLL) return kUnsupported;
   const int esz = dtype == kF32 ? 4 : 2;
-  // 32-bit buffer offsets inside one image's planes (fp32 y: two 2-byte planes)
-  if (((c + 15) / 16) * 16 * h * w * 4 > 0x7fffffffLL) return kUnsupported;
+  // 32-bit buffer offsets inside one image's planes (channels padded to 16)
+  if (((c + 15) / 16) * 16 * h * w * esz > 0x7fffffffLL) return kUnsupported;
   // 32-bit indices of the split reduction
   if ((int64_t)3 * kernel_size * kernel_size * c * (c + 1) > 0x7fffffffLL) return kUnsupported;
   WGradGeom g;
   wgrad_geom(g, n, c, h, w, gg.d0, gg.d1, gg.d2);
-  const int64_t pbytes = wg_partial_bytes(g, c, kernel_size);
-  const int64_t need = dtype == kF32 ? wg_align(pbytes) + n * 2 * c * h * w * 2 : pbytes;
+  const int64_t need = wg_partial_bytes(g, c, kernel_size);
   if (need > 0 && (!workspace || workspace_bytes < need)) return kWorkspaceTooSmall;
-  uint16_t* ys = dtype == kF32 ? (uint16_t*)((char*)workspace + wg_align(pbytes)) : nullptr;
-  const uint16_t* ysrc = dtype == kF32 ? ys : (const uint16_t*)y;
   // LDS-direct dword copies of x rows need every row to start on a dword boundary
   g.xdma = (esz == 4) || ((w % 2 == 0) && ((uintptr_t)x % 4 == 0));
   g.x16 = (w % (16 / esz) == 0) && ((uintptr_t)x % 16 == 0);
-  g.x4 = (w % 8 == 0) && ((uintptr_t)ysrc % 16 == 0) && ((uintptr_t)grad_out % 16 == 0);
+  g.x4 = (w % 8 == 0) && ((uintptr_t)grad_out % 16 == 0) &&
+         (esz == 4 || (uintptr_t)y % 16 == 0);
+  g.y4 = (w % 4 == 0) && ((uintptr_t)y % 16 == 0);
   const int mb = c > 64 ? 4 : (int)((c + 15) / 16);  // 16-channel blocks of i per workgroup
   const int kk = kernel_size * kernel_size;
   float* pw = g.direct ? nullptr : (float*)workspace;
   float* pb = g.direct ? nullptr : pw + (int64_t)g.splits * 3 * kk * c * c;
-  if (dtype == kF32) {
-    const int e = launch_ysplit((const float*)y, ys, c * h * w, n * c * h * w, stream);
-    if (e != 0) return e;
-  }
   return wg_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
     auto launch = [&](auto ks, auto mbc) {
@@ -763,7 +837,7 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
       if (ae != 0) return ae;
       hipLaunchKernelGGL((gen_bwd_w_partial_kernel<T, KS, MB>), grid,
                          dim3(64 * kWgSegs * WgTaps<KS>::kGroups), lds, stream, (const T*)x,
-                         ysrc, (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g);
+                         (const T*)y, (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g);
       int e = (int)hipGetLastError();
       if (e != 0 || g.direct) return e;
       const int64_t total_w = (int64_t)3 * KKc * c * c;

@@ -180,8 +180,8 @@ int ddpm_gen_bwd_y_noalloc(const void* x, const void* weight, const void* grad_o
 int64_t ddpm_gen_bwd_y_noalloc_scratch_bytes(void);
 
 /* Bytes of workspace ddpm_gen_bwd_w needs for `dtype`: its fp32 split
- * partials (none when one split writes grad_weight / grad_bias directly),
- * then, for fp32, the bf16 hi / lo planes of y; 0 for an invalid dtype.
+ * partials (none when one split writes grad_weight / grad_bias directly; the
+ * same for every dtype); 0 for an invalid dtype.
  * Replaces the partial-buffer sizing of _GeneratorDynamicCat.backward (_triton_kernels.py:1001-1017). */
 int64_t ddpm_gen_bwd_w_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size,
                                        int dtype);
