@@ -260,16 +260,24 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk) {
         const int col = el0 + 16 * blk + dw;
-        float bv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if constexpr (sizeof(T) == 4)
-            bv[e] = __uint_as_float(xq[4 * e * L::kXS + col]);
-          else
-            bv[e] = to_f(reinterpret_cast<const T*>(xq + 4 * e * L::kXS)[col]);
-        }
         V bfr[P];
-        M::pack(bv, bfr);
+        if constexpr (sizeof(T) == 4) {
+          float bv[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) bv[e] = __uint_as_float(xq[4 * e * L::kXS + col]);
+          M::pack(bv, bfr);
+        } else {
+          // the 8 two-byte values as loaded, paired into dwords (no fp32 round trip)
+          const uint16_t* __restrict__ xb = reinterpret_cast<const uint16_t*>(xq);
+          u32x4 wv;
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) {
+            const uint32_t lo = xb[2 * (8 * e2) * L::kXS + col];
+            const uint32_t hi = xb[2 * (8 * e2 + 4) * L::kXS + col];
+            wv[e2] = lo | (hi << 16);
+          }
+          bfr[0] = __builtin_bit_cast(V, wv);
+        }
 #pragma unroll
         for (int ib = 0; ib < MB; ++ib) acc[blk][ib] = M::mac(afr[ib], bfr, acc[blk][ib]);
       }

@@ -274,11 +274,20 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
     }
 #pragma unroll
     for (int kj = 0; kj < 3; ++kj) {
-      float xv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xv[e] = cw_lds_elem<T>(bb, xel[kj] + e);
       V afr[P];
-      M::pack(xv, afr);
+      if constexpr (sizeof(T) == 4) {
+        float xv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[e] = cw_lds_elem<T>(bb, xel[kj] + e);
+        M::pack(xv, afr);
+      } else {
+        // the 8 two-byte values as staged, paired into dwords (no fp32 round trip)
+        const uint16_t* __restrict__ xb = reinterpret_cast<const uint16_t*>(bb) + xel[kj];
+        u32x4 wv;
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) wv[e2] = (uint32_t)xb[2 * e2] | ((uint32_t)xb[2 * e2 + 1] << 16);
+        afr[0] = __builtin_bit_cast(V, wv);
+      }
 #pragma unroll
       for (int ib = 0; ib < MB; ++ib) acc[kj][ib] = M::mac(afr, bfr[ib], acc[kj][ib]);
     }
