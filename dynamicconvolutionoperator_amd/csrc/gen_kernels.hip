@@ -667,6 +667,7 @@ struct GyGeom {
   int stages;            // ceil(oc / KCH)
   int splits;
   int stages_per_split;
+  int dma;               // dK rows start on 16-byte boundaries: LDS-direct chunk copies
 };
 
 template <typename T, int MB>
@@ -753,12 +754,43 @@ __global__ __launch_bounds__(256) void gk_bwd_y_kernel(const T* __restrict__ gk,
   auto stage = [&](int st, int buf) {
     char* dst = reinterpret_cast<char*>(ysm) + buf * L::BUF;
     const int o0 = st * L::ROWS;
+    if (g.dma) {
 #pragma unroll
-    for (int j = 0; j < NDW; ++j) {
-      const int o = o0 + drow[j], px = px0 + dpx[j];
-      const uint32_t off = (o < O && px < HW) ? ((uint32_t)o * (uint32_t)HW + (uint32_t)px) * E : kOob;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          dres, (__attribute__((address_space(3))) void*)(dst + (wave * NDW + j) * 1024), 16, off, 0, 0, 0);
+      for (int j = 0; j < NDW; ++j) {
+        const int o = o0 + drow[j], px = px0 + dpx[j];
+        const uint32_t off = (o < O && px < HW) ? ((uint32_t)o * (uint32_t)HW + (uint32_t)px) * E : kOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            dres, (__attribute__((address_space(3))) void*)(dst + (wave * NDW + j) * 1024), 16, off, 0,
+            0, 0);
+      }
+    } else {
+      // H*W with rows off 16-byte boundaries: the same chunks element by
+      // element through registers (pixels past the row end read zero)
+#pragma unroll
+      for (int j = 0; j < NDW; ++j) {
+        const int o = o0 + drow[j], px = px0 + dpx[j];
+        constexpr int CPX = 16 / (int)E;
+        uint32_t raw[CPX];
+#pragma unroll
+        for (int e = 0; e < CPX; ++e) {
+          const uint32_t off = (o < O && px + e < HW)
+                                   ? ((uint32_t)o * (uint32_t)HW + (uint32_t)(px + e)) * E
+                                   : kOob;
+          if constexpr (E == 4)
+            raw[e] = __builtin_amdgcn_raw_buffer_load_b32(dres, off, 0, 0);
+          else
+            raw[e] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(dres, off, 0, 0);
+        }
+        u32x4 q;
+        if constexpr (E == 4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) q[e] = raw[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) q[e] = raw[2 * e] | (raw[2 * e + 1] << 16);
+        }
+        *reinterpret_cast<u32x4*>(dst + (wave * NDW + j) * 1024 + lane * 16) = q;
+      }
     }
     // the stage's W^T slice: KCH chunks x MB x P units, contiguous in pk
     const int units = (g.oc - st * L::KCH < L::KCH ? g.oc - st * L::KCH : L::KCH) * MB * P;
@@ -1157,11 +1189,12 @@ extern "C" int ddpm_gen_kernels_bwd_y(const void* weight, const void* grad_kerne
   if (!weight || !grad_kernels || !grad_y) return kBadArgument;
   const int64_t esz = dtype == kF32 ? 4 : 2;
   const int64_t hw = h * w, o = 3 * c * kernel_size * kernel_size;
-  // 16-byte chunks of whole dK rows; 32-bit offsets inside one image's planes
-  if (hw % 8 != 0 || (uintptr_t)grad_kernels % 16 != 0) return kUnsupported;
+  // 32-bit offsets inside one image's planes
   if (o * hw * esz > 0x7fffffffLL || n * ((hw + kGyPX - 1) / kGyPX) > 0x7fffffffLL) return kUnsupported;
   GyGeom g;
   gy_geom(g, n, c, hw, o, esz == 2 ? 2 : 1);
+  // whole 16-byte chunks of every dK row: LDS-direct copies
+  g.dma = (hw * esz) % 16 == 0 && (uintptr_t)grad_kernels % 16 == 0;
   const int parts = esz == 4 ? 2 : 1;
   const int64_t pkb = gy_pack_bytes(g, parts);
   if (!workspace || (uintptr_t)workspace % 16 != 0 ||

@@ -334,8 +334,8 @@ class _GeneratorKernels(torch.autograd.Function):
 
 
 def _generator_kernels_input_grad(w2, g, n, c, h, w, k):
-    """dY = Wᵀ·dK of the generator convolution through ``ddpm_gen_kernels_bwd_y``;
-    shapes it does not cover (H·W not a multiple of 8) use a batched product."""
+    """dY = Wᵀ·dK of the generator convolution through ``ddpm_gen_kernels_bwd_y``
+    (every shape :func:`generator_kernels_supported` accepts)."""
     lib = _lib.load()
     grad_y = torch.empty((n, c, h, w), dtype=g.dtype, device=g.device)
     with torch.cuda.device(g.device):
@@ -343,8 +343,6 @@ def _generator_kernels_input_grad(w2, g, n, c, h, w, k):
         ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=g.device)
         code = lib.ddpm_gen_kernels_bwd_y(_ptr(w2), _ptr(g), _ptr(grad_y), _ptr(ws), ws_bytes, n, c, h,
                                           w, k, _dt(g), _stream(g))
-    if code == _lib.STATUS_UNSUPPORTED:
-        return torch.matmul(w2.t().contiguous(), g).view(n, c, h, w)
     _lib.check(code, "ddpm_gen_kernels_bwd_y")
     return grad_y
 

@@ -89,8 +89,9 @@ int ddpm_gen_kernels_bwd_w(const void* y, const void* grad_kernels, void* grad_w
 /* Input gradient of that convolution: grad_y[n][i][p] =
  * sum_o weight[o][i] * grad_kernels[n][o][p], accumulated in fp32 and rounded
  * once to `dtype` (deterministic: o-split partials summed in split order).
- * weight: [3*c*k*k][c]; grad_kernels: [n][3*c*k*k][h][w], 16-byte aligned;
- * kUnsupported when h*w is not a multiple of 8 or c > 128.  Replaces the
+ * weight: [3*c*k*k][c]; grad_kernels: [n][3*c*k*k][h][w] (rows whose
+ * 16-byte chunks are aligned are copied to LDS directly, others element by
+ * element); kUnsupported when c > 128.  Replaces the
  * backward-data convolution of self.generator on the reference's
  * materialized path (triton_impl.py:340-347, autograd of nn.Conv2d). */
 int64_t ddpm_gen_kernels_bwd_y_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w,

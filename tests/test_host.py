@@ -47,18 +47,17 @@ def test_host_only_queries():
     assert lib.ddpm_gen_supported(64, 3, 9) == 0
     assert lib.ddpm_gen_supported(64, 1, 50) == 1
     # at most 16 splits of 27 (branch, tap) x C x (C + 1) fp32 partials, at least
-    # 4 steps (row segments of 128 columns) each: 16 at 256x256, then for fp32
-    # the bf16 hi / lo planes of y (2 x 2 bytes per element); 2-byte dtypes
-    # need the partials only
-    ysplit = lambda n, c, h, w: n * c * h * w * 4  # noqa: E731
+    # 4 steps (row segments of 128 columns) each: 16 at 256x256; the same
+    # for every dtype (fp32 y is split into bf16 hi / lo while it is staged)
+    ysplit = lambda n, c, h, w: n * c * h * w * 4  # noqa: E731  (generator GEMM's y planes)
     part = 16 * 27 * 64 * 65 * 4
-    assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 64, 256, 256, 3, 0) == part + ysplit(1, 64, 256, 256)
+    assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 64, 256, 256, 3, 0) == part
     assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 64, 256, 256, 3, 1) == part
     assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 64, 256, 256, 3, 7) == 0  # invalid dtype
     # 30 steps at 4 per split: 8 splits
-    assert lib.ddpm_gen_bwd_w_workspace_bytes(2, 24, 15, 17, 3, 0) == 8 * 27 * 24 * 25 * 4 + ysplit(2, 24, 15, 17)
+    assert lib.ddpm_gen_bwd_w_workspace_bytes(2, 24, 15, 17, 3, 0) == 8 * 27 * 24 * 25 * 4
     # 4 steps or fewer: one split writes the gradients directly
-    assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 24, 4, 17, 3, 0) == ysplit(1, 24, 4, 17)
+    assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 24, 4, 17, 3, 0) == 0
     assert lib.ddpm_gen_bwd_w_workspace_bytes(1, 24, 4, 17, 3, 2) == 0
     # dX partials: 16x64 tiles (4 x 16 of them) x 4 channel blocks x 16 channels x
     # the 16+2R rows of the halo tile, R = 5, each padded from 64+2R = 74 columns
