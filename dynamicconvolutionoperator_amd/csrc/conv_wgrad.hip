@@ -8,7 +8,8 @@
 // per tap, the same shape as the fused generator's weight gradient
 // (gen_bwd_w.hip) with the shifted cat rows in place of dK and grad_out in
 // place of y.  Work decomposition (CDNA4):
-//   * one workgroup per (pixel split, 16-plane block of ci): at most 16
+//   * one workgroup per (pixel split, 16-plane block of ci, and above 64
+//     output planes half of the co planes): at most 16
 //     splits of at least 4 steps -- a step is one image-row segment of 128
 //     columns -- (16 splits x 16 blocks = 256 workgroups at C = 64, 256x256);
 //     their fp32 partials are summed in split order by a second kernel
@@ -44,6 +45,7 @@ constexpr int kCwMinSteps = 4;
 struct CwGeom {
   int N, C, CI, H, W;   // C output planes (co), CI = 4C input planes (ci)
   int cblocks;          // ceil(CI / 16)
+  int ohalves;          // 1, or 2 when C > 64: a workgroup covers 64 output planes co
   int col_blocks;       // ceil(W / kCwTW)
   int splits, steps, steps_per_split;
   int direct;
@@ -112,8 +114,11 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
   extern __shared__ __attribute__((aligned(16))) uint32_t csm[];
 
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int split = logical / g.cblocks;
-  const int cb = logical - split * g.cblocks;
+  const int oh = logical % g.ohalves;
+  const int lsc = logical / g.ohalves;
+  const int split = lsc / g.cblocks;
+  const int cb = lsc - split * g.cblocks;
+  const int co0 = oh * MB * 16;  // first output plane of this workgroup
   const int C = g.C, CI = g.CI, H = g.H, W = g.W;
   const int64_t HW = (int64_t)H * W;
   const int tid = threadIdx.x;
@@ -121,8 +126,10 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
   const int lane = tid & 63;
   const int col16 = lane & 15, quad = lane >> 4;
   const int sg = wave % kCwSegs, ki = wave / kCwSegs;  // token segment, kernel row
-  // bias: workgroup cb < ceil(C/16) sums grad_out block cb (kernel-row-0 waves)
-  const bool do_bias = cb < (C + 15) / 16 && ki == 0;
+  // bias: workgroup cb < ceil(C/16) of the half holding grad_out block cb sums
+  // that block (kernel-row-0 waves)
+  const bool bias_wg = cb < (C + 15) / 16 && cb / MB == oh;
+  const bool do_bias = bias_wg && ki == 0;
 
   const int step_beg = split * g.steps_per_split;
   int step_end = step_beg + g.steps_per_split;
@@ -145,7 +152,7 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
       const int row = ii * YRPC + lane / L::kYC, pos = lane % L::kYC;
       const int part = row / (MB * 16), i = row - part * (MB * 16);
       cpc[j] = (pos ^ (i & 15)) * 8;
-      if (i < C) cpo[j] = ((uint32_t)(part * C + i) * (uint32_t)HW + (uint32_t)cpc[j]) * 2u;
+      if (co0 + i < C) cpo[j] = ((uint32_t)(part * C + co0 + i) * (uint32_t)HW + (uint32_t)cpc[j]) * 2u;
     }
   }
 
@@ -209,8 +216,9 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
         const int part = row / (MB * 16), i = row - part * (MB * 16);
         const int w = p.w0 + j;
         const uint32_t off =
-            (i < C && w < W) ? ((uint32_t)(part * C + i) * (uint32_t)HW + rowel + (uint32_t)w) * 2u
-                             : kOob;
+            (co0 + i < C && w < W)
+                ? ((uint32_t)(part * C + co0 + i) * (uint32_t)HW + rowel + (uint32_t)w) * 2u
+                : kOob;
         const int kc = (j >> 3) ^ (i & 15);
         dy[row * L::kYD * 2 + kc * 8 + (j & 7)] =
             (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(yres, off, 0, 0);
@@ -248,7 +256,7 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
   int xel[3];
 #pragma unroll
   for (int kj = 0; kj < 3; ++kj) xel[kj] = (ki * 16 + col16) * L::kXSD * L::kPerD + kCwPad + wl + kj - 1;
-  const int bib = cb;  // the gO block this workgroup sums for the bias
+  const int bib = cb - oh * MB;  // the staged gO block this workgroup sums for the bias
   for (int s = 0; s < steps; ++s) {
     const int buf = s & 1;
     if (s + 1 < steps) {
@@ -324,7 +332,7 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
     const int rem2 = q - t * 16 * NO;
     const int c = rem2 / NO, i = rem2 - c * NO;
     const int ci = cb * 16 + c;
-    if (ci >= CI || i >= C) continue;
+    if (ci >= CI || co0 + i >= C) continue;
     const float* __restrict__ sp = red + (t * 16 + c) * RS + i;
     float v[4];
 #pragma unroll
@@ -332,19 +340,19 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
     if (g.direct) {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (i + e < C) dw_out[((int64_t)(i + e) * CI + ci) * 9 + t] = from_f<T>(v[e]);
+        if (co0 + i + e < C) dw_out[((int64_t)(co0 + i + e) * CI + ci) * 9 + t] = from_f<T>(v[e]);
     } else {
-      float* __restrict__ dst = pwb + ((int64_t)t * CI + ci) * C + i;
+      float* __restrict__ dst = pwb + ((int64_t)t * CI + ci) * C + co0 + i;
       if (v4) {
         *reinterpret_cast<f32x4*>(dst) = (f32x4){v[0], v[1], v[2], v[3]};
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (i + e < C) dst[e] = v[e];
+          if (co0 + i + e < C) dst[e] = v[e];
       }
     }
   }
-  if (cb < (C + 15) / 16 && tid < 16) {
+  if (bias_wg && tid < 16) {
     const int co = cb * 16 + tid;
     if (co < C) {
       const float v = ((rb[tid] + rb[16 + tid]) + rb[32 + tid]) + rb[48 + tid];
@@ -431,6 +439,7 @@ void cw_geom(CwGeom& g, int64_t n, int64_t c, int64_t h, int64_t w) {
   g.H = (int)h;
   g.W = (int)w;
   g.cblocks = (int)((4 * c + 15) / 16);
+  g.ohalves = c > 64 ? 2 : 1;
   g.col_blocks = (int)((w + kCwTW - 1) / kCwTW);
   const int64_t steps = n * h * g.col_blocks;
   int64_t splits = kCwMaxSplits;
@@ -473,7 +482,7 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
                                          hipStream_t stream) {
   if (dtype < kF32 || dtype > kF16) return kBadArgument;
   if (n < 0 || c < 0 || h < 0 || w < 0) return kBadArgument;
-  if (c > 64) return kUnsupported;  // grad_out rows of all output planes are staged together
+  if (c > 128) return kUnsupported;  // a workgroup stages the grad_out rows of 64 output planes
   if (c == 0) return kOk;
   if (!grad_weight || !grad_bias) return kBadArgument;
   const int esz = dtype == kF32 ? 4 : 2;
@@ -508,7 +517,7 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
     const int e = launch_ysplit((const float*)grad_out, gs, c * h * w, n * c * h * w, stream);
     if (e != 0) return e;
   }
-  const int mb = (int)((c + 15) / 16);
+  const int mb = c > 64 ? 4 : (int)((c + 15) / 16);  // 16-plane blocks of co per workgroup
   return cw_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
     return cw_with_mb(mb, [&](auto mbc) {
@@ -520,7 +529,7 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
       auto kern = conv_wgrad_partial_kernel<T, MB>;
       const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
       if (ae != 0) return ae;
-      hipLaunchKernelGGL(kern, dim3((unsigned)(g.splits * g.cblocks)), dim3(kCwThreads), lds, stream,
+      hipLaunchKernelGGL(kern, dim3((unsigned)(g.splits * g.cblocks * g.ohalves)), dim3(kCwThreads), lds, stream,
                          (const T*)cat, gsrc, pw, pb, (T*)grad_weight, (T*)grad_bias, g);
       int e = (int)hipGetLastError();
       if (e != 0 || g.direct) return e;

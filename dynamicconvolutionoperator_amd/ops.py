@@ -414,7 +414,7 @@ class _FuseConv3x3(torch.autograd.Function):
     convolution as HIP MFMA kernels: forward and input gradient
     (``ddpm_fuse_conv_fwd`` / ``_bwd_data``, implicit GEMMs over the input
     planes), weight and bias gradients (``ddpm_fuse_conv_bwd_weight``, a
-    split pixel reduction; more than 64 output channels use the library's
+    split pixel reduction; more than 128 output channels use the library's
     backward-filter convolution)."""
 
     @staticmethod

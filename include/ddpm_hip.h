@@ -233,7 +233,8 @@ int64_t ddpm_fuse_conv_bwd_weight_workspace_bytes(int64_t n, int64_t c, int64_t 
  *                               cat[n][ci][h+ki-1][w+kj-1]  (zero padding),
  * grad_bias[co] = sum grad_out[n][co][h][w]; fp32 accumulation in at most 16
  * pixel splits summed in split order (deterministic), rounded once to
- * `dtype`; an empty batch writes zeros.  c <= 64 (kUnsupported beyond).
+ * `dtype`; an empty batch writes zeros.  c <= 128 (kUnsupported beyond; above
+ * 64 output planes workgroups take halves of 64).
  * Replaces the cuDNN backward-filter convolution of self.fuse (autograd of
  * nn.Conv2d, triton_impl.py:294, 392). */
 int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, void* grad_weight,

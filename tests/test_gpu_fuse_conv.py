@@ -57,6 +57,16 @@ def test_fuse_conv_full_size(dtype, hw):
     _check((1, 64, hw, hw), dtype, 910)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("c", [72, 96, 128])
+def test_fuse_conv_wide_channels(c, dtype):
+    """65..128 output planes: the weight gradient runs in two halves of 64
+    output planes (72: a half with 8 valid planes and the bias blocks split
+    4 + 1 over the halves), the forward and input gradient in m groups."""
+    say(f"fuse conv C={c} dtype={dtype}")
+    _check((1, c, 24, 40), dtype, 940 + c)
+
+
 def test_fuse_conv_without_bias_and_fallback():
     cat = randn((1, 32, 9, 16), 920).to(DEV)
     wt = randn((8, 32, 3, 3), 921, scale=0.1).to(DEV)
