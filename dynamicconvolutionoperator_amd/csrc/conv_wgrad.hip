@@ -16,10 +16,13 @@
 //     (deterministic, no atomics); a single split writes the gradients
 //     directly;
 //   * per step the 3 cat rows {h-1, h, h+1} of the 16 planes (128 + 16
-//     columns) and the grad_out rows of all C planes (fp32: pre-split into
-//     bf16 hi / lo planes by gen_ysplit_kernel) are copied global -> LDS by
-//     16-byte buffer loads that write LDS directly (zero outside the image),
-//     one step ahead into a second buffer;
+//     columns) and the grad_out rows of the workgroup's (up to 64) output
+//     planes are staged in LDS one step ahead, into a second buffer: cat and
+//     2-byte grad_out rows by 16-byte buffer loads that write LDS directly
+//     (zero outside the image); fp32 grad_out rows through registers, split
+//     into bf16 hi / lo rows on the way (each thread loads its 4-column pieces
+//     of the next step's rows before the step's MFMAs and writes their split
+//     after them: no pre-pass over grad_out);
 //   * 12 waves = 4 token segments x 3 kernel rows (three waves per SIMD); a
 //     wave accumulates its row's 3 taps x 16 ci x C co on
 //     v_mfma_f32_16x16x32_{bf16,f16} (fp32 operands as three bf16 products);
@@ -50,14 +53,15 @@ struct CwGeom {
   int splits, steps, steps_per_split;
   int direct;
   int x16;              // cat rows hold whole 16-byte chunks: one 16-byte copy per row
-  int g16;              // grad_out (planes) rows 16-byte aligned with W % 8 == 0: 16-byte copies
+  int g16;              // 2-byte grad_out rows 16-byte aligned (W % 8 == 0): 16-byte copies
+  int y4;               // fp32 grad_out rows 16-byte aligned (W % 4 == 0): 16-byte register loads
 };
 
 // One LDS staging buffer (dwords):
 //   cat rows [3*16][kXSD]   T elements; odd pitch (the 64 lanes' reads of one
 //                           element fall at most two to a bank)
 //   gO rows  [P][MB*16][kYD] 2-byte elements (grad_out, or the bf16 hi / lo
-//                           planes of an fp32 grad_out): 16 chunks of 16
+//                           rows of an fp32 grad_out): 16 chunks of 16
 //                           bytes, chunk k of row i at position k ^ (i & 15)
 template <typename T, int MB>
 struct CwLds {
@@ -100,10 +104,9 @@ struct CwPos {
   }
 };
 
-// gb: grad_out itself (2-byte types) or its bf16 hi / lo planes [n][2][C][H*W] (fp32).
 template <typename T, int MB>
 __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
-    const T* __restrict__ cat, const uint16_t* __restrict__ gb, float* __restrict__ pw,
+    const T* __restrict__ cat, const T* __restrict__ gout, float* __restrict__ pw,
     float* __restrict__ pb, T* __restrict__ dw_out, T* __restrict__ db_out, CwGeom g) {
   typedef Mma<T> M;
   typedef typename M::V V;
@@ -111,6 +114,9 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
   typedef CwLds<T, MB> L;
   constexpr int P = M::P;
   constexpr int E = (int)sizeof(T);
+  // fp32: grad_out goes through registers and is split into bf16 hi / lo rows
+  // on the way to LDS; 2-byte types copy it global -> LDS directly
+  constexpr bool kYReg = E == 4;
   extern __shared__ __attribute__((aligned(16))) uint32_t csm[];
 
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
@@ -139,8 +145,8 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
   // gO copies (16-byte lanes): the lane's byte offset within one image's
   // planes at row 0, column 0 (kOob for planes >= C) and its chunk's column
   constexpr int YRPC = 64 / L::kYC;  // gO rows per 1 KB copy
-  constexpr int NY = L::kYRows / YRPC;
-  constexpr int NJ = (NY + kCwNW - 1) / kCwNW;
+  constexpr int NY = kYReg ? 0 : L::kYRows / YRPC;
+  constexpr int NJ = NY > 0 ? (NY + kCwNW - 1) / kCwNW : 1;  // (no copies when NY = 0)
   uint32_t cpo[NJ];
   int cpc[NJ];
 #pragma unroll
@@ -193,7 +199,7 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
       }
     }
     // gO rows (P parts x MB*16 planes) in the swizzled chunk layout; planes >= C read zero
-    const BufRes yres = make_buf(gb + (int64_t)p.n * P * C * HW, (uint32_t)(P * C * HW * 2));
+    const BufRes yres = make_buf(gout + (int64_t)p.n * C * HW, (uint32_t)(C * HW * E));
     const uint32_t rowel = (uint32_t)(p.h * W);
     if (g.g16) {
       const uint32_t ystep = (rowel + (uint32_t)p.w0) * 2u;
@@ -201,7 +207,7 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int ii = wave + kCwNW * j;
-        if (NY % kCwNW != 0 && ii >= NY) break;
+        if ((NY == 0 || NY % kCwNW != 0) && ii >= NY) break;
         uint32_t vo = cpo[j];
         if (!full) vo = p.w0 + cpc[j] < W ? vo : kOob;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -210,18 +216,67 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
       }
     } else {
       uint16_t* __restrict__ dy = reinterpret_cast<uint16_t*>(dstb + L::kYOff);
-      constexpr int PY = L::kYRows * kCwTW;
+      constexpr int PY = kYReg ? 0 : L::kYRows * kCwTW;
       for (int idx = tid; idx < PY; idx += kCwThreads) {
         const int row = idx / kCwTW, j = idx - row * kCwTW;
-        const int part = row / (MB * 16), i = row - part * (MB * 16);
+        const int i = row;
         const int w = p.w0 + j;
         const uint32_t off =
-            (co0 + i < C && w < W)
-                ? ((uint32_t)(part * C + co0 + i) * (uint32_t)HW + rowel + (uint32_t)w) * 2u
-                : kOob;
+            (co0 + i < C && w < W) ? ((uint32_t)(co0 + i) * (uint32_t)HW + rowel + (uint32_t)w) * 2u
+                                   : kOob;
         const int kc = (j >> 3) ^ (i & 15);
         dy[row * L::kYD * 2 + kc * 8 + (j & 7)] =
             (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(yres, off, 0, 0);
+      }
+    }
+  };
+
+  // ---- fp32 grad_out rows of step `p`: thread tid loads the 4-column pieces
+  //      u = tid + NT*j (row u / 32, columns 4*(u % 32) .. +3) into registers
+  //      (yload, before a step's MFMAs) and writes their bf16 hi / lo split to
+  //      the gO rows of LDS buffer `buf` (ystore, after them), as the two
+  //      8-byte halves of the row's chunk (u % 32) / 2 in the swizzled layout.
+  //      Columns past the image and planes >= C read zero.
+  constexpr int YU = kYReg ? MB * 16 * (kCwTW / 4) : 1;
+  constexpr int YUT = (YU + kCwThreads - 1) / kCwThreads;
+  f32x4 yreg[YUT];
+  auto yload = [&](const CwPos& p) {
+    if constexpr (kYReg) {
+      const BufRes yres = make_buf(gout + (int64_t)p.n * C * HW, (uint32_t)(C * HW * E));
+      const uint32_t rowel = (uint32_t)(p.h * W);
+#pragma unroll
+      for (int j = 0; j < YUT; ++j) {
+        const int u = tid + kCwThreads * j;
+        if (YU % kCwThreads != 0 && u >= YU) break;  // wave-uniform
+        const int i = u >> 5, w = p.w0 + 4 * (u & 31);
+        const bool okc = co0 + i < C;
+        const uint32_t base = ((uint32_t)(co0 + i) * (uint32_t)HW + rowel + (uint32_t)w) * 4u;
+        if (g.y4) {
+          yreg[j] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(yres, okc && w < W ? base : kOob, 0, 0));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            yreg[j][e] = buf_load1<float>(yres, okc && w + e < W ? base + 4u * e : kOob);
+        }
+      }
+    }
+  };
+  auto ystore = [&](int buf) {
+    if constexpr (kYReg) {
+      uint32_t* __restrict__ yl = csm + buf * L::kBuf + L::kYOff;
+#pragma unroll
+      for (int j = 0; j < YUT; ++j) {
+        const int u = tid + kCwThreads * j;
+        if (YU % kCwThreads != 0 && u >= YU) break;
+        const int i = u >> 5, q = u & 31;
+        const int dw = i * L::kYD + 4 * ((q >> 1) ^ (i & 15)) + 2 * (q & 1);
+        uint32_t h0, l0, h1, l1;
+        split_bf16x2(yreg[j][0], yreg[j][1], h0, l0);
+        split_bf16x2(yreg[j][2], yreg[j][3], h1, l1);
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<u32x2*>(yl + dw) = (u32x2){h0, h1};
+        *reinterpret_cast<u32x2*>(yl + MB * 16 * L::kYD + dw) = (u32x2){l0, l1};
       }
     }
   };
@@ -245,8 +300,10 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
     nxt.h = row - nxt.n * H;
   }
   if (steps > 0) {
+    yload(nxt);
     stage(nxt, 0);
     nxt.advance(g);
+    ystore(0);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -259,7 +316,9 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
   const int bib = cb - oh * MB;  // the staged gO block this workgroup sums for the bias
   for (int s = 0; s < steps; ++s) {
     const int buf = s & 1;
-    if (s + 1 < steps) {
+    const bool more = s + 1 < steps;
+    if (more) {
+      yload(nxt);
       stage(nxt, buf ^ 1);
       nxt.advance(g);
     }
@@ -299,6 +358,7 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
 #pragma unroll
       for (int ib = 0; ib < MB; ++ib) acc[kj][ib] = M::mac(afr, bfr[ib], acc[kj][ib]);
     }
+    if (more) ystore(buf ^ 1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
@@ -451,9 +511,8 @@ void cw_geom(CwGeom& g, int64_t n, int64_t c, int64_t h, int64_t w) {
   g.direct = g.splits == 1;
   g.x16 = 0;
   g.g16 = 0;
+  g.y4 = 0;
 }
-
-int64_t cw_align(int64_t v) { return (v + 255) / 256 * 256; }
 
 int64_t cw_partial_bytes(const CwGeom& g) {
   if (g.direct) return 0;
@@ -471,9 +530,7 @@ extern "C" int64_t ddpm_fuse_conv_bwd_weight_workspace_bytes(int64_t n, int64_t 
   if (n * h * ((w + kCwTW - 1) / kCwTW) > 0x7fffffffLL) return 0;
   CwGeom g;
   cw_geom(g, n, c, h, w);
-  const int64_t pbytes = cw_partial_bytes(g);
-  // fp32: the bf16 hi / lo planes of grad_out follow the partials
-  return dtype == kF32 ? cw_align(pbytes) + n * 2 * c * h * w * 2 : pbytes;
+  return cw_partial_bytes(g);
 }
 
 extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, void* grad_weight,
@@ -500,23 +557,17 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
   }
   if (!cat || !grad_out) return kBadArgument;
   if (n * h * ((w + kCwTW - 1) / kCwTW) > 0x7fffffffLL) return kUnsupported;
-  // 32-bit buffer offsets inside one image's planes (fp32 grad_out: two 2-byte planes)
-  if (4 * c * h * w * esz > 0x7fffffffLL || 2 * c * h * w * 2 > 0x7fffffffLL) return kUnsupported;
+  // 32-bit buffer offsets inside one image's planes
+  if (4 * c * h * w * esz > 0x7fffffffLL) return kUnsupported;
   CwGeom g;
   cw_geom(g, n, c, h, w);
-  const int64_t pbytes = cw_partial_bytes(g);
-  const int64_t need = dtype == kF32 ? cw_align(pbytes) + n * 2 * c * h * w * 2 : pbytes;
+  const int64_t need = cw_partial_bytes(g);
   if (need > 0 && (!workspace || workspace_bytes < need)) return kWorkspaceTooSmall;
-  uint16_t* gs = dtype == kF32 ? (uint16_t*)((char*)workspace + cw_align(pbytes)) : nullptr;
-  const uint16_t* gsrc = dtype == kF32 ? gs : (const uint16_t*)grad_out;
   g.x16 = (w % (16 / esz) == 0) && ((uintptr_t)cat % 16 == 0);
-  g.g16 = (w % 8 == 0) && ((uintptr_t)gsrc % 16 == 0);
+  g.g16 = (w % 8 == 0) && ((uintptr_t)grad_out % 16 == 0);
+  g.y4 = (w % 4 == 0) && ((uintptr_t)grad_out % 16 == 0);
   float* pw = g.direct ? nullptr : (float*)workspace;
   float* pb = g.direct ? nullptr : pw + (int64_t)g.splits * 9 * 4 * c * c;
-  if (dtype == kF32) {
-    const int e = launch_ysplit((const float*)grad_out, gs, c * h * w, n * c * h * w, stream);
-    if (e != 0) return e;
-  }
   const int mb = c > 64 ? 4 : (int)((c + 15) / 16);  // 16-plane blocks of co per workgroup
   return cw_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
@@ -530,7 +581,7 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
       const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
       if (ae != 0) return ae;
       hipLaunchKernelGGL(kern, dim3((unsigned)(g.splits * g.cblocks * g.ohalves)), dim3(kCwThreads), lds, stream,
-                         (const T*)cat, gsrc, pw, pb, (T*)grad_weight, (T*)grad_bias, g);
+                         (const T*)cat, (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g);
       int e = (int)hipGetLastError();
       if (e != 0 || g.direct) return e;
       const int64_t items = (int64_t)9 * 4 * c * c + c;

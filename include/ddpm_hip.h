@@ -224,8 +224,8 @@ int ddpm_fuse_conv_bwd_data(const void* grad_out, const void* weight, void* grad
                             int64_t h, int64_t w, int dtype, hipStream_t stream);
 
 /* Bytes of workspace ddpm_fuse_conv_bwd_weight needs for `dtype`: fp32
- * split partials of the weight and bias gradients (none with one split),
- * then for fp32 the bf16 hi / lo planes of grad_out. */
+ * split partials of the weight and bias gradients (none with one split; the
+ * same for every dtype). */
 int64_t ddpm_fuse_conv_bwd_weight_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w,
                                                   int dtype);
 
