@@ -58,13 +58,14 @@ def test_fuse_conv_full_size(dtype, hw):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("c", [72, 96, 128])
-def test_fuse_conv_wide_channels(c, dtype):
+@pytest.mark.parametrize("shape", [(1, 72, 24, 40), (1, 96, 24, 40), (1, 128, 24, 40), (1, 96, 11, 19)])
+def test_fuse_conv_wide_channels(shape, dtype):
     """65..128 output planes: the weight gradient runs in two halves of 64
     output planes (72: a half with 8 valid planes and the bias blocks split
-    4 + 1 over the halves), the forward and input gradient in m groups."""
-    say(f"fuse conv C={c} dtype={dtype}")
-    _check((1, c, 24, 40), dtype, 940 + c)
+    4 + 1 over the halves), the forward and input gradient in m groups;
+    W = 19 stages the concat and grad_out rows element by element."""
+    say(f"fuse conv shape={shape} dtype={dtype}")
+    _check(shape, dtype, 940 + shape[1] + shape[3])
 
 
 def test_fuse_conv_without_bias_and_fallback():
