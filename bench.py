@@ -25,7 +25,10 @@ Also reported on the same line (``extra``):
     and bf16, C = 128 fp32), each route in its own child process started
     before this process uses the GPU, with gradients released before the
     baseline is read (gpu_memory_bench.py:47-76);
-  * the Unfold route's GPU step time.
+  * the Unfold route's GPU training-step and inference times (256x256 fp32
+    and bf16, 128x128 fp32, K=5 128x128 bf16) and the fused path's speedups
+    over it, beside the ratios the reference publishes for its Triton path
+    on an RTX 5090 (README.md:139-145).
 ``cpu_baseline``: the reference's CPU path, timed on this host's cores in
 the same run -- the CPU branch of the drop-in module (streaming with
 per-tile checkpoint at fp32, triton_impl.py:169-244,381-391; Unfold training
@@ -273,7 +276,7 @@ def filter_op_bandwidth(op, dtype, h=H, w=W, k=K, sets=2, repeats=30):
             "frac_of_8TBps": nbytes / ms / 1e6 / HBM_PEAK_GBS}
 
 
-def unfold_route_step(params, x, y):
+def unfold_route_step(params, x, y, k=K):
     """The reference's Unfold route (unfold_impl.py:21-42) with the module's
     parameters, used here only as the GPU memory/time baseline."""
     import torch
@@ -281,10 +284,10 @@ def unfold_route_step(params, x, y):
 
     gw, gb, fw, fb = params
     n, c, h, w = x.shape
-    kernels = F.conv2d(y, gw, gb).reshape(n, 3, c, K * K, h, w)
+    kernels = F.conv2d(y, gw, gb).reshape(n, 3, c, k * k, h, w)
     outs = [x]
     for b, d in enumerate(DIL):
-        cols = F.unfold(x, K, dilation=d, padding=K // 2 * d).reshape(n, c, K * K, h, w)
+        cols = F.unfold(x, k, dilation=d, padding=k // 2 * d).reshape(n, c, k * k, h, w)
         outs.append((cols * kernels[:, b]).sum(2))
     return F.conv2d(torch.cat(outs, 1), fw, fb, padding=1)
 
@@ -679,8 +682,39 @@ def main():
                 unfold_route_step(params, x, y).square().mean().backward()
 
             extra[f"unfold_route_train_ms_{name}"] = time_loop(unfold_step, 10, 3)
+            with torch.inference_mode():
+                extra[f"unfold_route_infer_ms_{name}"] = time_loop(
+                    lambda: unfold_route_step(params, x, y), 10, 3)
             del module, x, y, params
             torch.cuda.empty_cache()
+        # the Unfold route's inference at the 128x128 shapes (K=3 fp32, K=5 bf16)
+        for key, k, dtype in (("unfold_route_infer_ms_128_fp32", 3, torch.float32),
+                              ("unfold_route_infer_ms_k5_128_bf16", 5, torch.bfloat16)):
+            from dynamicconvolutionoperator_amd import DDPM
+
+            torch.manual_seed(21)
+            params = [p.detach() for p in DDPM(C, k).cuda().to(dtype).parameters()]
+            torch.manual_seed(20)
+            x = torch.randn(1, C, 128, 128, device="cuda", dtype=dtype)
+            y = torch.randn_like(x)
+            with torch.inference_mode():
+                extra[key] = time_loop(lambda: unfold_route_step(params, x, y, k), 10, 3)
+            del params, x, y
+            torch.cuda.empty_cache()
+        # speedups over the Unfold route on the same GPU, beside the ratios the
+        # reference publishes for its own Triton path on an RTX 5090
+        # (README.md:139-145, plot_performance.py)
+        extra["speedup_vs_unfold"] = {
+            "infer_256_fp32": extra["unfold_route_infer_ms_fp32"] / extra["infer_ms_fp32"],
+            "infer_256_bf16": extra["unfold_route_infer_ms_bf16"] / extra["infer_ms_bf16"],
+            "infer_128_fp32": extra["unfold_route_infer_ms_128_fp32"] / extra["c2_infer_128_fp32"]["fused_infer_ms"],
+            "infer_k5_128_bf16": extra["unfold_route_infer_ms_k5_128_bf16"] / extra["c4_k5_128_bf16"]["infer_ms"],
+            "train_256_fp32": extra["unfold_route_train_ms_fp32"] / train_ms,
+            "train_256_bf16": extra["unfold_route_train_ms_bf16"] / extra["train_ms_bf16"],
+            "reference_rtx5090": {"infer_256_fp32": 3.73, "infer_256_bf16": 5.23,
+                                  "infer_128_fp32": 2.78, "infer_k5_128_bf16": 4.42,
+                                  "train_256_fp32": 2.16, "train_256_bf16": 2.78},
+        }
 
     cpu = None
     if not args.no_cpu_baseline:

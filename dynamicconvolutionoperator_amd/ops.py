@@ -19,7 +19,9 @@ kernels run asynchronously on the current stream.  Tensors must be on a ROCm
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
+import functools
 
 import torch
 
@@ -39,8 +41,40 @@ def _ptr(t: torch.Tensor) -> ctypes.c_void_p:
     return ctypes.c_void_p(t.data_ptr())
 
 
+# The current device and the raw handle of its current stream straight from
+# torch's C layer: torch.cuda.current_stream() builds a Stream object per
+# call (about 10 us of host time inside a backward, several calls per step).
+_current_device = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None) or (
+    lambda idx: torch.cuda.current_stream(idx).cuda_stream)
+
+
 def _stream(t: torch.Tensor) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    """The current stream of t's device, as the C-ABI's hipStream_t."""
+    idx = t.device.index
+    return ctypes.c_void_p(_raw_stream(_current_device() if idx is None else idx))
+
+
+def _on(device: torch.device):
+    """Device guard for a launch: a no-op when `device` is already current
+    (the usual case)."""
+    if device.index is None or device.index == _current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
+
+
+@functools.lru_cache(maxsize=512)
+def _ws_bytes(query: str, *args) -> int:
+    """Workspace bytes from a C-ABI ``*_workspace_bytes`` query (a pure
+    function of its arguments, so each shape is asked once)."""
+    return int(getattr(_lib.load(), query)(*args))
+
+
+def _as(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """t in `dtype`, contiguous (no torch call when it already is)."""
+    if t.dtype != dtype:
+        t = t.to(dtype)
+    return t if t.is_contiguous() else t.contiguous()
 
 
 def _require_device(*tensors: torch.Tensor) -> None:
@@ -85,7 +119,7 @@ def _check_filter_inputs(x: torch.Tensor, kernels: torch.Tensor, k: int) -> None
 def _filter_call(fn_name: str, a, b, out, x_shape, k, dil, x_dtype: int, k_dtype: int):
     lib = _lib.load()
     n, c, h, w = x_shape
-    with torch.cuda.device(out.device):
+    with _on(out.device):
         code = getattr(lib, fn_name)(
             _ptr(a), _ptr(b), _ptr(out), n, c, h, w, k, dil[0], dil[1], dil[2], x_dtype, k_dtype,
             _stream(out),
@@ -112,7 +146,7 @@ class _DynamicCat(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         x, kernels = ctx.saved_tensors
-        grad_out = grad_out.to(kernels.dtype).contiguous()
+        grad_out = _as(grad_out, kernels.dtype)
         grad_x = grad_k = None
         if ctx.needs_input_grad[0]:
             grad_x = torch.empty_like(x)
@@ -146,7 +180,7 @@ def generator_supported(channels: int, kernel_size: int, dilations=(1, 3, 5), sh
     if not _lib.load().ddpm_gen_supported(int(channels), int(kernel_size), int(max(dilations))):
         return False
     if shape is not None:
-        esize = torch.empty((), dtype=dtype if dtype is not None else torch.float32).element_size()
+        esize = (dtype if dtype is not None else torch.float32).itemsize
         if int(shape[1]) * int(shape[2]) * int(shape[3]) * esize > _FUSED_MAX_IMAGE_BYTES:
             return False
     return True
@@ -176,7 +210,7 @@ def _launch_generator_dynamic_cat(x, y, weight, bias, k, dil):
     n, c, h, w = x.shape
     out = torch.empty((n, 4 * c, h, w), dtype=x.dtype, device=x.device)
     lib = _lib.load()
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         code = lib.ddpm_gen_fwd(
             _ptr(x), _ptr(y), _ptr(weight), _ptr(bias), _ptr(out), n, c, h, w, k, *dil, _dt(x),
             _stream(x),
@@ -203,17 +237,17 @@ class _GeneratorDynamicCat(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         x, y, weight, bias = ctx.saved_tensors
-        grad_out = grad_out.to(x.dtype).contiguous()
+        grad_out = _as(grad_out, x.dtype)
         k, dil = ctx.kernel_size, ctx.dilations
         n, c, h, w = x.shape
         lib = _lib.load()
         dt = _dt(x)
         stream = _stream(x)
         grad_x = grad_y = grad_w = grad_b = None
-        with torch.cuda.device(x.device):
+        with _on(x.device):
             if ctx.needs_input_grad[0]:
                 grad_x = torch.empty_like(x)
-                wsx_bytes = int(lib.ddpm_gen_bwd_x_workspace_bytes(n, c, h, w, k, *dil))
+                wsx_bytes = _ws_bytes("ddpm_gen_bwd_x_workspace_bytes", n, c, h, w, k, *dil)
                 wsx = torch.empty(wsx_bytes, dtype=torch.uint8, device=x.device)
                 _lib.check(
                     lib.ddpm_gen_bwd_x(_ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
@@ -224,7 +258,7 @@ class _GeneratorDynamicCat(torch.autograd.Function):
                 del wsx
             if ctx.needs_input_grad[1]:
                 grad_y = torch.empty_like(y)
-                wsy_bytes = int(lib.ddpm_gen_bwd_y_workspace_bytes(c, k))
+                wsy_bytes = _ws_bytes("ddpm_gen_bwd_y_workspace_bytes", c, k)
                 wsy = torch.empty(wsy_bytes, dtype=torch.uint8, device=x.device)
                 _lib.check(
                     lib.ddpm_gen_bwd_y(_ptr(x), _ptr(weight), _ptr(grad_out), _ptr(grad_y),
@@ -234,7 +268,7 @@ class _GeneratorDynamicCat(torch.autograd.Function):
             if ctx.needs_input_grad[2] or ctx.needs_input_grad[3]:
                 grad_w = torch.empty_like(weight)
                 grad_b = torch.empty_like(bias)
-                ws_bytes = int(lib.ddpm_gen_bwd_w_workspace_bytes(n, c, h, w, k, dt))
+                ws_bytes = _ws_bytes("ddpm_gen_bwd_w_workspace_bytes", n, c, h, w, k, dt)
                 ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
                 _lib.check(
                     lib.ddpm_gen_bwd_w(_ptr(x), _ptr(y), _ptr(grad_out), _ptr(grad_w),
@@ -297,7 +331,7 @@ class _GeneratorKernels(torch.autograd.Function):
         b = bias.contiguous()
         out = torch.empty((n, o, h, w), dtype=y.dtype, device=y.device)
         lib = _lib.load()
-        with torch.cuda.device(y.device):
+        with _on(y.device):
             code = lib.ddpm_gen_kernels(_ptr(y), _ptr(w2), _ptr(b), _ptr(out), n, c, h, w, k, _dt(y),
                                         _stream(y))
         _lib.check(code, "ddpm_gen_kernels")
@@ -320,8 +354,8 @@ class _GeneratorKernels(torch.autograd.Function):
             lib = _lib.load()
             gw = torch.empty((o, c), dtype=y.dtype, device=y.device)
             gb = torch.empty((o,), dtype=y.dtype, device=y.device)
-            with torch.cuda.device(y.device):
-                ws_bytes = int(lib.ddpm_gen_kernels_bwd_w_workspace_bytes(n, c, h, w, k))
+            with _on(y.device):
+                ws_bytes = _ws_bytes("ddpm_gen_kernels_bwd_w_workspace_bytes", n, c, h, w, k)
                 ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=y.device)
                 code = lib.ddpm_gen_kernels_bwd_w(_ptr(y), _ptr(g), _ptr(gw), _ptr(gb), _ptr(ws),
                                                   ws_bytes, n, c, h, w, k, _dt(y), _stream(y))
@@ -338,8 +372,8 @@ def _generator_kernels_input_grad(w2, g, n, c, h, w, k):
     (every shape :func:`generator_kernels_supported` accepts)."""
     lib = _lib.load()
     grad_y = torch.empty((n, c, h, w), dtype=g.dtype, device=g.device)
-    with torch.cuda.device(g.device):
-        ws_bytes = int(lib.ddpm_gen_kernels_bwd_y_workspace_bytes(n, c, h, w, k))
+    with _on(g.device):
+        ws_bytes = _ws_bytes("ddpm_gen_kernels_bwd_y_workspace_bytes", n, c, h, w, k)
         ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=g.device)
         code = lib.ddpm_gen_kernels_bwd_y(_ptr(w2), _ptr(g), _ptr(grad_y), _ptr(ws), ws_bytes, n, c, h,
                                           w, k, _dt(g), _stream(g))
@@ -405,7 +439,7 @@ def fuse_conv_supported(cat, weight, bias) -> bool:
 
 
 def _fuse_conv_workspace(c, dt, device):
-    nbytes = int(_lib.load().ddpm_fuse_conv_workspace_bytes(c, dt))
+    nbytes = _ws_bytes("ddpm_fuse_conv_workspace_bytes", c, dt)
     return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device), nbytes
 
 
@@ -426,7 +460,7 @@ class _FuseConv3x3(torch.autograd.Function):
         out = torch.empty((n, c, h, w), dtype=cat.dtype, device=cat.device)
         dt = _dt(cat)
         lib = _lib.load()
-        with torch.cuda.device(cat.device):
+        with _on(cat.device):
             ws, nbytes = _fuse_conv_workspace(c, dt, cat.device)
             code = lib.ddpm_fuse_conv_fwd(_ptr(cat), _ptr(weight),
                                           _ptr(bias.contiguous()) if bias is not None else None,
@@ -439,7 +473,7 @@ class _FuseConv3x3(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         cat, weight = ctx.saved_tensors
-        grad_out = grad_out.to(cat.dtype).contiguous()
+        grad_out = _as(grad_out, cat.dtype)
         n, ci, h, w = cat.shape
         c = weight.shape[0]
         grad_cat = grad_w = grad_b = None
@@ -447,7 +481,7 @@ class _FuseConv3x3(torch.autograd.Function):
             grad_cat = torch.empty_like(cat)
             dt = _dt(cat)
             lib = _lib.load()
-            with torch.cuda.device(cat.device):
+            with _on(cat.device):
                 ws, nbytes = _fuse_conv_workspace(c, dt, cat.device)
                 code = lib.ddpm_fuse_conv_bwd_data(_ptr(grad_out), _ptr(weight), _ptr(grad_cat),
                                                    _ptr(ws), nbytes, n, c, h, w, dt, _stream(cat))
@@ -459,8 +493,8 @@ class _FuseConv3x3(torch.autograd.Function):
             lib = _lib.load()
             gw = torch.empty_like(weight)
             gb = torch.empty((c,), dtype=cat.dtype, device=cat.device)
-            with torch.cuda.device(cat.device):
-                nbytes = int(lib.ddpm_fuse_conv_bwd_weight_workspace_bytes(n, c, h, w, dt))
+            with _on(cat.device):
+                nbytes = _ws_bytes("ddpm_fuse_conv_bwd_weight_workspace_bytes", n, c, h, w, dt)
                 ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=cat.device)
                 code = lib.ddpm_fuse_conv_bwd_weight(_ptr(cat), _ptr(grad_out), _ptr(gw), _ptr(gb),
                                                      _ptr(ws), nbytes, n, c, h, w, dt, _stream(cat))
