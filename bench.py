@@ -465,7 +465,7 @@ def kernel_mode(args):
     wsb = max(int(lib.ddpm_gen_bwd_w_workspace_bytes(B, C, hw, hw, k, code)),
               int(lib.ddpm_gen_bwd_y_workspace_bytes(C, k)),
               int(lib.ddpm_gen_bwd_x_workspace_bytes(B, C, hw, hw, k, *DIL)),
-              int(lib.ddpm_fuse_conv_workspace_bytes(C, code)),
+              int(lib.ddpm_fuse_conv_workspace_bytes(B, C, hw, hw, code)),
               int(lib.ddpm_fuse_conv_bwd_weight_workspace_bytes(B, C, hw, hw, code)), 1)
     cw = rnd(C, 4 * C, 3, 3) * 0.02
     cb, dcw, dcb = rnd(C), torch.empty(C, 4 * C, 3, 3, device="cuda", dtype=dt), torch.empty(C, device="cuda", dtype=dt)

@@ -44,7 +44,7 @@ SIGNATURES: dict[str, tuple[list, type]] = {
     "ddpm_gen_bwd_y_noalloc": ([_P, _P, _P, _P, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
     "ddpm_gen_bwd_y_noalloc_scratch_bytes": ([], _L),
     "ddpm_gen_bwd_w_workspace_bytes": ([_L, _L, _L, _L, _I, _I], _L),
-    "ddpm_fuse_conv_workspace_bytes": ([_L, _I], _L),
+    "ddpm_fuse_conv_workspace_bytes": ([_L, _L, _L, _L, _I], _L),
     "ddpm_fuse_conv_fwd": ([_P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _P], _I),
     "ddpm_fuse_conv_bwd_data": ([_P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _P], _I),
     "ddpm_fuse_conv_bwd_weight_workspace_bytes": ([_L, _L, _L, _L, _I], _L),
@@ -53,7 +53,7 @@ SIGNATURES: dict[str, tuple[list, type]] = {
 }
 
 
-ABI_VERSION = 2  # include/ddpm_hip.h
+ABI_VERSION = 3  # include/ddpm_hip.h
 
 
 class HipLibraryError(RuntimeError):

@@ -54,6 +54,8 @@ struct ConvGeom {
   int nc32;           // ceil(K / 32)
   int mb;             // 16-plane blocks of m per workgroup
   int mgroups;        // ceil(M / (mb * 16))
+  int ks;             // splits of the input planes (K): 1, or more for small images
+  int cc_per;         // 32-plane chunks per K split
   int seg;            // staged elements per segment row (sw + 2 * kCvPad)
   int x4;             // input rows copied in 16-byte lanes (W % 8 == 0, aligned base)
 };
@@ -127,11 +129,14 @@ struct CvLds {
   static_assert(kCvPix == 256, "segments hold at most kXD dwords per plane");
 };
 
+// out: the result in T (ks = 1), or with K split (ks > 1) the fp32 partial
+// sums part[ksplit][n][M][H*W] (no bias) that conv3x3_reduce_kernel adds up.
 template <typename T, bool BIAS, int MB, bool WIDE>
 __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict__ in,
                                                              const uint32_t* __restrict__ pk,
                                                              const T* __restrict__ bias,
-                                                             T* __restrict__ out, ConvGeom g) {
+                                                             T* __restrict__ out,
+                                                             float* __restrict__ part, ConvGeom g) {
   typedef Mma<T> M;
   typedef typename M::V V;
   typedef CvLds<T, MB, WIDE> L;
@@ -141,7 +146,9 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
 
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int mg = bid % g.mgroups;
-  const int tile = bid / g.mgroups;
+  const int rest = bid / g.mgroups;
+  const int ksplit = rest % g.ks;
+  const int tile = rest / g.ks;
   const int tiles_img = g.tiles_h * g.tiles_w;
   const int n = tile / tiles_img;
   const int trem = tile - n * tiles_img;
@@ -153,7 +160,11 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int col16 = lane & 15, quad = lane >> 4;
-  const int nstage = 3 * g.nc32;  // (cc, ki)
+  // stages (cc, ki) of this workgroup's K split: s0 .. s0 + nstage - 1
+  const int cc0 = ksplit * g.cc_per;
+  const int cc1 = cc0 + g.cc_per < g.nc32 ? cc0 + g.cc_per : g.nc32;
+  const int s0 = 3 * cc0;
+  const int nstage = cc1 > cc0 ? 3 * (cc1 - cc0) : 0;
   // this wave's 32 pixels: segment row wseg (wave-uniform), columns pcol0 ..
   const int wseg = (32 * wave) / g.sw;
   const int pcol0 = 32 * wave - wseg * g.sw;
@@ -237,12 +248,12 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
   // staged element of this lane's block-0 pixel at tap column 0: segment row
   // wseg, column pad + pcol0 + col16
   const int el0 = wseg * g.seg + kCvPad + pcol0 + col16;
-  stage(0, 0);
+  if (nstage > 0) stage(s0, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int s = 0; s < nstage; ++s) {
     const int buf = s & 1;
-    if (s + 1 < nstage) stage(s + 1, buf ^ 1);
+    if (s + 1 < nstage) stage(s0 + s + 1, buf ^ 1);
     const uint32_t* __restrict__ bb = csm + buf * L::kBuf;
     // this lane's input elements: plane 4e + quad, element el0 + 16 blk + dw
     const uint32_t* __restrict__ xq = bb + quad * L::kXS;
@@ -293,7 +304,7 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
     for (int blk = 0; blk < 2; ++blk) {
       const int w = w0 + pcol0 + col16 + 16 * blk;
       if (w < W) {
-        T* __restrict__ yo = out + (int64_t)n * g.M * HW + (int64_t)h * W + w;
+        const int64_t o = ((int64_t)ksplit * g.N + n) * g.M * HW + (int64_t)h * W + w;
 #pragma unroll
         for (int ib = 0; ib < MB; ++ib)
 #pragma unroll
@@ -301,13 +312,42 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
             const int m = (mg * MB + ib) * 16 + 4 * quad + e;
             if (m < g.M) {
               float v = acc[blk][ib][e];
-              if constexpr (BIAS) v += to_f(bias[m]);
-              yo[(int64_t)m * HW] = from_f<T>(v);
+              if (g.ks > 1) {
+                part[o + (int64_t)m * HW] = v;
+              } else {
+                if constexpr (BIAS) v += to_f(bias[m]);
+                out[o + (int64_t)m * HW] = from_f<T>(v);
+              }
             }
           }
       }
     }
   }
+}
+
+// out[n][m][p] = bias[m] + sum over the K splits of part[s][n][m][p], in
+// split order (deterministic); VEC consecutive pixels per thread.
+template <typename T, bool BIAS, int VEC>
+__global__ __launch_bounds__(256) void conv3x3_reduce_kernel(const float* __restrict__ part,
+                                                             const T* __restrict__ bias,
+                                                             T* __restrict__ out, int64_t total,
+                                                             int64_t hw, int m, int ks) {
+  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * VEC;
+  if (i0 >= total) return;
+  float v[VEC];
+  const float b = BIAS ? to_f(bias[(i0 / hw) % m]) : 0.f;  // VEC pixels share a plane (hw % VEC == 0)
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) v[e] = b;
+  for (int s = 0; s < ks; ++s) {
+    if constexpr (VEC == 4) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(part + (int64_t)s * total + i0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += a[e];
+    } else {
+      v[0] += part[(int64_t)s * total + i0];
+    }
+  }
+  VecIO<T, VEC>::store(out + i0, v);
 }
 
 namespace {
@@ -350,7 +390,16 @@ void cv_geom(ConvGeom& g, int64_t n, int64_t k, int64_t m, int64_t h, int64_t w,
   g.nc32 = (int)((k + 31) / 32);
   g.mb = kCvMaxMB;
   const int64_t tiles = n * g.tiles_h * g.tiles_w;
-  while (g.mb > 1 && tiles * ((m + g.mb * 16 - 1) / (g.mb * 16)) < kCvFillWGs) g.mb /= 2;
+  // fewer workgroups than CUs with four-block m groups: first split the input
+  // planes (K) over up to nc32 / 2 workgroups (fp32 partials summed by a
+  // second kernel; each split keeps >= 2 chunks of 32 planes, so >= 6 stages),
+  // then halve the m blocks
+  g.ks = 1;
+  const int64_t mg4 = (m + kCvMaxMB * 16 - 1) / (kCvMaxMB * 16);
+  while (tiles * mg4 * g.ks < kCvFillWGs && 2 * g.ks * 2 <= g.nc32) g.ks *= 2;
+  g.cc_per = (g.nc32 + g.ks - 1) / g.ks;
+  g.ks = (g.nc32 + g.cc_per - 1) / g.cc_per;
+  while (g.mb > 1 && tiles * ((m + g.mb * 16 - 1) / (g.mb * 16)) * g.ks < kCvFillWGs) g.mb /= 2;
   g.mgroups = (int)((m + g.mb * 16 - 1) / (g.mb * 16));
   g.seg = sw + 2 * kCvPad;
   (void)esz;
@@ -377,15 +426,26 @@ int cv_check(int64_t n, int64_t k, int64_t m, int64_t h, int64_t w, int dtype) {
   return kOk;
 }
 
+int64_t cv_align(int64_t v) { return (v + 255) / 256 * 256; }
+
+// Workspace of one direction: the packed weight, then (K split) the fp32
+// partial sums [ks][n][m][h*w].
+int64_t cv_workspace_bytes(const ConvGeom& g, int dtype) {
+  const int64_t pk = cv_pack_bytes(g, dtype);
+  if (g.ks <= 1) return pk;
+  return cv_align(pk) + (int64_t)g.ks * g.N * g.M * g.H * g.W * (int64_t)sizeof(float);
+}
+
 int cv_run(const void* in, const void* wt, const void* bias, void* out, void* workspace,
            int64_t workspace_bytes, int64_t n, int64_t k, int64_t m, int64_t h, int64_t w, int rot,
            int dtype, hipStream_t stream) {
   const int esz = dtype == kF32 ? 4 : 2;
   ConvGeom g;
   cv_geom(g, n, k, m, h, w, esz);
-  const int64_t need = cv_pack_bytes(g, dtype);
+  const int64_t need = cv_workspace_bytes(g, dtype);
   if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 16 != 0)
     return kWorkspaceTooSmall;
+  float* part = g.ks > 1 ? (float*)((char*)workspace + cv_align(cv_pack_bytes(g, dtype))) : nullptr;
   g.x4 = (w % 8 == 0) && ((uintptr_t)in % 16 == 0);
   return cv_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
@@ -402,13 +462,31 @@ int cv_run(const void* in, const void* wt, const void* bias, void* out, void* wo
                          (uint32_t*)workspace, g, rot);
     int e = (int)hipGetLastError();
     if (e != 0) return e;
-    const dim3 grid((unsigned)((int64_t)n * g.tiles_h * g.tiles_w * g.mgroups));
+    const dim3 grid((unsigned)((int64_t)n * g.tiles_h * g.tiles_w * g.mgroups * g.ks));
     auto launch = [&](auto kern, size_t lds) {
       const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
       if (ae != 0) return ae;
       hipLaunchKernelGGL(kern, grid, dim3(kCvThreads), lds, stream, (const T*)in,
-                         (const uint32_t*)workspace, (const T*)bias, (T*)out, g);
-      return (int)hipGetLastError();
+                         (const uint32_t*)workspace, (const T*)bias, (T*)out, part, g);
+      int e2 = (int)hipGetLastError();
+      if (e2 != 0 || g.ks <= 1) return e2;
+      // the K splits' partial sums (and the bias) in split order
+      const int64_t total = n * m * h * w, hw = h * w;
+      const bool v4 = hw % 4 == 0 && (uintptr_t)out % (4 * sizeof(T)) == 0;
+      const int64_t items = v4 ? total / 4 : total;
+      const dim3 rgrid((unsigned)((items + 255) / 256));
+      auto reduce = [&](auto bconst, auto vconst) {
+        constexpr bool RB = decltype(bconst)::value;
+        constexpr int RV = decltype(vconst)::value;
+        hipLaunchKernelGGL((conv3x3_reduce_kernel<T, RB, RV>), rgrid, dim3(256), 0, stream,
+                           (const float*)part, (const T*)bias, (T*)out, total, hw, (int)m, g.ks);
+        return (int)hipGetLastError();
+      };
+      if (bias)
+        return v4 ? reduce(std::true_type(), std::integral_constant<int, 4>())
+                  : reduce(std::true_type(), std::integral_constant<int, 1>());
+      return v4 ? reduce(std::false_type(), std::integral_constant<int, 4>())
+                : reduce(std::false_type(), std::integral_constant<int, 1>());
     };
     auto pick = [&](auto b) {
       constexpr bool B = decltype(b)::value;
@@ -431,14 +509,15 @@ int cv_run(const void* in, const void* wt, const void* bias, void* out, void* wo
 
 using namespace ddpm;
 
-extern "C" int64_t ddpm_fuse_conv_workspace_bytes(int64_t c, int dtype) {
-  if (c <= 0 || dtype < kF32 || dtype > kF16) return 0;
-  // the largest packed weight over the shapes: four-block m groups (fewer
-  // blocks per group pack no more bytes)
+extern "C" int64_t ddpm_fuse_conv_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w,
+                                                  int dtype) {
+  if (n < 0 || c <= 0 || h < 0 || w < 0 || dtype < kF32 || dtype > kF16) return 0;
+  if (n == 0 || h == 0 || w == 0) return 0;
+  // the larger of the two directions' needs at this shape
   ConvGeom gf, gd;
-  cv_geom(gf, 1 << 20, 4 * c, c, 1, 1, dtype == kF32 ? 4 : 2);  // forward: K = 4C, M = C
-  cv_geom(gd, 1 << 20, c, 4 * c, 1, 1, dtype == kF32 ? 4 : 2);  // input gradient: K = C, M = 4C
-  const int64_t a = cv_pack_bytes(gf, dtype), b = cv_pack_bytes(gd, dtype);
+  cv_geom(gf, n, 4 * c, c, h, w, dtype == kF32 ? 4 : 2);  // forward: K = 4C, M = C
+  cv_geom(gd, n, c, 4 * c, h, w, dtype == kF32 ? 4 : 2);  // input gradient: K = C, M = 4C
+  const int64_t a = cv_workspace_bytes(gf, dtype), b = cv_workspace_bytes(gd, dtype);
   return a > b ? a : b;
 }
 

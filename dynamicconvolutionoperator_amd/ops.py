@@ -438,8 +438,8 @@ def fuse_conv_supported(cat, weight, bias) -> bool:
     return ci * h * w * cat.element_size() <= 2**31 - 1
 
 
-def _fuse_conv_workspace(c, dt, device):
-    nbytes = _ws_bytes("ddpm_fuse_conv_workspace_bytes", c, dt)
+def _fuse_conv_workspace(n, c, h, w, dt, device):
+    nbytes = _ws_bytes("ddpm_fuse_conv_workspace_bytes", n, c, h, w, dt)
     return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device), nbytes
 
 
@@ -461,7 +461,7 @@ class _FuseConv3x3(torch.autograd.Function):
         dt = _dt(cat)
         lib = _lib.load()
         with _on(cat.device):
-            ws, nbytes = _fuse_conv_workspace(c, dt, cat.device)
+            ws, nbytes = _fuse_conv_workspace(n, c, h, w, dt, cat.device)
             code = lib.ddpm_fuse_conv_fwd(_ptr(cat), _ptr(weight),
                                           _ptr(bias.contiguous()) if bias is not None else None,
                                           _ptr(out), _ptr(ws), nbytes, n, c, h, w, dt, _stream(cat))
@@ -482,7 +482,7 @@ class _FuseConv3x3(torch.autograd.Function):
             dt = _dt(cat)
             lib = _lib.load()
             with _on(cat.device):
-                ws, nbytes = _fuse_conv_workspace(c, dt, cat.device)
+                ws, nbytes = _fuse_conv_workspace(n, c, h, w, dt, cat.device)
                 code = lib.ddpm_fuse_conv_bwd_data(_ptr(grad_out), _ptr(weight), _ptr(grad_cat),
                                                    _ptr(ws), nbytes, n, c, h, w, dt, _stream(cat))
             _lib.check(code, "ddpm_fuse_conv_bwd_data")

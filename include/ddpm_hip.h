@@ -38,7 +38,7 @@ extern "C" {
 #define DDPM_DTYPE_BF16 1
 #define DDPM_DTYPE_F16 2
 
-/* ABI version of this header (2). */
+/* ABI version of this header (3). */
 int ddpm_abi_version(void);
 
 /* Text for any status code returned by this library (static storage). */
@@ -201,10 +201,13 @@ int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out, void* gra
 
 /* ---- the 3x3 fuse convolution (Conv2d(4C -> C, 3, padding 1)) -------- */
 
-/* Bytes of workspace ddpm_fuse_conv_fwd / _bwd_data need for their packed
- * weight (MFMA fragment order; fp32 as bf16 hi / lo): the larger of the two
+/* Bytes of workspace ddpm_fuse_conv_fwd / _bwd_data need at this shape: the
+ * packed weight (MFMA fragment order; fp32 as bf16 hi / lo) and, where the
+ * image is too small to fill the GPU with whole input-plane loops (e.g.
+ * 128x128 C=64 forward), the fp32 partial sums of the input-plane splits,
+ * summed by a second kernel in split order.  The larger of the two
  * directions, so one buffer serves both. */
-int64_t ddpm_fuse_conv_workspace_bytes(int64_t c, int dtype);
+int64_t ddpm_fuse_conv_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w, int dtype);
 
 /* out[n][co][h][w] = bias[co] + sum_{ci,ki,kj} weight[co][ci][ki][kj] *
  *                    cat[n][ci][h+ki-1][w+kj-1]  (zero padding), accumulated in
