@@ -115,14 +115,23 @@ __device__ __forceinline__ void stage_plane(TS* __restrict__ s, const T* __restr
   }
 }
 
-// Staged value at tile row `lrow` (0 = first staged row) and staged column j.
+// Staged value at tile row `lrow` (0 = first staged row) and staged column j
+// = jc + t, for a lane whose first staged column jc is a multiple of V (the
+// column pad CP and the lane's V * cl both are): `rb` = lrow * RS + jc / V is
+// the lane's part, formed once per staged row, and `t` is
+// wave-uniform (a tap's column shift plus the element index), so the phase
+// and index arithmetic runs on the scalar unit and a read costs one vector
+// add (per-element phase / index / multiply by PS had made the filter
+// kernels VALU-bound).
 template <int V, typename TS = float>
-__device__ __forceinline__ float staged(const TS* __restrict__ s, const FilterGeom& g, int lrow,
-                                        int j) {
+__device__ __forceinline__ float staged(const TS* __restrict__ s, const FilterGeom& g, int rb,
+                                          int t) {
   if constexpr (V == 1) {
-    return to_f(s[lrow * g.RS + j]);
+    return to_f(s[rb + t]);
   } else {
-    return to_f(s[lrow * g.RS + (j & (V - 1)) * g.PS + (j / V)]);
+    constexpr int L = V == 8 ? 3 : (V == 4 ? 2 : 1);
+    static_assert(V == 2 || V == 4 || V == 8, "phase split by a power of two");
+    return to_f(s[rb + (t & (V - 1)) * g.PS + (t >> L)]);
   }
 }
 
@@ -184,7 +193,7 @@ __global__ __launch_bounds__(kFilterThreads) void filter_fwd_kernel(const TX* __
   {
     float xv[V];
 #pragma unroll
-    for (int v = 0; v < V; ++v) xv[v] = staged<V>(xs, g, trow + g.R, jc + v);
+    for (int v = 0; v < V; ++v) xv[v] = staged<V>(xs, g, (trow + g.R) * g.RS + jc / V, v);
     VecIO<TK, V>::store_nt(op, xv);
   }
 #pragma unroll
@@ -202,7 +211,7 @@ __global__ __launch_bounds__(kFilterThreads) void filter_fwd_kernel(const TX* __
 #pragma unroll
     for (int v = 0; v < V; ++v) acc[v] = 0.f;
     for (int ki = 0; ki < K; ++ki) {
-      const int lrow = trow + g.R + (ki - r) * d;
+      const int rb = (trow + g.R + (ki - r) * d) * g.RS + jc / V;
       for (int kj = 0; kj < K; ++kj) {
         const int t = ki * K + kj;
         KV kv;
@@ -212,9 +221,9 @@ __global__ __launch_bounds__(kFilterThreads) void filter_fwd_kernel(const TX* __
           kv = kpre[b * KS * KS + t];
         else
           kv = __builtin_nontemporal_load(reinterpret_cast<const KV*>(kp + b * bstride + t * HW));
-        const int j0 = jc + (kj - r) * d;
+        const int t0 = (kj - r) * d;
 #pragma unroll
-        for (int v = 0; v < V; ++v) acc[v] = fmaf(to_f(kv[v]), staged<V>(xs, g, lrow, j0 + v), acc[v]);
+        for (int v = 0; v < V; ++v) acc[v] = fmaf(to_f(kv[v]), staged<V>(xs, g, rb, t0 + v), acc[v]);
       }
     }
     VecIO<TK, V>::store_nt(op + (b + 1) * ostride, acc);
@@ -267,12 +276,12 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_k_kernel(const TX* 
   for (int b = 0; b < 3; ++b) {
     const int d = dil_of(b, g.d0, g.d1, g.d2);
     for (int ki = 0; ki < K; ++ki) {
-      const int lrow = trow + g.R + (ki - r) * d;
+      const int rb = (trow + g.R + (ki - r) * d) * g.RS + jc / V;
       for (int kj = 0; kj < K; ++kj) {
-        const int j0 = jc + (kj - r) * d;
+        const int t0 = (kj - r) * d;
         float prod[V];
 #pragma unroll
-        for (int v = 0; v < V; ++v) prod[v] = go[b][v] * staged<V>(xs, g, lrow, j0 + v);
+        for (int v = 0; v < V; ++v) prod[v] = go[b][v] * staged<V>(xs, g, rb, t0 + v);
         // non-temporal: the 3*K*K planes are written once and not read back
         // here (measured 17% faster than plain stores at 256x256)
         VecIO<TK, V>::store_nt(kp + b * bstride + (int64_t)(ki * K + kj) * HW, prod);
@@ -527,16 +536,15 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_vec_kernel(const 
     if (it + 1 < 3 * KS) load_row((it + 1) / KS, (it + 1) % KS, nxt);
     const int d = dil_of(b, g.d0, g.d1, g.d2);
     const TS* __restrict__ gb = gs + b * lplane;
-    const int lrow = trow + g.R - (ki - r) * d;
+    const int rb = (trow + g.R - (ki - r) * d) * g.RS + jc / V;
 #pragma unroll
     for (int kj = 0; kj < KS; ++kj) {
       const int dw = (kj - r) * d;
       const int s = ((-dw) % V + V) % V;
       float kv[V];
       realign<TK, V>(cur[kj][0], cur[kj][1], s, kv);
-      const int j0 = jc - dw;
 #pragma unroll
-      for (int v = 0; v < V; ++v) acc[v] = fmaf(kv[v], staged<V, TS>(gb, g, lrow, j0 + v), acc[v]);
+      for (int v = 0; v < V; ++v) acc[v] = fmaf(kv[v], staged<V, TS>(gb, g, rb, v - dw), acc[v]);
     }
   }
   VecIO<TX, V>::store_nt(gx + (int64_t)plane * HW + (int64_t)gh * g.W + gw, acc);

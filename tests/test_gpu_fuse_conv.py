@@ -52,7 +52,8 @@ def test_fuse_conv_matches_conv2d(shape, dtype):
 @pytest.mark.parametrize("hw", [256, 128])
 def test_fuse_conv_full_size(dtype, hw):
     """256x256 (one-row segments, four-block m groups) and 128x128 (two-row
-    segments; the forward's 64 output planes in four single-block groups)."""
+    segments; the forward's 256 input planes in four splits of two 32-plane
+    chunks, their fp32 partials summed by the reduce kernel)."""
     say(f"fuse conv {hw}x{hw} C=64 dtype={dtype}")
     _check((1, 64, hw, hw), dtype, 910)
 
@@ -96,3 +97,27 @@ def test_fuse_conv_weight_gradient_empty_batch_and_determinism():
         ops.fuse_conv3x3(cat, w2, b2).backward(g)
         grads.append((w2.grad.clone(), b2.grad.clone()))
     assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(1, 40, 16, 32), (1, 56, 9, 33), (2, 128, 8, 20)])
+def test_fuse_conv_uneven_plane_splits(shape, dtype):
+    """Small images whose input-plane chunks do not divide evenly among the
+    splits: C=40 forward has 5 chunks of 32 planes in splits of 3 + 2, C=56
+    7 chunks in 4 + 3 (W = 33: element-wise rows), and the C=128 input
+    gradient 4 chunks in 2 + 2 over two images."""
+    say(f"fuse conv uneven splits shape={shape} dtype={dtype}")
+    _check(shape, dtype, 970 + shape[1])
+
+
+def test_fuse_conv_split_determinism():
+    """The split partials are summed in a fixed order: two forward calls at
+    128x128 C=64 (four splits) are bit-identical."""
+    say("fuse conv split determinism 128x128")
+    cat = randn((1, 256, 128, 128), 990).to(DEV)
+    conv = torch.nn.Conv2d(256, 64, 3, 1, 1)
+    wt, b = conv.weight.detach().to(DEV), conv.bias.detach().to(DEV)
+    o1 = ops.fuse_conv3x3(cat, wt, b)
+    o2 = ops.fuse_conv3x3(cat, wt, b)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
