@@ -128,6 +128,65 @@ def time_loop(fn, steps, warmup):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
+def graph_loop(fn, steps, warmup, prepare=None):
+    """Mean ms per replay of `fn` captured once in a HIP graph
+    (torch.cuda.graph): warm-up calls on a side stream, capture, one replay,
+    then `steps` replays bracketed by syncs.  `prepare` runs before each
+    warm-up call and before the capture (outside the graph)."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(max(warmup, 2)):
+            if prepare is not None:
+                prepare()
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    if prepare is not None:
+        prepare()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    del graph
+    return ms
+
+
+def graph_cases(module, x, y, steps, warmup):
+    """Inference and forward + backward (from a fixed output gradient, no
+    loss kernels) of `module`: eager and replayed from a HIP graph."""
+    import torch
+
+    module.eval()
+    with torch.no_grad():
+        res = {"infer_eager_ms": time_loop(lambda: module(x, y), steps, warmup),
+               "infer_graph_ms": graph_loop(lambda: module(x, y), steps, warmup)}
+    module.train()
+    xg = x.detach().clone().requires_grad_()
+    yg = y.detach().clone().requires_grad_()
+    gout = torch.randn_like(x)
+
+    def clear():
+        module.zero_grad(set_to_none=True)
+        xg.grad = None
+        yg.grad = None
+
+    def fwd_bwd():
+        torch.autograd.backward(module(xg, yg), gout)
+
+    res["fwd_bwd_eager_ms"] = time_loop(lambda: (clear(), fwd_bwd()), steps, warmup)
+    res["fwd_bwd_graph_ms"] = graph_loop(fwd_bwd, steps, warmup, prepare=clear)
+    clear()
+    return res
+
+
 class LaunchTimer:
     """Brackets every call of the named C-ABI entry points with HIP events.
 
@@ -625,6 +684,12 @@ def main():
         x, y = make_inputs(torch.float32, grad=False)
         with torch.inference_mode():
             extra["infer_ms_fp32"] = time_loop(lambda: module(x, y), args.steps, args.warmup)
+        # ---- the same module launched from HIP graphs (captured once, replayed)
+        hip_graph = {"256_fp32": graph_cases(module, x, y, args.steps, args.warmup)}
+        del module, x, y
+        module = make_module(torch.bfloat16)
+        x, y = make_inputs(torch.bfloat16, grad=False)
+        hip_graph["256_bf16"] = graph_cases(module, x, y, args.steps, args.warmup)
         del module, x, y
         torch.cuda.empty_cache()
         progress("bf16 training and inference done")
@@ -647,6 +712,7 @@ def main():
         with torch.inference_mode():
             c2["fused_infer_ms"] = time_loop(lambda: module(x, y), args.steps, args.warmup)
         extra["c2_infer_128_fp32"] = c2
+        hip_graph["128_fp32"] = graph_cases(module, x, y, args.steps, args.warmup)
         del module, x, y
 
         # ---- K=5 128x128 C=64 bf16, materialized route: inference, fwd+bwd
@@ -661,6 +727,10 @@ def main():
         with torch.inference_mode():
             c4["infer_ms"] = time_loop(lambda: module(x, y), args.steps, args.warmup)
         c4["route"] = "materialized (HIP generator GEMMs + HIP filter)"
+        hip_graph["k5_128_bf16"] = graph_cases(module, x.detach(), y.detach(), args.steps, args.warmup)
+        hip_graph["note"] = ("eager vs HIP-graph replay of the same module: inference, and forward + "
+                             "backward from a fixed output gradient (no loss kernels); ms per call")
+        extra["hip_graph"] = hip_graph
         # the filter forward alone (two 157 MB kernel tensors rotate past the MALL)
         c4["filter_fwd"] = filter_op_bandwidth("ddpm_filter_fwd", torch.bfloat16, 128, 128, k=5, sets=2)
         extra["c4_k5_128_bf16"] = c4
