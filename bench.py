@@ -256,6 +256,8 @@ def work_per_launch(name, esize):
         "ddpm_gen_bwd_x": ((6 * E + G * (C + 1)) * esize, gemm),  # y, gO (4E) in; dX out
         "ddpm_gen_bwd_y": ((5 * E + G * C) * esize, gemm),  # x, gO branches (3E) in; dY out
         "ddpm_gen_bwd_w": ((5 * E) * esize + G * (C + 1) * esize, gemm),  # x, y, gO branches in
+        # dX and dW/db in one call: x, y, gO (4E) in, dX out, W/b in, dW/db out; both GEMMs
+        "ddpm_gen_bwd_xw": ((7 * E + 2 * G * (C + 1)) * esize, 2 * gemm),
         # the 3x3 fuse convolution 4C -> C: GEMMs of 2*N*H*W*C*4C*9 flops
         "ddpm_fuse_conv_fwd": ((5 * E + 36 * C * C) * esize, conv),  # cat (4E) in, out (E)
         "ddpm_fuse_conv_bwd_data": ((5 * E + 36 * C * C) * esize, conv),  # gO (E) in, d cat (4E)
@@ -491,27 +493,20 @@ def cpu_baseline(budget_s):
 COPY_BYTES = 2**30  # 'copy': a plain 1 GiB device copy (4x the MALL; reads and writes this many bytes)
 
 
-def kernel_mode(args):
-    """Launches the named entry points `reps` times each at B1 C64 (K, res from
-    the arguments; dilations 1/3/5) on seeded inputs, rotating through `sets`
-    input sets, and 'copy' as a plain device copy of COPY_BYTES, so that
-    rocprofv3 can read each kernel's duration and HBM counters (FETCH_SIZE /
-    WRITE_SIZE) and the copy calibrates them."""
+def make_calls(lib, dt, k, hw, nsets):
+    """Seeded inputs at B1 C64 (kernel size k, hw x hw, dilations 1/3/5) in
+    `nsets` input sets, and one launch function per C-ABI entry point (taking
+    an input set; 'copy' is a plain device copy of COPY_BYTES)."""
     import ctypes
 
     import torch
 
-    from dynamicconvolutionoperator_amd import _lib
-
-    lib = _lib.load()
-    dt = {"f32": torch.float32, "bf16": torch.bfloat16}[args.dtype]
     code = 0 if dt == torch.float32 else 1
-    k, hw = args.kernel_size, args.res
     ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     g = torch.Generator(device="cuda").manual_seed(1)
     rnd = lambda *shape: torch.randn(*shape, device="cuda", generator=g).to(dt)  # noqa: E731
     sets = []
-    for _ in range(max(1, args.sets)):
+    for _ in range(max(1, nsets)):
         sets.append({
             "x": rnd(B, C, hw, hw), "y": rnd(B, C, hw, hw), "go": rnd(B, 4 * C, hw, hw),
             "kern": rnd(B, 3, C, k * k, hw, hw),
@@ -530,6 +525,8 @@ def kernel_mode(args):
     cb, dcw, dcb = rnd(C), torch.empty(C, 4 * C, 3, 3, device="cuda", dtype=dt), torch.empty(C, device="cuda", dtype=dt)
     cout = torch.empty(B, C, hw, hw, device="cuda", dtype=dt)
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    wsxb = max(int(lib.ddpm_gen_bwd_x_workspace_bytes(B, C, hw, hw, k, *DIL)), 1)
+    wsx = torch.empty(wsxb, dtype=torch.uint8, device="cuda")
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -543,6 +540,9 @@ def kernel_mode(args):
                                                        wsb, *shp, code, s),
         "ddpm_gen_bwd_w": lambda t: lib.ddpm_gen_bwd_w(ptr(t["x"]), ptr(t["y"]), ptr(t["go"]), ptr(dw),
                                                        ptr(db), ptr(ws), wsb, *shp, code, s),
+        "ddpm_gen_bwd_xw": lambda t: lib.ddpm_gen_bwd_xw(ptr(t["x"]), ptr(t["y"]), ptr(wt), ptr(bs),
+                                                         ptr(t["go"]), ptr(dx), ptr(dw), ptr(db), ptr(wsx),
+                                                         wsxb, ptr(ws), wsb, *shp, code, s),
         # the generator 1x1 convolution of the materialized route writes the kernel tensor
         "ddpm_gen_kernels": lambda t: lib.ddpm_gen_kernels(ptr(t["y"]), ptr(wt), ptr(bs), ptr(t["kern"]), B, C,
                                                            hw, hw, k, code, s),
@@ -563,6 +563,48 @@ def kernel_mode(args):
                                                                              wsb, B, C, hw, hw, code, s),
         "copy": lambda t: (dst.copy_(src), 0)[1],
     }
+    return calls, sets
+
+
+def standalone_ms(lib, names, dt, reps=20):
+    """Mean ms per launch of each named entry point launched alone at the
+    headline shape (HIP events around `reps` launches, two input sets)."""
+    import torch
+
+    calls, sets = make_calls(lib, dt, K, H, 2)
+    res = {}
+    for name in names:
+        for i in range(2):
+            calls[name](sets[i])
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for i in range(reps):
+            rc = calls[name](sets[i % 2])
+            if rc:
+                raise RuntimeError(f"{name} failed with status {rc}")
+        t1.record()
+        torch.cuda.synchronize()
+        res[name] = t0.elapsed_time(t1) / reps
+    del calls, sets
+    torch.cuda.empty_cache()
+    return res
+
+
+def kernel_mode(args):
+    """Launches the named entry points `reps` times each at B1 C64 (K, res from
+    the arguments; dilations 1/3/5) on seeded inputs, rotating through `sets`
+    input sets, and 'copy' as a plain device copy of COPY_BYTES, so that
+    rocprofv3 can read each kernel's duration and HBM counters (FETCH_SIZE /
+    WRITE_SIZE) and the copy calibrates them."""
+    import torch
+
+    from dynamicconvolutionoperator_amd import _lib
+
+    lib = _lib.load()
+    dt = {"f32": torch.float32, "bf16": torch.bfloat16}[args.dtype]
+    k, hw = args.kernel_size, args.res
+    calls, sets = make_calls(lib, dt, k, hw, args.sets)
     names = args.kernel.split(",")
     for name in names:
         if name not in calls:
@@ -645,9 +687,18 @@ def main():
     #      now) and the roofline entry
     timer = LaunchTimer(lib, entries)
     kernels = kernel_breakdown(lib, timer, module, x, y)
-    dominant = max(kernels, key=lambda n: kernels[n]["share_of_step_ms"])
+    cands = {n: v["share_of_step_ms"] for n, v in kernels.items()}
+    if "ddpm_gen_bwd_xw" in cands:
+        # the step runs dX and dW as one call (dX's halo reduction on the CUs
+        # dW leaves free): the roofline takes its two GEMM entry points timed
+        # alone at the same shape
+        alone = standalone_ms(lib, ("ddpm_gen_bwd_x", "ddpm_gen_bwd_w"), torch.float32)
+        extra["standalone_fp32_ms"] = alone
+        cands.pop("ddpm_gen_bwd_xw")
+        cands.update(alone)
+    dominant = max(cands, key=cands.get)
     nbytes, flops = work_per_launch(dominant, 4)
-    dom_ms = kernels[dominant]["ms"]
+    dom_ms = cands[dominant]
     if flops > 0:
         # fp32 operands run as three bf16 MFMA products: ceiling = bf16 dense peak / 3
         peak = BF16_DENSE_TFLOPS / 3.0

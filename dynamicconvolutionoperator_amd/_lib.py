@@ -50,10 +50,12 @@ SIGNATURES: dict[str, tuple[list, type]] = {
     "ddpm_fuse_conv_bwd_weight_workspace_bytes": ([_L, _L, _L, _L, _I], _L),
     "ddpm_fuse_conv_bwd_weight": ([_P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _P], _I),
     "ddpm_gen_bwd_w": ([_P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
+    "ddpm_gen_bwd_xw": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _P, _L, _L, _L, _L, _L, _I, _I, _I,
+                         _I, _I, _P], _I),
 }
 
 
-ABI_VERSION = 3  # include/ddpm_hip.h
+ABI_VERSION = 4  # include/ddpm_hip.h
 
 
 class HipLibraryError(RuntimeError):

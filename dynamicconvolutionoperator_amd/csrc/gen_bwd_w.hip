@@ -31,7 +31,7 @@
 // writes their split to LDS after the step's MFMAs (no pre-pass over y, no
 // workspace planes), so every B fragment is a plain 16-byte LDS read.
 
-#include "gen_common.h"
+#include "gen_bwd_x.h"
 #include <type_traits>
 
 namespace ddpm {
@@ -58,6 +58,7 @@ struct WGradGeom {
   int x16;             // x rows hold whole 16-byte chunks (W % (16/E) == 0, aligned): 16-byte copies
   int x4;              // y and gradient rows 16-byte aligned (W % 8 == 0): 16-byte copies
   int y4;              // fp32 y rows 16-byte aligned (W % 4 == 0): 16-byte register loads
+  int dw_blocks;       // weight-gradient workgroups; any further ones are helpers (see below)
 };
 
 // Tap groups per kernel size: the K = 3 taps are split over three waves of 3
@@ -157,11 +158,15 @@ __global__ __launch_bounds__(256) void gen_ysplit_kernel(const float* __restrict
   }
 }
 
+// Workgroups past g.dw_blocks (ddpm_gen_bwd_xw) are helpers: with at most 16
+// splits x 3 branches x the channel blocks, the weight gradient leaves CUs
+// free (64 of 256 at C = 64), and the helpers run the input gradient's halo
+// reduction (`fin`) there, alongside, instead of as a kernel of its own.
 template <typename T, int KS, int MB>
 __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_partial_kernel(
     const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ gout,
     float* __restrict__ pw, float* __restrict__ pb, T* __restrict__ dw_out, T* __restrict__ db_out,
-    WGradGeom g) {
+    WGradGeom g, BxFinish fin) {
   typedef Mma<T> M;
   typedef typename M::V V;
   typedef typename M::E ME;
@@ -184,7 +189,21 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
   constexpr bool kVBias = E == 4;
   extern __shared__ __attribute__((aligned(16))) uint32_t wsm[];
 
-  const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  if ((int)blockIdx.x >= g.dw_blocks) {
+    // helper workgroup (uniform branch, before any barrier): items of the
+    // halo reduction, grid-strided over the helpers
+    const int64_t stride = (int64_t)(gridDim.x - g.dw_blocks) * NT;
+    const int64_t first = (int64_t)(blockIdx.x - g.dw_blocks) * NT + threadIdx.x;
+    const T* __restrict__ fgo = static_cast<const T*>(fin.gout);
+    T* __restrict__ fgx = static_cast<T*>(fin.gx);
+    if (fin.vec == 4) {
+      for (int64_t it = first; it < fin.items; it += stride) bx_reduce_item<T, 4>(fin.part, fgo, fgx, fin.g, it);
+    } else {
+      for (int64_t it = first; it < fin.items; it += stride) bx_reduce_item<T, 1>(fin.part, fgo, fgx, fin.g, it);
+    }
+    return;
+  }
+  const int logical = xcd_remap(blockIdx.x, g.dw_blocks);
   const int ih = logical % g.ihalves;
   const int lg = logical / g.ihalves;
   const int per_split = 3 * g.cblocks;
@@ -766,6 +785,7 @@ void wgrad_geom(WGradGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int d0
   g.x16 = 0;
   g.x4 = 0;
   g.y4 = 0;
+  g.dw_blocks = 0;
 }
 
 // Workspace: the fp32 split partials (none with one split).
@@ -789,11 +809,23 @@ extern "C" int64_t ddpm_gen_bwd_w_workspace_bytes(int64_t n, int64_t c, int64_t 
   return wg_partial_bytes(g, c, kernel_size);
 }
 
-extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out,
-                              void* grad_weight, void* grad_bias, void* workspace,
-                              int64_t workspace_bytes, int64_t n, int64_t c, int64_t h, int64_t w,
-                              int kernel_size, int d0, int d1, int d2, int dtype,
-                              hipStream_t stream) {
+namespace {
+
+// Helper workgroups for a deferred halo reduction: the CUs the weight-gradient
+// grid leaves free, when that is at least a quarter of them (else the
+// reduction runs as its own kernel after the partial kernel).
+constexpr int kWgFillCUs = 256;
+int wg_helpers(int dw_blocks) {
+  const int free = kWgFillCUs - dw_blocks;
+  return free >= kWgFillCUs / 4 ? free : 0;
+}
+
+// ddpm_gen_bwd_w's work.  check_only: validate and return before launching.
+// fin (optional): a halo reduction of the input gradient to run alongside.
+int bw_run(const void* x, const void* y, const void* grad_out, void* grad_weight,
+           void* grad_bias, void* workspace, int64_t workspace_bytes, int64_t n, int64_t c,
+           int64_t h, int64_t w, int kernel_size, int d0, int d1, int d2, int dtype,
+           hipStream_t stream, bool check_only, const BxFinish* fin) {
   if (dtype < kF32 || dtype > kF16) return kBadArgument;
   GenGeom gg;
   int st = gen_make_geom(gg, n, c, h, w, kernel_size, d0, d1, d2);
@@ -819,6 +851,11 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
   g.y4 = (w % 4 == 0) && ((uintptr_t)y % 16 == 0);
   const int mb = c > 64 ? 4 : (int)((c + 15) / 16);  // 16-channel blocks of i per workgroup
   const int kk = kernel_size * kernel_size;
+  if (kernel_size != 1 && kernel_size != 3) return kUnsupported;
+  if (check_only) return kOk;
+  g.dw_blocks = g.splits * 3 * g.cblocks * g.ihalves;
+  const int helpers = fin ? wg_helpers(g.dw_blocks) : 0;
+  const BxFinish none{nullptr, nullptr, nullptr, TileGeom{}, 0, 1};
   float* pw = g.direct ? nullptr : (float*)workspace;
   float* pb = g.direct ? nullptr : pw + (int64_t)g.splits * 3 * kk * c * c;
   return wg_with_type(dtype, [&](auto tag) {
@@ -831,14 +868,16 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
       const size_t stage = (size_t)2 * L::kBuf * 4;
       const size_t red = (size_t)(kWgSegs * KKc * 16 * (MB * 16 + 1) + KKc * kWgSegs * 16) * sizeof(float);
       const size_t lds = stage > red ? stage : red;
-      const dim3 grid((unsigned)(g.splits * 3 * g.cblocks * g.ihalves));
+      const dim3 grid((unsigned)(g.dw_blocks + helpers));
       const int ae = allow_dynamic_lds(
           reinterpret_cast<const void*>(&gen_bwd_w_partial_kernel<T, KS, MB>), lds);
       if (ae != 0) return ae;
       hipLaunchKernelGGL((gen_bwd_w_partial_kernel<T, KS, MB>), grid,
                          dim3(64 * kWgSegs * WgTaps<KS>::kGroups), lds, stream, (const T*)x,
-                         (const T*)y, (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g);
+                         (const T*)y, (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g,
+                         helpers > 0 ? *fin : none);
       int e = (int)hipGetLastError();
+      if (e == 0 && fin && helpers == 0) e = bx_finish(*fin, dtype, stream);
       if (e != 0 || g.direct) return e;
       const int64_t total_w = (int64_t)3 * KKc * c * c;
       // four input channels per thread when the rows allow 16-byte partial
@@ -860,8 +899,37 @@ extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out
     };
     return wg_with_mb(mb, [&](auto mbc) {
       if (kernel_size == 1) return launch(std::integral_constant<int, 1>(), mbc);
-      if (kernel_size == 3) return launch(std::integral_constant<int, 3>(), mbc);
-      return (int)kUnsupported;
+      return launch(std::integral_constant<int, 3>(), mbc);
     });
   });
+}
+
+}  // namespace
+
+extern "C" int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out,
+                              void* grad_weight, void* grad_bias, void* workspace,
+                              int64_t workspace_bytes, int64_t n, int64_t c, int64_t h, int64_t w,
+                              int kernel_size, int d0, int d1, int d2, int dtype,
+                              hipStream_t stream) {
+  return bw_run(x, y, grad_out, grad_weight, grad_bias, workspace, workspace_bytes, n, c, h, w,
+                kernel_size, d0, d1, d2, dtype, stream, false, nullptr);
+}
+
+extern "C" int ddpm_gen_bwd_xw(const void* x, const void* y, const void* weight, const void* bias,
+                               const void* grad_out, void* grad_x, void* grad_weight,
+                               void* grad_bias, void* workspace_x, int64_t workspace_x_bytes,
+                               void* workspace_w, int64_t workspace_w_bytes, int64_t n, int64_t c,
+                               int64_t h, int64_t w, int kernel_size, int d0, int d1, int d2,
+                               int dtype, hipStream_t stream) {
+  // the weight-gradient part is validated first: nothing is launched when
+  // either part would fail
+  int st = bw_run(x, y, grad_out, grad_weight, grad_bias, workspace_w, workspace_w_bytes, n, c, h,
+                  w, kernel_size, d0, d1, d2, dtype, stream, true, nullptr);
+  if (st != kOk) return st;
+  BxFinish fin{nullptr, nullptr, nullptr, TileGeom{}, 0, 1};
+  st = bx_run(y, weight, bias, grad_out, grad_x, workspace_x, workspace_x_bytes, n, c, h, w,
+              kernel_size, d0, d1, d2, dtype, stream, &fin);
+  if (st != kOk || fin.part == nullptr) return st;  // fin stays empty for empty shapes
+  return bw_run(x, y, grad_out, grad_weight, grad_bias, workspace_w, workspace_w_bytes, n, c, h, w,
+                kernel_size, d0, d1, d2, dtype, stream, false, &fin);
 }

@@ -22,7 +22,7 @@
 //      order, so the result is deterministic; 4 columns per thread, every
 //      access 16 bytes wide (8 for 2-byte dX) when W % 4 == 0.
 
-#include "gen_tile.h"
+#include "gen_bwd_x.h"
 #include <type_traits>
 
 namespace ddpm {
@@ -34,64 +34,12 @@ __global__ __launch_bounds__(kGtThreads) __attribute__((amdgpu_waves_per_eu(gt_w
   gen_tile_body<T, KS, NK, CB, true>(gout, y, wt, bias, nullptr, part, g);
 }
 
-// VEC consecutive columns of one row of dX per thread (VEC = 4 needs W % 4
-// == 0: 16-byte aligned partial groups, as the tile kernel lays them out).
-// The halo of at most one vertical and one horizontal neighbour covers a
-// pixel (R <= 8 is at most half a tile side), so the sum is gO_x + own +
-// vertical + horizontal + diagonal partial, in that order.
+// One thread per item (bx_reduce_item: VEC columns of one row of dX).
 template <typename T, int VEC>
 __global__ __launch_bounds__(256) void gen_bwd_x_reduce_kernel(const float* __restrict__ part,
                                                                const T* __restrict__ gout,
                                                                T* __restrict__ gx, TileGeom g) {
-  typedef float FV __attribute__((ext_vector_type(4)));
-  typedef T TV __attribute__((ext_vector_type(4)));
-  // one thread per (row, group of VEC columns), flattened over all rows so
-  // that every lane has work (a block per row left 3 of 4 waves idle at
-  // W = 256)
-  const int gpr = (g.W + VEC - 1) / VEC;  // column groups per row
-  const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t rows = (int64_t)g.N * g.C * g.H;
-  if (item >= rows * gpr) return;
-  const int row = (int)(item / gpr);      // (n*C + c)*H + h
-  const int gi = (int)(item - (int64_t)row * gpr);
-  const int w = gi * VEC;
-  const int nc = row / g.H, h = row - nc * g.H;
-  const int n = nc / g.C, c = nc - n * g.C;
-  const int cb = c >> 4, ch = c & 15;
-  const int ty = h / kGtTH, lr = h - ty * kGtTH;
-  const int tx = w / g.TW, lc = w - tx * g.TW;
-  const int tiles_h = g.tiles / g.tiles_w;
-  int dy = lr < g.R ? -1 : (lr >= kGtTH - g.R ? 1 : 0);
-  if (ty + dy < 0 || ty + dy >= tiles_h) dy = 0;
-  int dx = lc < g.R ? -1 : (lc + VEC - 1 >= g.TW - g.R ? 1 : 0);
-  if (tx + dx < 0 || tx + dx >= g.tiles_w) dx = 0;
-  const int64_t LHp = (int64_t)g.LH * g.LWp;
-  auto at = [&](int ddy, int ddx) {
-    const int64_t wg = ((int64_t)n * g.tiles + (ty + ddy) * g.tiles_w + tx + ddx) * g.cblocks + cb;
-    return part + (wg * 16 + ch) * LHp + (lr + g.R - ddy * kGtTH) * g.LWp +
-           (lc + g.R + g.pad - ddx * g.TW);
-  };
-  const int64_t HW = (int64_t)g.H * g.W;
-  const int64_t pix = (int64_t)h * g.W + w;
-  const T* __restrict__ go = gout + ((int64_t)n * 4 * g.C + c) * HW + pix;
-  T* __restrict__ dst = gx + (int64_t)nc * HW + pix;
-  if constexpr (VEC == 4) {
-    const TV gv = *reinterpret_cast<const TV*>(go);
-    FV s = {to_f(gv[0]), to_f(gv[1]), to_f(gv[2]), to_f(gv[3])};
-    s += *reinterpret_cast<const FV*>(at(0, 0));
-    if (dy != 0) s += *reinterpret_cast<const FV*>(at(dy, 0));
-    if (dx != 0) s += *reinterpret_cast<const FV*>(at(0, dx));
-    if (dy != 0 && dx != 0) s += *reinterpret_cast<const FV*>(at(dy, dx));
-    const TV o = {from_f<T>(s[0]), from_f<T>(s[1]), from_f<T>(s[2]), from_f<T>(s[3])};
-    *reinterpret_cast<TV*>(dst) = o;
-  } else {
-    float s = to_f(go[0]);
-    s += *at(0, 0);
-    if (dy != 0) s += *at(dy, 0);
-    if (dx != 0) s += *at(0, dx);
-    if (dy != 0 && dx != 0) s += *at(dy, dx);
-    dst[0] = from_f<T>(s);
-  }
+  bx_reduce_item<T, VEC>(part, gout, gx, g, (int64_t)blockIdx.x * 256 + threadIdx.x);
 }
 
 namespace {
@@ -138,11 +86,24 @@ extern "C" int64_t ddpm_gen_bwd_x_workspace_bytes(int64_t n, int64_t c, int64_t 
   return bx_part_bytes(g);
 }
 
-extern "C" int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bias,
-                              const void* grad_out, void* grad_x, void* workspace,
-                              int64_t workspace_bytes, int64_t n, int64_t c, int64_t h, int64_t w,
-                              int kernel_size, int d0, int d1, int d2, int dtype,
-                              hipStream_t stream) {
+int ddpm::bx_finish(const BxFinish& f, int dtype, hipStream_t stream) {
+  return xt_with_type(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    const dim3 rgrid((unsigned)((f.items + 255) / 256));
+    if (f.vec == 4)
+      hipLaunchKernelGGL((gen_bwd_x_reduce_kernel<T, 4>), rgrid, dim3(256), 0, stream, f.part,
+                         (const T*)f.gout, (T*)f.gx, f.g);
+    else
+      hipLaunchKernelGGL((gen_bwd_x_reduce_kernel<T, 1>), rgrid, dim3(256), 0, stream, f.part,
+                         (const T*)f.gout, (T*)f.gx, f.g);
+    return (int)hipGetLastError();
+  });
+}
+
+int ddpm::bx_run(const void* y, const void* weight, const void* bias, const void* grad_out,
+                 void* grad_x, void* workspace, int64_t workspace_bytes, int64_t n, int64_t c,
+                 int64_t h, int64_t w, int kernel_size, int d0, int d1, int d2, int dtype,
+                 hipStream_t stream, BxFinish* defer) {
   if (dtype < kF32 || dtype > kF16) return kBadArgument;
   GenGeom gg;
   int st = gen_make_geom(gg, n, c, h, w, kernel_size, d0, d1, d2);
@@ -175,14 +136,12 @@ extern "C" int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bia
                          (const T*)weight, (const T*)bias, part, g);
       int e = (int)hipGetLastError();
       if (e != 0) return e;
-      const dim3 rgrid((unsigned)((ritems + 255) / 256));
-      if (vec == 4)
-        hipLaunchKernelGGL((gen_bwd_x_reduce_kernel<T, 4>), rgrid, dim3(256), 0, stream,
-                           (const float*)part, (const T*)grad_out, (T*)grad_x, g);
-      else
-        hipLaunchKernelGGL((gen_bwd_x_reduce_kernel<T, 1>), rgrid, dim3(256), 0, stream,
-                           (const float*)part, (const T*)grad_out, (T*)grad_x, g);
-      return (int)hipGetLastError();
+      const BxFinish fin{part, grad_out, grad_x, g, ritems, vec};
+      if (defer) {
+        *defer = fin;
+        return (int)kOk;
+      }
+      return bx_finish(fin, dtype, stream);
     };
     // 1 or 2 chunks of 32 input channels, or 4 (65..128 channels, always
     // 32-column tiles; chunks past C read zeros)
@@ -201,4 +160,13 @@ extern "C" int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bia
     if (kernel_size == 1) return pick(std::integral_constant<int, 1>());
     return pick(std::integral_constant<int, 3>());
   });
+}
+
+extern "C" int ddpm_gen_bwd_x(const void* y, const void* weight, const void* bias,
+                              const void* grad_out, void* grad_x, void* workspace,
+                              int64_t workspace_bytes, int64_t n, int64_t c, int64_t h, int64_t w,
+                              int kernel_size, int d0, int d1, int d2, int dtype,
+                              hipStream_t stream) {
+  return bx_run(y, weight, bias, grad_out, grad_x, workspace, workspace_bytes, n, c, h, w,
+                kernel_size, d0, d1, d2, dtype, stream, nullptr);
 }

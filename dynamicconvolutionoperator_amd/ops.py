@@ -244,18 +244,49 @@ class _GeneratorDynamicCat(torch.autograd.Function):
         dt = _dt(x)
         stream = _stream(x)
         grad_x = grad_y = grad_w = grad_b = None
+        need_x = ctx.needs_input_grad[0]
+        need_wb = ctx.needs_input_grad[2] or ctx.needs_input_grad[3]
         with _on(x.device):
-            if ctx.needs_input_grad[0]:
+            if need_x:
                 grad_x = torch.empty_like(x)
                 wsx_bytes = _ws_bytes("ddpm_gen_bwd_x_workspace_bytes", n, c, h, w, k, *dil)
                 wsx = torch.empty(wsx_bytes, dtype=torch.uint8, device=x.device)
+            if need_wb:
+                grad_w = torch.empty_like(weight)
+                grad_b = torch.empty_like(bias)
+                ws_bytes = _ws_bytes("ddpm_gen_bwd_w_workspace_bytes", n, c, h, w, k, dt)
+                ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+            if need_x and need_wb:
+                # one call: dX's halo reduction runs on the CUs dW leaves free
+                _lib.check(
+                    lib.ddpm_gen_bwd_xw(_ptr(x), _ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
+                                        _ptr(grad_x), _ptr(grad_w), _ptr(grad_b), _ptr(wsx),
+                                        wsx_bytes, _ptr(ws), ws_bytes, n, c, h, w, k, *dil, dt,
+                                        stream),
+                    "ddpm_gen_bwd_xw",
+                )
+            elif need_x:
                 _lib.check(
                     lib.ddpm_gen_bwd_x(_ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
                                        _ptr(grad_x), _ptr(wsx), wsx_bytes, n, c, h, w, k, *dil,
                                        dt, stream),
                     "ddpm_gen_bwd_x",
                 )
+            elif need_wb:
+                _lib.check(
+                    lib.ddpm_gen_bwd_w(_ptr(x), _ptr(y), _ptr(grad_out), _ptr(grad_w),
+                                       _ptr(grad_b), _ptr(ws), ws_bytes, n, c, h, w, k, *dil, dt,
+                                       stream),
+                    "ddpm_gen_bwd_w",
+                )
+            if need_x:
                 del wsx
+            if need_wb:
+                del ws
+                if not ctx.needs_input_grad[2]:
+                    grad_w = None
+                if not ctx.needs_input_grad[3]:
+                    grad_b = None
             if ctx.needs_input_grad[1]:
                 grad_y = torch.empty_like(y)
                 wsy_bytes = _ws_bytes("ddpm_gen_bwd_y_workspace_bytes", c, k)
@@ -265,21 +296,6 @@ class _GeneratorDynamicCat(torch.autograd.Function):
                                        _ptr(wsy), wsy_bytes, n, c, h, w, k, *dil, dt, stream),
                     "ddpm_gen_bwd_y",
                 )
-            if ctx.needs_input_grad[2] or ctx.needs_input_grad[3]:
-                grad_w = torch.empty_like(weight)
-                grad_b = torch.empty_like(bias)
-                ws_bytes = _ws_bytes("ddpm_gen_bwd_w_workspace_bytes", n, c, h, w, k, dt)
-                ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
-                _lib.check(
-                    lib.ddpm_gen_bwd_w(_ptr(x), _ptr(y), _ptr(grad_out), _ptr(grad_w),
-                                       _ptr(grad_b), _ptr(ws), ws_bytes, n, c, h, w, k, *dil, dt,
-                                       stream),
-                    "ddpm_gen_bwd_w",
-                )
-                if not ctx.needs_input_grad[2]:
-                    grad_w = None
-                if not ctx.needs_input_grad[3]:
-                    grad_b = None
         return grad_x, grad_y, grad_w, grad_b, None, None
 
 

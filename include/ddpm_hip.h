@@ -38,7 +38,7 @@ extern "C" {
 #define DDPM_DTYPE_BF16 1
 #define DDPM_DTYPE_F16 2
 
-/* ABI version of this header (3). */
+/* ABI version of this header (4). */
 int ddpm_abi_version(void);
 
 /* Text for any status code returned by this library (static storage). */
@@ -198,6 +198,23 @@ int ddpm_gen_bwd_w(const void* x, const void* y, const void* grad_out, void* gra
                    void* grad_bias, void* workspace, int64_t workspace_bytes, int64_t n, int64_t c,
                    int64_t h, int64_t w, int kernel_size, int d0, int d1, int d2, int dtype,
                    hipStream_t stream);
+
+/* ddpm_gen_bwd_x and ddpm_gen_bwd_w in one call, with the same results bit
+ * for bit: the input gradient's tile kernel runs first, and its halo
+ * reduction then runs on the CUs the weight gradient's workgroups leave free
+ * (at most 16 splits x 3 branches x the 16-channel blocks: 192 of 256 CUs at
+ * C = 64), as extra workgroups of the weight-gradient launch, instead of as a
+ * kernel of its own (a separate kernel where fewer than a quarter of the CUs
+ * are free).  workspace_x / workspace_w as for the two calls; both are
+ * validated before anything is launched.
+ * Replaces the _generator_dynamic_cat_bwd_x launch and the weight-gradient
+ * launches of _GeneratorDynamicCat.backward (_triton_kernels.py:944-961,
+ * 973-1053) when both gradients are needed. */
+int ddpm_gen_bwd_xw(const void* x, const void* y, const void* weight, const void* bias,
+                    const void* grad_out, void* grad_x, void* grad_weight, void* grad_bias,
+                    void* workspace_x, int64_t workspace_x_bytes, void* workspace_w,
+                    int64_t workspace_w_bytes, int64_t n, int64_t c, int64_t h, int64_t w,
+                    int kernel_size, int d0, int d1, int d2, int dtype, hipStream_t stream);
 
 /* ---- the 3x3 fuse convolution (Conv2d(4C -> C, 3, padding 1)) -------- */
 
