@@ -258,6 +258,8 @@ def work_per_launch(name, esize):
         "ddpm_gen_bwd_w": ((5 * E) * esize + G * (C + 1) * esize, gemm),  # x, y, gO branches in
         # dX and dW/db in one call: x, y, gO (4E) in, dX out, W/b in, dW/db out; both GEMMs
         "ddpm_gen_bwd_xw": ((7 * E + 2 * G * (C + 1)) * esize, 2 * gemm),
+        # all four gradients in one call: as above plus dY out; three GEMMs
+        "ddpm_gen_bwd": ((8 * E + 2 * G * (C + 1)) * esize, 3 * gemm),
         # the 3x3 fuse convolution 4C -> C: GEMMs of 2*N*H*W*C*4C*9 flops
         "ddpm_fuse_conv_fwd": ((5 * E + 36 * C * C) * esize, conv),  # cat (4E) in, out (E)
         "ddpm_fuse_conv_bwd_data": ((5 * E + 36 * C * C) * esize, conv),  # gO (E) in, d cat (4E)
@@ -527,6 +529,8 @@ def make_calls(lib, dt, k, hw, nsets):
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
     wsxb = max(int(lib.ddpm_gen_bwd_x_workspace_bytes(B, C, hw, hw, k, *DIL)), 1)
     wsx = torch.empty(wsxb, dtype=torch.uint8, device="cuda")
+    wsyb = max(int(lib.ddpm_gen_bwd_y_workspace_bytes(C, k)), 1)
+    wsy = torch.empty(wsyb, dtype=torch.uint8, device="cuda")
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -543,6 +547,9 @@ def make_calls(lib, dt, k, hw, nsets):
         "ddpm_gen_bwd_xw": lambda t: lib.ddpm_gen_bwd_xw(ptr(t["x"]), ptr(t["y"]), ptr(wt), ptr(bs),
                                                          ptr(t["go"]), ptr(dx), ptr(dw), ptr(db), ptr(wsx),
                                                          wsxb, ptr(ws), wsb, *shp, code, s),
+        "ddpm_gen_bwd": lambda t: lib.ddpm_gen_bwd(ptr(t["x"]), ptr(t["y"]), ptr(wt), ptr(bs), ptr(t["go"]),
+                                                   ptr(dx), ptr(dy), ptr(dw), ptr(db), ptr(wsx), wsxb,
+                                                   ptr(wsy), wsyb, ptr(ws), wsb, *shp, code, s),
         # the generator 1x1 convolution of the materialized route writes the kernel tensor
         "ddpm_gen_kernels": lambda t: lib.ddpm_gen_kernels(ptr(t["y"]), ptr(wt), ptr(bs), ptr(t["kern"]), B, C,
                                                            hw, hw, k, code, s),
@@ -688,14 +695,17 @@ def main():
     timer = LaunchTimer(lib, entries)
     kernels = kernel_breakdown(lib, timer, module, x, y)
     cands = {n: v["share_of_step_ms"] for n, v in kernels.items()}
-    if "ddpm_gen_bwd_xw" in cands:
-        # the step runs dX and dW as one call (dX's halo reduction on the CUs
-        # dW leaves free): the roofline takes its two GEMM entry points timed
-        # alone at the same shape
-        alone = standalone_ms(lib, ("ddpm_gen_bwd_x", "ddpm_gen_bwd_w"), torch.float32)
-        extra["standalone_fp32_ms"] = alone
-        cands.pop("ddpm_gen_bwd_xw")
-        cands.update(alone)
+    combined = {"ddpm_gen_bwd": ("ddpm_gen_bwd_x", "ddpm_gen_bwd_y", "ddpm_gen_bwd_w"),
+                "ddpm_gen_bwd_xw": ("ddpm_gen_bwd_x", "ddpm_gen_bwd_w")}
+    for name, parts in combined.items():
+        if name in cands:
+            # the step runs these GEMMs as one call (small pieces of them on
+            # the CUs dW leaves free): the roofline takes its GEMM entry points
+            # timed alone at the same shape
+            alone = standalone_ms(lib, parts, torch.float32)
+            extra["standalone_fp32_ms"] = alone
+            cands.pop(name)
+            cands.update(alone)
     dominant = max(cands, key=cands.get)
     nbytes, flops = work_per_launch(dominant, 4)
     dom_ms = cands[dominant]

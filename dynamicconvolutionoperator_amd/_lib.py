@@ -52,6 +52,8 @@ SIGNATURES: dict[str, tuple[list, type]] = {
     "ddpm_gen_bwd_w": ([_P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
     "ddpm_gen_bwd_xw": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _P, _L, _L, _L, _L, _L, _I, _I, _I,
                          _I, _I, _P], _I),
+    "ddpm_gen_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _P, _L, _P, _L, _L, _L, _L, _L, _I,
+                      _I, _I, _I, _I, _P], _I),
 }
 
 

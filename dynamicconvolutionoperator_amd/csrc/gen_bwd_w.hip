@@ -31,7 +31,7 @@
 // writes their split to LDS after the step's MFMAs (no pre-pass over y, no
 // workspace planes), so every B fragment is a plain 16-byte LDS read.
 
-#include "gen_bwd_x.h"
+#include "gen_bwd.h"
 #include <type_traits>
 
 namespace ddpm {
@@ -158,15 +158,17 @@ __global__ __launch_bounds__(256) void gen_ysplit_kernel(const float* __restrict
   }
 }
 
-// Workgroups past g.dw_blocks (ddpm_gen_bwd_xw) are helpers: with at most 16
-// splits x 3 branches x the channel blocks, the weight gradient leaves CUs
-// free (64 of 256 at C = 64), and the helpers run the input gradient's halo
-// reduction (`fin`) there, alongside, instead of as a kernel of its own.
+// Workgroups past g.dw_blocks (ddpm_gen_bwd_xw, ddpm_gen_bwd) are helpers:
+// with at most 16 splits x 3 branches x the channel blocks, the weight
+// gradient leaves CUs free (64 of 256 at C = 64), and the helpers run the dY
+// kernel's weight packing (`yp`, none when yp.total is 0) and the input
+// gradient's halo reduction (`fin`) there, alongside, instead of as kernels of
+// their own.
 template <typename T, int KS, int MB>
 __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_partial_kernel(
     const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ gout,
     float* __restrict__ pw, float* __restrict__ pb, T* __restrict__ dw_out, T* __restrict__ db_out,
-    WGradGeom g, BxFinish fin) {
+    WGradGeom g, BxFinish fin, YPack yp) {
   typedef Mma<T> M;
   typedef typename M::V V;
   typedef typename M::E ME;
@@ -194,6 +196,9 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
     // halo reduction, grid-strided over the helpers
     const int64_t stride = (int64_t)(gridDim.x - g.dw_blocks) * NT;
     const int64_t first = (int64_t)(blockIdx.x - g.dw_blocks) * NT + threadIdx.x;
+    const T* __restrict__ ywt = static_cast<const T*>(yp.wt);
+    for (int64_t it = first; it < yp.total; it += stride)
+      yt_pack_item<T, KS, MB>(ywt, yp.pk, yp.C, yp.nc32, (int)it);
     const T* __restrict__ fgo = static_cast<const T*>(fin.gout);
     T* __restrict__ fgx = static_cast<T*>(fin.gx);
     if (fin.vec == 4) {
@@ -825,7 +830,7 @@ int wg_helpers(int dw_blocks) {
 int bw_run(const void* x, const void* y, const void* grad_out, void* grad_weight,
            void* grad_bias, void* workspace, int64_t workspace_bytes, int64_t n, int64_t c,
            int64_t h, int64_t w, int kernel_size, int d0, int d1, int d2, int dtype,
-           hipStream_t stream, bool check_only, const BxFinish* fin) {
+           hipStream_t stream, bool check_only, const BxFinish* fin, const YPack* yp = nullptr) {
   if (dtype < kF32 || dtype > kF16) return kBadArgument;
   GenGeom gg;
   int st = gen_make_geom(gg, n, c, h, w, kernel_size, d0, d1, d2);
@@ -854,8 +859,13 @@ int bw_run(const void* x, const void* y, const void* grad_out, void* grad_weight
   if (kernel_size != 1 && kernel_size != 3) return kUnsupported;
   if (check_only) return kOk;
   g.dw_blocks = g.splits * 3 * g.cblocks * g.ihalves;
-  const int helpers = fin ? wg_helpers(g.dw_blocks) : 0;
+  const int helpers = (fin || yp) ? wg_helpers(g.dw_blocks) : 0;
   const BxFinish none{nullptr, nullptr, nullptr, TileGeom{}, 0, 1};
+  const YPack nopack{nullptr, nullptr, 0, 0, 0};
+  if (yp && helpers == 0) {
+    const int e = yt_pack(*yp, kernel_size, dtype, stream);
+    if (e != 0) return e;
+  }
   float* pw = g.direct ? nullptr : (float*)workspace;
   float* pb = g.direct ? nullptr : pw + (int64_t)g.splits * 3 * kk * c * c;
   return wg_with_type(dtype, [&](auto tag) {
@@ -875,7 +885,7 @@ int bw_run(const void* x, const void* y, const void* grad_out, void* grad_weight
       hipLaunchKernelGGL((gen_bwd_w_partial_kernel<T, KS, MB>), grid,
                          dim3(64 * kWgSegs * WgTaps<KS>::kGroups), lds, stream, (const T*)x,
                          (const T*)y, (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g,
-                         helpers > 0 ? *fin : none);
+                         helpers > 0 && fin ? *fin : none, helpers > 0 && yp ? *yp : nopack);
       int e = (int)hipGetLastError();
       if (e == 0 && fin && helpers == 0) e = bx_finish(*fin, dtype, stream);
       if (e != 0 || g.direct) return e;
@@ -932,4 +942,32 @@ extern "C" int ddpm_gen_bwd_xw(const void* x, const void* y, const void* weight,
   if (st != kOk || fin.part == nullptr) return st;  // fin stays empty for empty shapes
   return bw_run(x, y, grad_out, grad_weight, grad_bias, workspace_w, workspace_w_bytes, n, c, h, w,
                 kernel_size, d0, d1, d2, dtype, stream, false, &fin);
+}
+
+extern "C" int ddpm_gen_bwd(const void* x, const void* y, const void* weight, const void* bias,
+                            const void* grad_out, void* grad_x, void* grad_y, void* grad_weight,
+                            void* grad_bias, void* workspace_x, int64_t workspace_x_bytes,
+                            void* workspace_y, int64_t workspace_y_bytes, void* workspace_w,
+                            int64_t workspace_w_bytes, int64_t n, int64_t c, int64_t h, int64_t w,
+                            int kernel_size, int d0, int d1, int d2, int dtype,
+                            hipStream_t stream) {
+  // the weight- and y-gradient parts are validated first (the x part on its
+  // launch): nothing is launched when any part would fail
+  int st = bw_run(x, y, grad_out, grad_weight, grad_bias, workspace_w, workspace_w_bytes, n, c, h,
+                  w, kernel_size, d0, d1, d2, dtype, stream, true, nullptr);
+  if (st != kOk) return st;
+  YPack yp{nullptr, nullptr, 0, 0, 0};
+  st = yt_run(x, weight, grad_out, grad_y, workspace_y, workspace_y_bytes, n, c, h, w, kernel_size,
+              d0, d1, d2, dtype, stream, kYtCheck, &yp);
+  if (st != kOk || yp.total == 0) return st;  // total 0: empty shape
+  BxFinish fin{nullptr, nullptr, nullptr, TileGeom{}, 0, 1};
+  st = bx_run(y, weight, bias, grad_out, grad_x, workspace_x, workspace_x_bytes, n, c, h, w,
+              kernel_size, d0, d1, d2, dtype, stream, &fin);
+  if (st != kOk || fin.part == nullptr) return st;
+  // dW and dW's split reduction; its helpers pack dY's weight and finish dX
+  st = bw_run(x, y, grad_out, grad_weight, grad_bias, workspace_w, workspace_w_bytes, n, c, h, w,
+              kernel_size, d0, d1, d2, dtype, stream, false, &fin, &yp);
+  if (st != kOk) return st;
+  return yt_run(x, weight, grad_out, grad_y, workspace_y, workspace_y_bytes, n, c, h, w,
+                kernel_size, d0, d1, d2, dtype, stream, kYtMain, nullptr);
 }

@@ -27,7 +27,7 @@
 //   * v_mfma_f32_16x16x32_{bf16,f16}; fp32 operands run as three bf16
 //     products (hi*hi + hi*lo + lo*hi).
 
-#include "gen_common.h"
+#include "gen_bwd.h"
 
 #include <atomic>
 #include <mutex>
@@ -51,47 +51,12 @@ struct YGeom {
   int x4;         // x rows can be copied in 16-byte lanes (W % 8 == 0, aligned base)
 };
 
-// Packed weight for the A fragments: 16-byte units
-//   [ih][b][cc][t][ib][part][lane]   lane (i = (ih*MB + ib)*16 + (lane & 15),
-//   q = lane >> 4) holding W[(b*C + c)*KK + t][i] for c = cc*32 + 4*e + q,
-//   e = 0..7 (ih: the output-channel half of a workgroup; ib < MB).
-template <typename T>
-__host__ __device__ constexpr int yt_parts() {
-  return sizeof(T) == 4 ? 2 : 1;
-}
-
 template <typename T, int KS, int MB>
 __global__ __launch_bounds__(256) void gen_pack_wt_kernel(const T* __restrict__ wt,
                                                           uint32_t* __restrict__ pk, int C,
-                                                          int nc32, int ihalves) {
-  constexpr int KK = KS * KS;
-  constexpr int P = yt_parts<T>();
-  const int total = ihalves * 3 * nc32 * KK * MB * 64;
+                                                          int nc32, int total) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total) return;
-  const int lane = idx & 63;
-  int rest = idx >> 6;
-  const int ib = rest % MB;
-  rest /= MB;
-  const int t = rest % KK;
-  rest /= KK;
-  const int cc = rest % nc32;
-  rest /= nc32;
-  const int b = rest % 3;
-  const int ih = rest / 3;
-  const int i = (ih * MB + ib) * 16 + (lane & 15), q = lane >> 4;
-  float v[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int c = cc * 32 + 4 * e + q;
-    v[e] = (i < C && c < C) ? to_f(wt[((int64_t)(b * C + c) * KK + t) * C + i]) : 0.f;
-  }
-  typename Mma<T>::V o[P];
-  Mma<T>::pack(v, o);
-  u32x4* __restrict__ dst = reinterpret_cast<u32x4*>(pk);
-  const int64_t unit = (((((int64_t)ih * 3 + b) * nc32 + cc) * KK + t) * MB + ib) * P * 64 + lane;
-#pragma unroll
-  for (int part = 0; part < P; ++part) dst[unit + part * 64] = __builtin_bit_cast(u32x4, o[part]);
+  if (idx < total) yt_pack_item<T, KS, MB>(wt, pk, C, nc32, idx);
 }
 
 // One LDS staging buffer (dwords): x rows [32 channels][kXS] then the
@@ -360,7 +325,7 @@ int yt_check(const void* x, const void* weight, const void* grad_out, void* grad
 // already validated by yt_check; `packed` holds yt_pack_bytes bytes).
 int yt_launch(const void* x, const void* weight, const void* grad_out, void* grad_y, void* packed,
               int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size, const GenGeom& gg,
-              int dtype, hipStream_t stream);
+              int dtype, hipStream_t stream, bool pack = true);
 
 }  // namespace
 
@@ -409,19 +374,56 @@ extern "C" int64_t ddpm_gen_bwd_y_workspace_bytes(int64_t c, int kernel_size) {
   return yt_pack_bytes(c, kernel_size, kF32);
 }
 
-extern "C" int ddpm_gen_bwd_y(const void* x, const void* weight, const void* grad_out,
-                              void* grad_y, void* workspace, int64_t workspace_bytes, int64_t n,
-                              int64_t c, int64_t h, int64_t w, int kernel_size, int d0, int d1,
-                              int d2, int dtype, hipStream_t stream) {
+int ddpm::yt_run(const void* x, const void* weight, const void* grad_out, void* grad_y,
+                 void* workspace, int64_t workspace_bytes, int64_t n, int64_t c, int64_t h,
+                 int64_t w, int kernel_size, int d0, int d1, int d2, int dtype, hipStream_t stream,
+                 int mode, YPack* pack) {
   GenGeom gg;
   bool empty;
   const int st =
       yt_check(x, weight, grad_out, grad_y, n, c, h, w, kernel_size, d0, d1, d2, dtype, gg, empty);
+  if (pack) *pack = YPack{weight, (uint32_t*)workspace, (int)c, (int)((c + 31) / 32), 0};
   if (st != kOk || empty) return st;
   const int64_t need = yt_pack_bytes(c, kernel_size, dtype);
   if (!workspace || workspace_bytes < need) return kWorkspaceTooSmall;
+  if (kernel_size != 1 && kernel_size != 3) return kUnsupported;
+  if (mode == kYtCheck) {
+    if (pack) {
+      int ih, mb;
+      yt_split(c, ih, mb);
+      pack->total = ih * 3 * pack->nc32 * kernel_size * kernel_size * mb * 64;
+    }
+    return kOk;
+  }
   return yt_launch(x, weight, grad_out, grad_y, workspace, n, c, h, w, kernel_size, gg, dtype,
-                   stream);
+                   stream, mode != kYtMain);
+}
+
+int ddpm::yt_pack(const YPack& p, int kernel_size, int dtype, hipStream_t stream) {
+  int ih, mb;
+  yt_split(p.C, ih, mb);
+  return yt_with_type(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    return yt_with_mb(mb, [&](auto mbc) {
+      constexpr int MB = decltype(mbc)::value;
+      const dim3 grid((unsigned)((p.total + 255) / 256));
+      if (kernel_size == 1)
+        hipLaunchKernelGGL((gen_pack_wt_kernel<T, 1, MB>), grid, dim3(256), 0, stream,
+                           (const T*)p.wt, p.pk, p.C, p.nc32, p.total);
+      else
+        hipLaunchKernelGGL((gen_pack_wt_kernel<T, 3, MB>), grid, dim3(256), 0, stream,
+                           (const T*)p.wt, p.pk, p.C, p.nc32, p.total);
+      return (int)hipGetLastError();
+    });
+  });
+}
+
+extern "C" int ddpm_gen_bwd_y(const void* x, const void* weight, const void* grad_out,
+                              void* grad_y, void* workspace, int64_t workspace_bytes, int64_t n,
+                              int64_t c, int64_t h, int64_t w, int kernel_size, int d0, int d1,
+                              int d2, int dtype, hipStream_t stream) {
+  return yt_run(x, weight, grad_out, grad_y, workspace, workspace_bytes, n, c, h, w, kernel_size,
+                d0, d1, d2, dtype, stream, kYtFull, nullptr);
 }
 
 extern "C" int ddpm_gen_bwd_y_noalloc(const void* x, const void* weight, const void* grad_out,
@@ -447,7 +449,7 @@ namespace {
 
 int yt_launch(const void* x, const void* weight, const void* grad_out, void* grad_y, void* packed,
               int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size, const GenGeom& gg,
-              int dtype, hipStream_t stream) {
+              int dtype, hipStream_t stream, bool pack) {
   void* workspace = packed;
   YGeom g;
   g.N = (int)n;
@@ -470,12 +472,14 @@ int yt_launch(const void* x, const void* weight, const void* grad_out, void* gra
       auto launch = [&](auto ks) {
         constexpr int KS = decltype(ks)::value;
         typedef YtLds<T, KS, MB> L;
-        const int units = g.ihalves * 3 * g.nc32 * KS * KS * MB * 64;
-        hipLaunchKernelGGL((gen_pack_wt_kernel<T, KS, MB>), dim3((units + 255) / 256), dim3(256), 0,
-                           stream, (const T*)weight, (uint32_t*)workspace, (int)c, g.nc32,
-                           g.ihalves);
-        int e = (int)hipGetLastError();
-        if (e != 0) return e;
+        if (pack) {
+          const int units = g.ihalves * 3 * g.nc32 * KS * KS * MB * 64;
+          hipLaunchKernelGGL((gen_pack_wt_kernel<T, KS, MB>), dim3((units + 255) / 256), dim3(256),
+                             0, stream, (const T*)weight, (uint32_t*)workspace, (int)c, g.nc32,
+                             units);
+          int e = (int)hipGetLastError();
+          if (e != 0) return e;
+        }
         const size_t lds = (size_t)2 * L::kBuf * 4;
         const int ae =
             allow_dynamic_lds(reinterpret_cast<const void*>(&gen_bwd_y_kernel<T, KS, MB>), lds);

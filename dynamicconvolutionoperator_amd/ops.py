@@ -245,6 +245,7 @@ class _GeneratorDynamicCat(torch.autograd.Function):
         stream = _stream(x)
         grad_x = grad_y = grad_w = grad_b = None
         need_x = ctx.needs_input_grad[0]
+        need_y = ctx.needs_input_grad[1]
         need_wb = ctx.needs_input_grad[2] or ctx.needs_input_grad[3]
         with _on(x.device):
             if need_x:
@@ -256,7 +257,23 @@ class _GeneratorDynamicCat(torch.autograd.Function):
                 grad_b = torch.empty_like(bias)
                 ws_bytes = _ws_bytes("ddpm_gen_bwd_w_workspace_bytes", n, c, h, w, k, dt)
                 ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
-            if need_x and need_wb:
+            if need_y:
+                grad_y = torch.empty_like(y)
+                wsy_bytes = _ws_bytes("ddpm_gen_bwd_y_workspace_bytes", c, k)
+                wsy = torch.empty(wsy_bytes, dtype=torch.uint8, device=x.device)
+            y_pending = need_y
+            if need_x and need_y and need_wb:
+                # one call: dY's weight packing and dX's halo reduction run on
+                # the CUs dW leaves free
+                _lib.check(
+                    lib.ddpm_gen_bwd(_ptr(x), _ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
+                                     _ptr(grad_x), _ptr(grad_y), _ptr(grad_w), _ptr(grad_b),
+                                     _ptr(wsx), wsx_bytes, _ptr(wsy), wsy_bytes, _ptr(ws), ws_bytes,
+                                     n, c, h, w, k, *dil, dt, stream),
+                    "ddpm_gen_bwd",
+                )
+                y_pending = False
+            elif need_x and need_wb:
                 # one call: dX's halo reduction runs on the CUs dW leaves free
                 _lib.check(
                     lib.ddpm_gen_bwd_xw(_ptr(x), _ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
@@ -287,10 +304,7 @@ class _GeneratorDynamicCat(torch.autograd.Function):
                     grad_w = None
                 if not ctx.needs_input_grad[3]:
                     grad_b = None
-            if ctx.needs_input_grad[1]:
-                grad_y = torch.empty_like(y)
-                wsy_bytes = _ws_bytes("ddpm_gen_bwd_y_workspace_bytes", c, k)
-                wsy = torch.empty(wsy_bytes, dtype=torch.uint8, device=x.device)
+            if y_pending:
                 _lib.check(
                     lib.ddpm_gen_bwd_y(_ptr(x), _ptr(weight), _ptr(grad_out), _ptr(grad_y),
                                        _ptr(wsy), wsy_bytes, n, c, h, w, k, *dil, dt, stream),

@@ -216,6 +216,22 @@ int ddpm_gen_bwd_xw(const void* x, const void* y, const void* weight, const void
                     int64_t workspace_w_bytes, int64_t n, int64_t c, int64_t h, int64_t w,
                     int kernel_size, int d0, int d1, int d2, int dtype, hipStream_t stream);
 
+/* All four gradients of the fused op in one call (ddpm_gen_bwd_x, _bwd_y and
+ * _bwd_w), bit-identical to the three calls: the dX tile kernel, then the
+ * weight-gradient launch whose helper workgroups (on the CUs its own grid
+ * leaves free) pack the dY kernel's weight and run dX's halo reduction, the
+ * split reduction, and the dY kernel.  The three workspaces as for the
+ * separate calls (workspace_y: ddpm_gen_bwd_y_workspace_bytes); all parts are
+ * validated before anything is launched.
+ * Replaces the three kernel launches of _GeneratorDynamicCat.backward
+ * (_triton_kernels.py:944-1053). */
+int ddpm_gen_bwd(const void* x, const void* y, const void* weight, const void* bias,
+                 const void* grad_out, void* grad_x, void* grad_y, void* grad_weight,
+                 void* grad_bias, void* workspace_x, int64_t workspace_x_bytes, void* workspace_y,
+                 int64_t workspace_y_bytes, void* workspace_w, int64_t workspace_w_bytes,
+                 int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size, int d0, int d1,
+                 int d2, int dtype, hipStream_t stream);
+
 /* ---- the 3x3 fuse convolution (Conv2d(4C -> C, 3, padding 1)) -------- */
 
 /* Bytes of workspace ddpm_fuse_conv_fwd / _bwd_data need at this shape: the

@@ -1,14 +1,17 @@
-"""ddpm_gen_bwd_xw against ddpm_gen_bwd_x + ddpm_gen_bwd_w, through the C-ABI.
+"""The combined backward entry points against the separate ones, through the
+C-ABI: ddpm_gen_bwd_xw against ddpm_gen_bwd_x + ddpm_gen_bwd_w, and
+ddpm_gen_bwd against ddpm_gen_bwd_x + ddpm_gen_bwd_y + ddpm_gen_bwd_w.
 
-The combined entry point runs the same kernels -- the dX tile kernel, the
-weight-gradient partial kernel and its split reduction -- but performs dX's
-halo reduction in helper workgroups of the weight-gradient launch (on the
-CUs its at most 16 x 3 x channel-block workgroups leave free), or as its own
-kernel where fewer than a quarter of the CUs are free.  Every result must be
-bit-identical to the two separate calls.  Shapes: 256x256 C=64 (64 helper
+The combined calls run the same kernels -- the dX tile kernel, the
+weight-gradient partial kernel and its split reduction, the dY kernel -- but
+perform dX's halo reduction (and, for ddpm_gen_bwd, the dY kernel's weight
+packing) in helper workgroups of the weight-gradient launch, on the CUs its
+at most 16 x 3 x channel-block workgroups leave free, or as kernels of their
+own where fewer than a quarter of the CUs are free.  Every result must be
+bit-identical to the separate calls.  Shapes: 256x256 C=64 (64 helper
 workgroups), C=16 (most of the grid is helpers), C=128 (two input-channel
-halves fill the CUs: separate reduction kernel), W % 4 != 0 (one column per
-item), K=1 (256-thread workgroups), and an empty batch.
+halves fill the CUs: separate kernels), W % 4 != 0 (one column per item), K=1
+(256-thread workgroups), and an empty batch.
 """
 
 import ctypes
@@ -38,29 +41,41 @@ def _run(shape, k, dtype, seed):
     wt, b = wt.to(DEV), b.to(DEV)
     g = randn((n, 4 * c, h, w), seed + 3).to(dtype).to(DEV)
     wsx_bytes = int(lib.ddpm_gen_bwd_x_workspace_bytes(n, c, h, w, k, *DIL))
+    wsy_bytes = int(lib.ddpm_gen_bwd_y_workspace_bytes(c, k))
     ws_bytes = int(lib.ddpm_gen_bwd_w_workspace_bytes(n, c, h, w, k, dt))
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     outs = []
-    for combined in (False, True):
+    for mode in ("separate", "xw", "all"):
         gx = torch.full_like(x, float("nan"))
+        gy = torch.full_like(y, float("nan"))
         gw = torch.full_like(wt, float("nan"))
         gb = torch.full_like(b, float("nan"))
         wsx = torch.empty(max(wsx_bytes, 16), dtype=torch.uint8, device=DEV)
+        wsy = torch.empty(max(wsy_bytes, 16), dtype=torch.uint8, device=DEV)
         ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=DEV)
-        if combined:
-            rc = lib.ddpm_gen_bwd_xw(_ptr(x), _ptr(y), _ptr(wt), _ptr(b), _ptr(g), _ptr(gx), _ptr(gw),
-                                     _ptr(gb), _ptr(wsx), wsx_bytes, _ptr(ws), ws_bytes, n, c, h, w, k,
-                                     *DIL, dt, stream)
+        if mode == "all":
+            rc = lib.ddpm_gen_bwd(_ptr(x), _ptr(y), _ptr(wt), _ptr(b), _ptr(g), _ptr(gx), _ptr(gy), _ptr(gw),
+                                  _ptr(gb), _ptr(wsx), wsx_bytes, _ptr(wsy), wsy_bytes, _ptr(ws), ws_bytes,
+                                  n, c, h, w, k, *DIL, dt, stream)
             assert rc == 0, lib.ddpm_status_string(rc).decode()
         else:
-            rc = lib.ddpm_gen_bwd_x(_ptr(y), _ptr(wt), _ptr(b), _ptr(g), _ptr(gx), _ptr(wsx), wsx_bytes,
-                                    n, c, h, w, k, *DIL, dt, stream)
-            assert rc == 0, rc
-            rc = lib.ddpm_gen_bwd_w(_ptr(x), _ptr(y), _ptr(g), _ptr(gw), _ptr(gb), _ptr(ws), ws_bytes,
+            if mode == "xw":
+                rc = lib.ddpm_gen_bwd_xw(_ptr(x), _ptr(y), _ptr(wt), _ptr(b), _ptr(g), _ptr(gx), _ptr(gw),
+                                         _ptr(gb), _ptr(wsx), wsx_bytes, _ptr(ws), ws_bytes, n, c, h, w, k,
+                                         *DIL, dt, stream)
+                assert rc == 0, lib.ddpm_status_string(rc).decode()
+            else:
+                rc = lib.ddpm_gen_bwd_x(_ptr(y), _ptr(wt), _ptr(b), _ptr(g), _ptr(gx), _ptr(wsx),
+                                        wsx_bytes, n, c, h, w, k, *DIL, dt, stream)
+                assert rc == 0, rc
+                rc = lib.ddpm_gen_bwd_w(_ptr(x), _ptr(y), _ptr(g), _ptr(gw), _ptr(gb), _ptr(ws), ws_bytes,
+                                        n, c, h, w, k, *DIL, dt, stream)
+                assert rc == 0, rc
+            rc = lib.ddpm_gen_bwd_y(_ptr(x), _ptr(wt), _ptr(g), _ptr(gy), _ptr(wsy), wsy_bytes,
                                     n, c, h, w, k, *DIL, dt, stream)
             assert rc == 0, rc
         torch.cuda.synchronize()
-        outs.append((gx, gw, gb))
+        outs.append((gx, gy, gw, gb))
     return outs
 
 
@@ -75,19 +90,26 @@ def _run(shape, k, dtype, seed):
         ((1, 32, 40, 56), 1, torch.bfloat16),
     ],
 )
-def test_bwd_xw_matches_separate_calls(shape, k, dtype):
-    say(f"bwd_xw shape={shape} K={k} {dtype}")
-    (sx, sw, sb), (cx, cw, cb) = _run(shape, k, dtype, 1200 + shape[1] + shape[3])
-    for name, a, e in (("dx", cx, sx), ("dw", cw, sw), ("db", cb, sb)):
-        assert not torch.isnan(e).any(), f"{name}: separate calls left unwritten entries"
-        assert torch.equal(a, e), f"{name}: max|diff| {(a.float() - e.float()).abs().max().item():.3e}"
+def test_combined_backward_matches_separate_calls(shape, k, dtype):
+    say(f"combined backward shape={shape} K={k} {dtype}")
+    sep, xw, al = _run(shape, k, dtype, 1200 + shape[1] + shape[3])
+    names = ("dx", "dy", "dw", "db")
+    for label, got in (("xw", xw), ("all", al)):
+        for name, a, e in zip(names, got, sep):
+            if label == "xw" and name == "dy":
+                continue  # ddpm_gen_bwd_xw leaves dY to ddpm_gen_bwd_y in both runs
+            assert not torch.isnan(e).any(), f"{name}: separate calls left unwritten entries"
+            assert torch.equal(a, e), f"{label} {name}: max|diff| {(a.float() - e.float()).abs().max().item():.3e}"
 
 
-def test_bwd_xw_empty_batch_launches_nothing():
-    say("bwd_xw empty batch")
+def test_combined_backward_empty_batch_launches_nothing():
+    say("combined backward empty batch")
     lib = _lib.load()
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     null = ctypes.c_void_p(0)
     rc = lib.ddpm_gen_bwd_xw(null, null, null, null, null, null, null, null, null, 0, null, 0,
                              0, 16, 8, 8, 3, *DIL, 0, stream)
+    assert rc == 0
+    rc = lib.ddpm_gen_bwd(null, null, null, null, null, null, null, null, null, null, 0, null, 0,
+                          null, 0, 0, 16, 8, 8, 3, *DIL, 0, stream)
     assert rc == 0
