@@ -674,7 +674,7 @@ def main():
     from dynamicconvolutionoperator_amd import _lib
 
     lib = _lib.load()
-    entries = [n for n in _lib.SIGNATURES if n.startswith(("ddpm_gen_fwd", "ddpm_gen_bwd_x", "ddpm_gen_bwd_y", "ddpm_gen_bwd_w", "ddpm_filter_", "ddpm_gen_kernels", "ddpm_fuse_conv"))]
+    entries = [n for n in _lib.SIGNATURES if n.startswith(("ddpm_gen_fwd", "ddpm_gen_bwd", "ddpm_filter_", "ddpm_gen_kernels", "ddpm_fuse_conv"))]
     entries = [n for n in entries if not n.endswith(("_workspace_bytes", "_supported", "_scratch_bytes"))]
 
     # ---- headline: fp32 fused recompute training step, uninstrumented

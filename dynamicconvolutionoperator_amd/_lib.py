@@ -57,7 +57,7 @@ SIGNATURES: dict[str, tuple[list, type]] = {
 }
 
 
-ABI_VERSION = 4  # include/ddpm_hip.h
+ABI_VERSION = 5  # include/ddpm_hip.h
 
 
 class HipLibraryError(RuntimeError):

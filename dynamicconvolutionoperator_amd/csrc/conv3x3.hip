@@ -72,7 +72,7 @@ __host__ __device__ constexpr int cv_parts() {
 template <typename T, int MB>
 __global__ __launch_bounds__(256) void conv3x3_pack_kernel(const T* __restrict__ wt,
                                                            uint32_t* __restrict__ pk, ConvGeom g,
-                                                           int rot) {
+                                                           int rot, int pairs) {
   constexpr int P = cv_parts<T>();
   // 32-bit indices: the host bounds the packed units below 2^31
   const int total = g.mgroups * g.nc32 * 9 * MB * 64;
@@ -91,7 +91,8 @@ __global__ __launch_bounds__(256) void conv3x3_pack_kernel(const T* __restrict__
   float v[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const int k = cc * 32 + 4 * e + q;
+    // pair planes (kF32Pairs input): slot 8q + e holds channel 2(q + 4(e/2)) + e%2
+    const int k = cc * 32 + (pairs ? 2 * q + 8 * (e >> 1) + (e & 1) : 4 * e + q);
     float a = 0.f;
     if (m < g.M && k < g.K) {
       // forward: weight[m][k][ki][kj]; input gradient: weight[k][m][2-ki][2-kj]
@@ -131,7 +132,7 @@ struct CvLds {
 
 // out: the result in T (ks = 1), or with K split (ks > 1) the fp32 partial
 // sums part[ksplit][n][M][H*W] (no bias) that conv3x3_reduce_kernel adds up.
-template <typename T, bool BIAS, int MB, bool WIDE>
+template <typename T, bool BIAS, int MB, bool WIDE, bool PAIR = false>
 __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict__ in,
                                                              const uint32_t* __restrict__ pk,
                                                              const T* __restrict__ bias,
@@ -272,7 +273,18 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
       for (int blk = 0; blk < 2; ++blk) {
         const int col = el0 + 16 * blk + dw;
         V bfr[P];
-        if constexpr (sizeof(T) == 4) {
+        if constexpr (PAIR) {
+          // pair planes: dword jj of the hi / lo fragment is staged plane
+          // quad + 4jj / 16 + quad + 4jj (the pair 8jj + 2quad, +1), already split
+          u32x4 h4, l4;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            h4[jj] = xq[4 * jj * L::kXS + col];
+            l4[jj] = xq[(16 + 4 * jj) * L::kXS + col];
+          }
+          bfr[0] = __builtin_bit_cast(V, h4);
+          bfr[1] = __builtin_bit_cast(V, l4);
+        } else if constexpr (sizeof(T) == 4) {
           float bv[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) bv[e] = __uint_as_float(xq[4 * e * L::kXS + col]);
@@ -438,7 +450,7 @@ int64_t cv_workspace_bytes(const ConvGeom& g, int dtype) {
 
 int cv_run(const void* in, const void* wt, const void* bias, void* out, void* workspace,
            int64_t workspace_bytes, int64_t n, int64_t k, int64_t m, int64_t h, int64_t w, int rot,
-           int dtype, hipStream_t stream) {
+           int dtype, hipStream_t stream, bool pairs = false) {
   const int esz = dtype == kF32 ? 4 : 2;
   ConvGeom g;
   cv_geom(g, n, k, m, h, w, esz);
@@ -453,13 +465,13 @@ int cv_run(const void* in, const void* wt, const void* bias, void* out, void* wo
     const dim3 pgrid((unsigned)((units + 255) / 256));
     if (g.mb == 4)
       hipLaunchKernelGGL((conv3x3_pack_kernel<T, 4>), pgrid, dim3(256), 0, stream, (const T*)wt,
-                         (uint32_t*)workspace, g, rot);
+                         (uint32_t*)workspace, g, rot, (int)pairs);
     else if (g.mb == 2)
       hipLaunchKernelGGL((conv3x3_pack_kernel<T, 2>), pgrid, dim3(256), 0, stream, (const T*)wt,
-                         (uint32_t*)workspace, g, rot);
+                         (uint32_t*)workspace, g, rot, (int)pairs);
     else
       hipLaunchKernelGGL((conv3x3_pack_kernel<T, 1>), pgrid, dim3(256), 0, stream, (const T*)wt,
-                         (uint32_t*)workspace, g, rot);
+                         (uint32_t*)workspace, g, rot, (int)pairs);
     int e = (int)hipGetLastError();
     if (e != 0) return e;
     const dim3 grid((unsigned)((int64_t)n * g.tiles_h * g.tiles_w * g.mgroups * g.ks));
@@ -488,19 +500,24 @@ int cv_run(const void* in, const void* wt, const void* bias, void* out, void* wo
       return v4 ? reduce(std::false_type(), std::integral_constant<int, 4>())
                 : reduce(std::false_type(), std::integral_constant<int, 1>());
     };
-    auto pick = [&](auto b) {
+    auto pick = [&](auto b, auto pr) {
       constexpr bool B = decltype(b)::value;
+      constexpr bool PR = decltype(pr)::value && sizeof(T) == 4;
       // one-row segments (wide images) with the narrower staging pitch
       if (g.mb == 4 && g.rs == 1)
-        return launch(conv3x3_kernel<T, B, 4, true>, (size_t)2 * CvLds<T, 4, true>::kBuf * 4);
+        return launch(conv3x3_kernel<T, B, 4, true, PR>, (size_t)2 * CvLds<T, 4, true>::kBuf * 4);
       if (g.mb == 4)
-        return launch(conv3x3_kernel<T, B, 4, false>, (size_t)2 * CvLds<T, 4, false>::kBuf * 4);
+        return launch(conv3x3_kernel<T, B, 4, false, PR>, (size_t)2 * CvLds<T, 4, false>::kBuf * 4);
       if (g.mb == 2)
-        return launch(conv3x3_kernel<T, B, 2, false>, (size_t)2 * CvLds<T, 2, false>::kBuf * 4);
-      return launch(conv3x3_kernel<T, B, 1, false>, (size_t)2 * CvLds<T, 1, false>::kBuf * 4);
+        return launch(conv3x3_kernel<T, B, 2, false, PR>, (size_t)2 * CvLds<T, 2, false>::kBuf * 4);
+      return launch(conv3x3_kernel<T, B, 1, false, PR>, (size_t)2 * CvLds<T, 1, false>::kBuf * 4);
     };
-    if (bias) return pick(std::true_type());
-    return pick(std::false_type());
+    if (pairs) {
+      if (bias) return pick(std::true_type(), std::true_type());
+      return pick(std::false_type(), std::true_type());
+    }
+    if (bias) return pick(std::true_type(), std::false_type());
+    return pick(std::false_type(), std::false_type());
   });
 }
 
@@ -511,6 +528,7 @@ using namespace ddpm;
 
 extern "C" int64_t ddpm_fuse_conv_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t w,
                                                   int dtype) {
+  if (dtype == kF32Pairs) dtype = kF32;  // the same packed weight and partials
   if (n < 0 || c <= 0 || h < 0 || w < 0 || dtype < kF32 || dtype > kF16) return 0;
   if (n == 0 || h == 0 || w == 0) return 0;
   // the larger of the two directions' needs at this shape
@@ -524,12 +542,18 @@ extern "C" int64_t ddpm_fuse_conv_workspace_bytes(int64_t n, int64_t c, int64_t 
 extern "C" int ddpm_fuse_conv_fwd(const void* cat, const void* weight, const void* bias, void* out,
                                   void* workspace, int64_t workspace_bytes, int64_t n, int64_t c,
                                   int64_t h, int64_t w, int dtype, hipStream_t stream) {
+  // kF32Pairs: the concat in pair planes (whole 32-plane chunks: C % 8 == 0)
+  const bool pairs = dtype == kF32Pairs;
+  if (pairs) {
+    if (c % 8 != 0) return kUnsupported;
+    dtype = kF32;
+  }
   int st = cv_check(n, 4 * c, c, h, w, dtype);
   if (st != kOk) return st;
   if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
   if (!cat || !weight || !out) return kBadArgument;
   return cv_run(cat, weight, bias, out, workspace, workspace_bytes, n, 4 * c, c, h, w, 0, dtype,
-                stream);
+                stream, pairs);
 }
 
 extern "C" int ddpm_fuse_conv_bwd_data(const void* grad_out, const void* weight, void* grad_cat,

@@ -89,6 +89,13 @@ __device__ __forceinline__ float cw_lds_elem(const uint32_t* __restrict__ base, 
   }
 }
 
+// Pair-plane index (kF32Pairs concat) of staged row c of 16-plane block cb:
+// rows 0..7 the hi planes of the block's 8 channel pairs, rows 8..15 their lo
+// planes (a 32-plane chunk holds 16 hi planes, then 16 lo planes).
+__device__ __forceinline__ int cw_pair_plane(int cb, int c) {
+  return (cb >> 1) * 32 + (c >> 3) * 16 + (cb & 1) * 8 + (c & 7);
+}
+
 struct CwPos {
   int n, h, w0, cbk;
   __device__ __forceinline__ void advance(const CwGeom& g) {
@@ -104,7 +111,10 @@ struct CwPos {
   }
 };
 
-template <typename T, int MB>
+// PP (fp32): `cat` holds pair planes (kF32Pairs); staged row c < 8 of a
+// 16-plane block holds the hi plane of its channels (2c, 2c+1), row 8 + c
+// their lo plane.
+template <typename T, int MB, bool PP = false>
 __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
     const T* __restrict__ cat, const T* __restrict__ gout, float* __restrict__ pw,
     float* __restrict__ pb, T* __restrict__ dw_out, T* __restrict__ db_out, CwGeom g) {
@@ -177,7 +187,7 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
         const int pr = wave + kCwNW * j;
         if (L::kXRows % kCwNW != 0 && pr >= L::kXRows) break;
         const int rr = pr >> 4, c = pr & 15;
-        const int ch = cb * 16 + c, hh = p.h + rr - 1;
+        const int ch = PP ? cw_pair_plane(cb, c) : cb * 16 + c, hh = p.h + rr - 1;
         const bool ok = ch < CI && (unsigned)hh < (unsigned)H;
         const uint32_t soff = ok ? ((uint32_t)ch * (uint32_t)HW + (uint32_t)(hh * W)) * E : 0u;
         const BufRes rs = ok ? xres : xnul;
@@ -192,7 +202,8 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
       for (int idx = tid; idx < L::kXRows * kCwLW; idx += kCwThreads) {
         const int pr = idx / kCwLW, j = idx - pr * kCwLW;
         const int rr = pr >> 4, c = pr & 15;
-        const int ch = cb * 16 + c, hh = p.h + rr - 1, gw = p.w0 - kCwPad + j;
+        const int ch = PP ? cw_pair_plane(cb, c) : cb * 16 + c;
+        const int hh = p.h + rr - 1, gw = p.w0 - kCwPad + j;
         const bool ok = ch < CI && (unsigned)hh < (unsigned)H && (unsigned)gw < (unsigned)W;
         const uint32_t off = ok ? (uint32_t)(((int64_t)ch * H + hh) * W + gw) * E : kOob;
         dst[pr * L::kXSD * L::kPerD + j] = from_f<T>(buf_load1<T>(xres, off));
@@ -313,6 +324,10 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
   int xel[3];
 #pragma unroll
   for (int kj = 0; kj < 3; ++kj) xel[kj] = (ki * 16 + col16) * L::kXSD * L::kPerD + kCwPad + wl + kj - 1;
+  // PP: this lane's channel is half (col16 & 1) of the pair in rows col16/2 (hi)
+  // and 8 + col16/2 (lo)
+  const int ppel = (ki * 16 + (col16 >> 1)) * L::kXSD + kCwPad + wl - 1;
+  const uint32_t ppsel = (col16 & 1) ? 0x07060302u : 0x05040100u;
   const int bib = cb - oh * MB;  // the staged gO block this workgroup sums for the bias
   for (int s = 0; s < steps; ++s) {
     const int buf = s & 1;
@@ -342,7 +357,22 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
 #pragma unroll
     for (int kj = 0; kj < 3; ++kj) {
       V afr[P];
-      if constexpr (sizeof(T) == 4) {
+      if constexpr (PP) {
+        uint32_t dh[8], dl[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          dh[e] = bb[ppel + kj + e];
+          dl[e] = bb[ppel + 8 * L::kXSD + kj + e];
+        }
+        u32x4 h4, l4;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          h4[jj] = __builtin_amdgcn_perm(dh[2 * jj + 1], dh[2 * jj], ppsel);
+          l4[jj] = __builtin_amdgcn_perm(dl[2 * jj + 1], dl[2 * jj], ppsel);
+        }
+        afr[0] = __builtin_bit_cast(V, h4);
+        afr[1] = __builtin_bit_cast(V, l4);
+      } else if constexpr (sizeof(T) == 4) {
         float xv[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) xv[e] = cw_lds_elem<T>(bb, xel[kj] + e);
@@ -526,6 +556,7 @@ using namespace ddpm;
 
 extern "C" int64_t ddpm_fuse_conv_bwd_weight_workspace_bytes(int64_t n, int64_t c, int64_t h,
                                                              int64_t w, int dtype) {
+  if (dtype == kF32Pairs) dtype = kF32;  // the same partials
   if (n <= 0 || c <= 0 || h <= 0 || w <= 0 || dtype < kF32 || dtype > kF16) return 0;
   if (n * h * ((w + kCwTW - 1) / kCwTW) > 0x7fffffffLL) return 0;
   CwGeom g;
@@ -537,6 +568,12 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
                                          void* grad_bias, void* workspace, int64_t workspace_bytes,
                                          int64_t n, int64_t c, int64_t h, int64_t w, int dtype,
                                          hipStream_t stream) {
+  // kF32Pairs: `cat` in pair planes (whole 32-plane chunks: C % 8 == 0)
+  const bool pp = dtype == kF32Pairs;
+  if (pp) {
+    if (c % 8 != 0) return kUnsupported;
+    dtype = kF32;
+  }
   if (dtype < kF32 || dtype > kF16) return kBadArgument;
   if (n < 0 || c < 0 || h < 0 || w < 0) return kBadArgument;
   if (c > 128) return kUnsupported;  // a workgroup stages the grad_out rows of 64 output planes
@@ -577,7 +614,7 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
       const size_t stage = (size_t)2 * L::kBuf * 4;
       const size_t red = (size_t)(kCwSegs * 9 * 16 * (MB * 16 + 1) + kCwSegs * 16) * sizeof(float);
       const size_t lds = stage > red ? stage : red;
-      auto kern = conv_wgrad_partial_kernel<T, MB>;
+      auto kern = pp ? conv_wgrad_partial_kernel<T, MB, sizeof(T) == 4> : conv_wgrad_partial_kernel<T, MB>;
       const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
       if (ae != 0) return ae;
       hipLaunchKernelGGL(kern, dim3((unsigned)(g.splits * g.cblocks * g.ohalves)), dim3(kCwThreads), lds, stream,

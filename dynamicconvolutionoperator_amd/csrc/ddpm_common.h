@@ -23,7 +23,13 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-enum DType : int { kF32 = 0, kBF16 = 1, kF16 = 2 };
+enum DType : int { kF32 = 0, kBF16 = 1, kF16 = 2, kF32Pairs = 3 };
+// kF32Pairs: fp32 data whose 4C-plane concat is stored as bf16 (hi, lo) pair
+// planes -- per 32-plane chunk, plane j < 16 holds the hi halves of channels
+// (2j, 2j+1) (low / high 16 bits) and plane 16 + j their lo halves (hi = the
+// top 16 bits of the fp32 pattern, lo = the remainder rounded to nearest
+// even): the same bytes as the fp32 concat, already split the way the fp32
+// MFMA path splits its operands.
 
 // Error codes returned next to hipError_t values (chosen above hipError_t's range).
 enum Status : int {

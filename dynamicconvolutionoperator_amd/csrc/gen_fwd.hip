@@ -21,11 +21,12 @@ namespace ddpm {
 // CB = 4: 256 registers per lane (one 8-wave workgroup per CU, whose 133 KB
 // halo tile fills the LDS anyway); CB = 2: 128 registers, two workgroups per
 // CU, unless the y operand needs more (gt_waves_per_eu).
-template <typename T, int KS, int NK, int CB>
+// PP: the concat as pair planes (kF32Pairs, fp32 only).
+template <typename T, int KS, int NK, int CB, bool PP = false>
 __global__ __launch_bounds__(kGtThreads) __attribute__((amdgpu_waves_per_eu(gt_waves_per_eu<T, NK, CB>()))) void gen_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ wt,
     const T* __restrict__ bias, T* __restrict__ out, TileGeom g) {
-  gen_tile_body<T, KS, NK, CB, false>(x, y, wt, bias, out, nullptr, g);
+  gen_tile_body<T, KS, NK, CB, false, PP>(x, y, wt, bias, out, nullptr, g);
 }
 
 // Two fp32 values rounded to nearest-even in T (bf16 / f16), packed low/high.
@@ -275,6 +276,12 @@ using namespace ddpm;
 extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, const void* bias,
                             void* out, int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size,
                             int d0, int d1, int d2, int dtype, hipStream_t stream) {
+  // kF32Pairs: fp32 inputs, the concat written as pair planes (C % 16 == 0)
+  const bool pp = dtype == kF32Pairs;
+  if (pp) {
+    if (c % 16 != 0 || 32 * h * w * 4 > 0x7fffffffLL) return kUnsupported;
+    dtype = kF32;
+  }
   if (dtype < kF32 || dtype > kF16) return kBadArgument;
   GenGeom gg;
   int st = gen_make_geom(gg, n, c, h, w, kernel_size, d0, d1, d2);
@@ -329,18 +336,23 @@ extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, co
     };
     // 1 or 2 chunks of 32 input channels, or 4 (65..128 channels; chunks
     // past C read zeros)
-    auto pick = [&](auto ks) {
+    auto pick = [&](auto ks, auto ppc) {
       constexpr int KS = decltype(ks)::value;
+      constexpr bool PP = decltype(ppc)::value && sizeof(T) == 4;
       if (nk > 2) {
-        return launch(gen_fwd_kernel<T, KS, 4, 2>);  // 32-column tiles
+        return launch(gen_fwd_kernel<T, KS, 4, 2, PP>);  // 32-column tiles
       }
       if (cb == 4)
-        return nk == 1 ? launch(gen_fwd_kernel<T, KS, 1, 4>) : launch(gen_fwd_kernel<T, KS, 2, 4>);
+        return nk == 1 ? launch(gen_fwd_kernel<T, KS, 1, 4, PP>) : launch(gen_fwd_kernel<T, KS, 2, 4, PP>);
       if (cb == 1)
-        return nk == 1 ? launch(gen_fwd_kernel<T, KS, 1, 1>) : launch(gen_fwd_kernel<T, KS, 2, 1>);
-      return nk == 1 ? launch(gen_fwd_kernel<T, KS, 1, 2>) : launch(gen_fwd_kernel<T, KS, 2, 2>);
+        return nk == 1 ? launch(gen_fwd_kernel<T, KS, 1, 1, PP>) : launch(gen_fwd_kernel<T, KS, 2, 1, PP>);
+      return nk == 1 ? launch(gen_fwd_kernel<T, KS, 1, 2, PP>) : launch(gen_fwd_kernel<T, KS, 2, 2, PP>);
     };
-    if (kernel_size == 1) return pick(std::integral_constant<int, 1>());
-    return pick(std::integral_constant<int, 3>());
+    if (pp) {
+      if (kernel_size == 1) return pick(std::integral_constant<int, 1>(), std::true_type());
+      return pick(std::integral_constant<int, 3>(), std::true_type());
+    }
+    if (kernel_size == 1) return pick(std::integral_constant<int, 1>(), std::false_type());
+    return pick(std::integral_constant<int, 3>(), std::false_type());
   });
 }

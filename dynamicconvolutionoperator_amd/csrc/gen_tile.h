@@ -168,7 +168,10 @@ __device__ __forceinline__ void gf_store_raw(BufRes r, uint32_t off, uint32_t v)
 // entries (XB bytes each) for the workgroup's 16-channel block starting at
 // channel c0 (nch of them), tile rows h0.., columns w0..; the tile's own
 // pixels also go to the identity channels of the concat `out`.
-template <typename T, int XB, int CB>
+// PP (fp32 only): the identity channels go to `out` as pair planes
+// (kF32Pairs): channels (c, c+1) of a 32-plane chunk as one hi and one lo
+// plane, 16 planes apart; C % 16 == 0.
+template <typename T, int XB, int CB, bool PP = false>
 __device__ __forceinline__ void gt_stage_x(const T* __restrict__ a, T* __restrict__ out,
                                            unsigned char* __restrict__ xs, const TileGeom& g,
                                            int n, int c0, int nch, int h0, int w0, int TW,
@@ -181,7 +184,9 @@ __device__ __forceinline__ void gt_stage_x(const T* __restrict__ a, T* __restric
   // ---- halo tile of x (zero outside the image) -> LDS planes; the tile's
   //      own pixels also go to the identity channels of the output
   const BufRes xres = make_buf(a + ((int64_t)n * C + c0) * HW, (uint32_t)nch * HWE);
-  const BufRes ores = make_buf(out + ((int64_t)n * 4 * C + c0) * HW, (uint32_t)nch * HWE);
+  const BufRes ores = PP ? make_buf(out + ((int64_t)n * 4 * C + (c0 & ~31)) * HW, 32u * HWE)
+                        : make_buf(out + ((int64_t)n * 4 * C + c0) * HW, (uint32_t)nch * HWE);
+  const uint32_t pp0 = (uint32_t)((c0 & 31) >> 1);  // PP: pair index of channels (c0, c0+1)
   if (g.vec) {
     // a task = (4-channel plane, halo row, 4 image columns a multiple of 4
     // apart from column 0): one 16-byte (8-byte) access per channel, the
@@ -240,13 +245,32 @@ __device__ __forceinline__ void gt_stage_x(const T* __restrict__ a, T* __restric
           *reinterpret_cast<XQ*>(xs + grp * g.plane + (i * LW + j) * XB) = q;
         }
         if (i >= R && i < R + kGtTH && 4 * k >= cpos && 4 * k < cpos + TW) {
+          if constexpr (PP) {
+            // channels (4grp + 2kp, +1): their 4 columns split into a hi and a lo vector
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t o = off[u] + (uint32_t)(4 * grp + e) * HWE;
-            if constexpr (E == 4)
-              __builtin_amdgcn_raw_buffer_store_b128(v[u][e], ores, o, 0, 0);
-            else
-              __builtin_amdgcn_raw_buffer_store_b64(v[u][e], ores, o, 0, 0);
+            for (int kp = 0; kp < 2; ++kp) {
+              VD hv, lv;
+#pragma unroll
+              for (int m = 0; m < 4; ++m) {
+                uint32_t hh, ll;
+                split_bf16x2(__uint_as_float(v[u][2 * kp][m]), __uint_as_float(v[u][2 * kp + 1][m]),
+                             hh, ll);
+                hv[m] = hh;
+                lv[m] = ll;
+              }
+              const uint32_t o = off[u] == kOob ? kOob : off[u] + (pp0 + 2 * grp + kp) * HWE;
+              __builtin_amdgcn_raw_buffer_store_b128(hv, ores, o, 0, 0);
+              __builtin_amdgcn_raw_buffer_store_b128(lv, ores, o == kOob ? kOob : o + 16u * HWE, 0, 0);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t o = off[u] + (uint32_t)(4 * grp + e) * HWE;
+              if constexpr (E == 4)
+                __builtin_amdgcn_raw_buffer_store_b128(v[u][e], ores, o, 0, 0);
+              else
+                __builtin_amdgcn_raw_buffer_store_b64(v[u][e], ores, o, 0, 0);
+            }
           }
         }
       }
@@ -273,10 +297,23 @@ __device__ __forceinline__ void gt_stage_x(const T* __restrict__ a, T* __restric
       for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int ch = 0; ch < 16; ++ch) v[s][ch] = gf_load_raw<E>(xres, lo[s] + ch * HWE);
+      if constexpr (PP) {
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
+        for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int ch = 0; ch < 16; ++ch) gf_store_raw<E>(ores, so[s] + ch * HWE, v[s][ch]);
+          for (int kp = 0; kp < 8; ++kp) {
+            uint32_t hh, ll;
+            split_bf16x2(__uint_as_float(v[s][2 * kp]), __uint_as_float(v[s][2 * kp + 1]), hh, ll);
+            const uint32_t o = so[s] == kOob ? kOob : so[s] + (pp0 + kp) * HWE;
+            __builtin_amdgcn_raw_buffer_store_b32(hh, ores, o, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b32(ll, ores, o == kOob ? kOob : o + 16u * HWE, 0, 0);
+          }
+      } else {
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int ch = 0; ch < 16; ++ch) gf_store_raw<E>(ores, so[s] + ch * HWE, v[s][ch]);
+      }
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         if (pix[s] >= g.npix) continue;
@@ -334,7 +371,7 @@ __device__ __forceinline__ void gt_load_y(const T* __restrict__ y,
 // own partial (c + R + pad) and in its left / right neighbour's (c + R + pad
 // -/+ TW), and the 4-column groups that a neighbour's halo only partly covers
 // read zeros for the rest.
-template <typename T, int KS, int NK, int CB, bool BX>
+template <typename T, int KS, int NK, int CB, bool BX, bool PP = false>
 __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* __restrict__ y,
                                               const T* __restrict__ wt, const T* __restrict__ bias,
                                               T* __restrict__ out, float* __restrict__ part,
@@ -449,7 +486,7 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
     // the x halo tile first (its loads are consumed there), then the bias
     // rows, the first weight slice and the y operand with their loads in
     // flight together
-    gt_stage_x<T, XB, CB>(a, out, xs, g, n, c0, nch, h0, w0, TW, tid);
+    gt_stage_x<T, XB, CB, PP>(a, out, xs, g, n, c0, nch, h0, w0, TW, tid);
     bias_load();
     wload(0);
     gt_load_y<T, NK, CB>(y, bfr, g, n, h0, w0, wave, col16, quad);
@@ -571,7 +608,26 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[blk][e] = fmaf(q[e], xv[e], acc[blk][e]);
       }
-      if (t == KK - 1) {
+      if (PP && t == KK - 1) {
+        // ---- branch b as pair planes: channels (4quad + 2kp, +1) of output
+        //      block b+1, split, to the hi / lo planes of their 32-plane chunk
+        const int chb = (b + 1) * C + c0;
+        const BufRes pres = make_buf(out + ((int64_t)n * 4 * C + (chb & ~31)) * HW, 32u * HWE);
+        const uint32_t pbase = (uint32_t)(((chb & 31) >> 1) + 2 * quad);
+#pragma unroll
+        for (int blk = 0; blk < NBW; ++blk) {
+          const int gh = h0 + 2 * wave + blk / CB, gw = w0 + 16 * (blk % CB) + col16;
+          const bool ok = gh < H && gw < W && 4 * quad < nch;
+#pragma unroll
+          for (int kp = 0; kp < 2; ++kp) {
+            uint32_t hh, ll;
+            split_bf16x2(acc[blk][2 * kp], acc[blk][2 * kp + 1], hh, ll);
+            const uint32_t o = ok ? (uint32_t)(gh * W + gw) * 4u + (pbase + kp) * HWE : kOob;
+            __builtin_amdgcn_raw_buffer_store_b32(hh, pres, o, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b32(ll, pres, ok ? o + 16u * HWE : kOob, 0, 0);
+          }
+        }
+      } else if (t == KK - 1) {
         // ---- branch b: channels c0 + 4*quad + e of output block b+1
         const BufRes bres = make_buf(out + ((int64_t)n * 4 * C + (int64_t)(b + 1) * C + c0) * HW,
                                      (uint32_t)nch * HWE);

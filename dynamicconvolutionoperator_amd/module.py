@@ -12,9 +12,12 @@ with the GPU route backed by HIP kernels for gfx950:
 * CPU tensors -> the reference's CPU branch (triton_impl.py:353-391).
 
 The final 3x3 ``fuse`` convolution is a plain ``nn.Conv2d`` (its parameters and
-state-dict keys are the reference's); on ROCm tensors its forward and input
-gradient run as HIP MFMA kernels (``fuse_conv_backend = "library"`` selects
-MIOpen through ``self.fuse`` instead).
+state-dict keys are the reference's); on ROCm tensors its forward and
+gradients run as HIP MFMA kernels (``fuse_conv_backend = "library"`` selects
+MIOpen through ``self.fuse`` instead).  For fp32 on the fused route with
+C % 16 == 0, generator, filter, concat and fuse convolution run as one
+autograd op (``ops.fused_ddpm``) whose concat is stored as bf16 pair planes,
+already split the way the fuse convolution's fp32 MFMA products need it.
 """
 
 from __future__ import annotations
@@ -40,7 +43,7 @@ def _load_hip_ops():
 
     _lib.load()
     return (ops.fused_dynamic_cat, ops.fused_generator_dynamic_cat, ops.generator_supported,
-            ops._generate, ops.fuse_conv3x3)
+            ops._generate, ops.fuse_conv3x3, ops.fused_ddpm, ops.fused_ddpm_supported)
 
 
 def _check_inputs(x: torch.Tensor, y: torch.Tensor, channels: int) -> None:
@@ -130,7 +133,7 @@ class DDPM(nn.Module):
         return "fused" if can_fuse else "materialized"
 
     def _cuda_cat(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
-        fused_dynamic_cat, fused_generator_dynamic_cat, gen_supported, generate, _ = _load_hip_ops()
+        fused_dynamic_cat, fused_generator_dynamic_cat, gen_supported, generate = _load_hip_ops()[:4]
         if self._route(x, y, gen_supported) == "fused":
             return fused_generator_dynamic_cat(
                 x, y, self.generator.weight, self.generator.bias, self.kernel_size, self.dilations
@@ -180,9 +183,27 @@ class DDPM(nn.Module):
             return fuse_conv3x3(cat_out, self.fuse.weight, self.fuse.bias)
         return self.fuse(cat_out)
 
+    def _cuda_pairs(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor | None:
+        """fp32 on the fused route with the HIP fuse convolution: generator,
+        filter, concat and fuse convolution as one op whose concat is stored
+        as bf16 pair planes (``ops.fused_ddpm``); ``None`` where it does not
+        apply."""
+        if self.fuse_conv_backend != "hip" or x.dtype != torch.float32:
+            return None
+        ops = _load_hip_ops()
+        fused_ddpm, supported = ops[5], ops[6]
+        args = (x, y, self.generator.weight, self.generator.bias, self.fuse.weight, self.fuse.bias,
+                self.kernel_size, self.dilations)
+        if not supported(*args) or self._route(x, y, ops[2]) != "fused":
+            return None
+        return fused_ddpm(*args)
+
     def forward(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         _check_inputs(x, y, self.dim)
         if x.is_cuda:
+            out = self._cuda_pairs(x, y)
+            if out is not None:
+                return out
             return self._cuda_fuse(self._cuda_cat(x, y))
         elif x.device.type == "cpu":
             cat_out = self._cpu_cat(x, y)

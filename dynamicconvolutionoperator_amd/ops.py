@@ -28,6 +28,11 @@ import torch
 from . import _lib
 
 _DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+# dtype code of an fp32 concat stored as bf16 (hi, lo) pair planes: per
+# 32-plane chunk, plane j < 16 holds the hi halves of channels (2j, 2j+1) and
+# plane 16 + j their lo halves (hi = the top 16 bits of the fp32 pattern, lo =
+# the remainder rounded to nearest even)
+_PAIR_PLANES = 3
 
 
 def _dt(t: torch.Tensor) -> int:
@@ -237,80 +242,86 @@ class _GeneratorDynamicCat(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         x, y, weight, bias = ctx.saved_tensors
-        grad_out = _as(grad_out, x.dtype)
-        k, dil = ctx.kernel_size, ctx.dilations
-        n, c, h, w = x.shape
-        lib = _lib.load()
-        dt = _dt(x)
-        stream = _stream(x)
-        grad_x = grad_y = grad_w = grad_b = None
-        need_x = ctx.needs_input_grad[0]
-        need_y = ctx.needs_input_grad[1]
-        need_wb = ctx.needs_input_grad[2] or ctx.needs_input_grad[3]
-        with _on(x.device):
-            if need_x:
-                grad_x = torch.empty_like(x)
-                wsx_bytes = _ws_bytes("ddpm_gen_bwd_x_workspace_bytes", n, c, h, w, k, *dil)
-                wsx = torch.empty(wsx_bytes, dtype=torch.uint8, device=x.device)
-            if need_wb:
-                grad_w = torch.empty_like(weight)
-                grad_b = torch.empty_like(bias)
-                ws_bytes = _ws_bytes("ddpm_gen_bwd_w_workspace_bytes", n, c, h, w, k, dt)
-                ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
-            if need_y:
-                grad_y = torch.empty_like(y)
-                wsy_bytes = _ws_bytes("ddpm_gen_bwd_y_workspace_bytes", c, k)
-                wsy = torch.empty(wsy_bytes, dtype=torch.uint8, device=x.device)
-            y_pending = need_y
-            if need_x and need_y and need_wb:
-                # one call: dY's weight packing and dX's halo reduction run on
-                # the CUs dW leaves free
-                _lib.check(
-                    lib.ddpm_gen_bwd(_ptr(x), _ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
-                                     _ptr(grad_x), _ptr(grad_y), _ptr(grad_w), _ptr(grad_b),
-                                     _ptr(wsx), wsx_bytes, _ptr(wsy), wsy_bytes, _ptr(ws), ws_bytes,
-                                     n, c, h, w, k, *dil, dt, stream),
-                    "ddpm_gen_bwd",
-                )
-                y_pending = False
-            elif need_x and need_wb:
-                # one call: dX's halo reduction runs on the CUs dW leaves free
-                _lib.check(
-                    lib.ddpm_gen_bwd_xw(_ptr(x), _ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
-                                        _ptr(grad_x), _ptr(grad_w), _ptr(grad_b), _ptr(wsx),
-                                        wsx_bytes, _ptr(ws), ws_bytes, n, c, h, w, k, *dil, dt,
-                                        stream),
-                    "ddpm_gen_bwd_xw",
-                )
-            elif need_x:
-                _lib.check(
-                    lib.ddpm_gen_bwd_x(_ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
-                                       _ptr(grad_x), _ptr(wsx), wsx_bytes, n, c, h, w, k, *dil,
-                                       dt, stream),
-                    "ddpm_gen_bwd_x",
-                )
-            elif need_wb:
-                _lib.check(
-                    lib.ddpm_gen_bwd_w(_ptr(x), _ptr(y), _ptr(grad_out), _ptr(grad_w),
-                                       _ptr(grad_b), _ptr(ws), ws_bytes, n, c, h, w, k, *dil, dt,
-                                       stream),
-                    "ddpm_gen_bwd_w",
-                )
-            if need_x:
-                del wsx
-            if need_wb:
-                del ws
-                if not ctx.needs_input_grad[2]:
-                    grad_w = None
-                if not ctx.needs_input_grad[3]:
-                    grad_b = None
-            if y_pending:
-                _lib.check(
-                    lib.ddpm_gen_bwd_y(_ptr(x), _ptr(weight), _ptr(grad_out), _ptr(grad_y),
-                                       _ptr(wsy), wsy_bytes, n, c, h, w, k, *dil, dt, stream),
-                    "ddpm_gen_bwd_y",
-                )
-        return grad_x, grad_y, grad_w, grad_b, None, None
+        grads = _generator_backward(x, y, weight, bias, _as(grad_out, x.dtype), ctx.kernel_size,
+                                    ctx.dilations, ctx.needs_input_grad[:4])
+        return (*grads, None, None)
+
+
+def _generator_backward(x, y, weight, bias, grad_out, k, dil, needs):
+    """The four gradients of the fused generator op (``None`` where
+    ``needs`` says no): one ``ddpm_gen_bwd`` call when all are needed, else
+    the combined dX / dW call or the separate entry points."""
+    n, c, h, w = x.shape
+    lib = _lib.load()
+    dt = _dt(x)
+    stream = _stream(x)
+    grad_x = grad_y = grad_w = grad_b = None
+    need_x, need_y = needs[0], needs[1]
+    need_wb = needs[2] or needs[3]
+    with _on(x.device):
+        if need_x:
+            grad_x = torch.empty_like(x)
+            wsx_bytes = _ws_bytes("ddpm_gen_bwd_x_workspace_bytes", n, c, h, w, k, *dil)
+            wsx = torch.empty(wsx_bytes, dtype=torch.uint8, device=x.device)
+        if need_wb:
+            grad_w = torch.empty_like(weight)
+            grad_b = torch.empty_like(bias)
+            ws_bytes = _ws_bytes("ddpm_gen_bwd_w_workspace_bytes", n, c, h, w, k, dt)
+            ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+        if need_y:
+            grad_y = torch.empty_like(y)
+            wsy_bytes = _ws_bytes("ddpm_gen_bwd_y_workspace_bytes", c, k)
+            wsy = torch.empty(wsy_bytes, dtype=torch.uint8, device=x.device)
+        y_pending = need_y
+        if need_x and need_y and need_wb:
+            # one call: dY's weight packing and dX's halo reduction run on
+            # the CUs dW leaves free
+            _lib.check(
+                lib.ddpm_gen_bwd(_ptr(x), _ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
+                                 _ptr(grad_x), _ptr(grad_y), _ptr(grad_w), _ptr(grad_b),
+                                 _ptr(wsx), wsx_bytes, _ptr(wsy), wsy_bytes, _ptr(ws), ws_bytes,
+                                 n, c, h, w, k, *dil, dt, stream),
+                "ddpm_gen_bwd",
+            )
+            y_pending = False
+        elif need_x and need_wb:
+            # one call: dX's halo reduction runs on the CUs dW leaves free
+            _lib.check(
+                lib.ddpm_gen_bwd_xw(_ptr(x), _ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
+                                    _ptr(grad_x), _ptr(grad_w), _ptr(grad_b), _ptr(wsx),
+                                    wsx_bytes, _ptr(ws), ws_bytes, n, c, h, w, k, *dil, dt,
+                                    stream),
+                "ddpm_gen_bwd_xw",
+            )
+        elif need_x:
+            _lib.check(
+                lib.ddpm_gen_bwd_x(_ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
+                                   _ptr(grad_x), _ptr(wsx), wsx_bytes, n, c, h, w, k, *dil,
+                                   dt, stream),
+                "ddpm_gen_bwd_x",
+            )
+        elif need_wb:
+            _lib.check(
+                lib.ddpm_gen_bwd_w(_ptr(x), _ptr(y), _ptr(grad_out), _ptr(grad_w),
+                                   _ptr(grad_b), _ptr(ws), ws_bytes, n, c, h, w, k, *dil, dt,
+                                   stream),
+                "ddpm_gen_bwd_w",
+            )
+        if need_x:
+            del wsx
+        if need_wb:
+            del ws
+            if not needs[2]:
+                grad_w = None
+            if not needs[3]:
+                grad_b = None
+        if y_pending:
+            _lib.check(
+                lib.ddpm_gen_bwd_y(_ptr(x), _ptr(weight), _ptr(grad_out), _ptr(grad_y),
+                                   _ptr(wsy), wsy_bytes, n, c, h, w, k, *dil, dt, stream),
+                "ddpm_gen_bwd_y",
+            )
+    return grad_x, grad_y, grad_w, grad_b
 
 
 # ---------------------------------------------------------------------------
@@ -473,6 +484,60 @@ def _fuse_conv_workspace(n, c, h, w, dt, device):
     return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device), nbytes
 
 
+def _fuse_conv_forward(cat, weight, bias, cat_code):
+    """``ddpm_fuse_conv_fwd`` of a contiguous concat; ``cat_code`` is the
+    concat's dtype code (3: fp32 pair planes)."""
+    n, ci, h, w = cat.shape
+    c = weight.shape[0]
+    out = torch.empty((n, c, h, w), dtype=weight.dtype, device=cat.device)
+    lib = _lib.load()
+    with _on(cat.device):
+        ws, nbytes = _fuse_conv_workspace(n, c, h, w, cat_code, cat.device)
+        code = lib.ddpm_fuse_conv_fwd(_ptr(cat), _ptr(weight),
+                                      _ptr(bias.contiguous()) if bias is not None else None,
+                                      _ptr(out), _ptr(ws), nbytes, n, c, h, w, cat_code, _stream(cat))
+    _lib.check(code, "ddpm_fuse_conv_fwd")
+    return out
+
+
+def _fuse_conv_backward(cat, weight, has_bias, grad_out, needs, cat_code):
+    """Gradients of the fuse convolution for the concat (plain layout), the
+    weight and the bias, ``None`` where ``needs`` says no.  ``cat_code`` 3
+    reads a pair-plane concat in the weight gradient (its input gradient is a
+    plain fp32 concat)."""
+    n, ci, h, w = cat.shape
+    c = weight.shape[0]
+    dt = _dt(weight)
+    grad_cat = grad_w = grad_b = None
+    lib = _lib.load()
+    if needs[0]:
+        grad_cat = torch.empty((n, ci, h, w), dtype=weight.dtype, device=cat.device)
+        with _on(cat.device):
+            ws, nbytes = _fuse_conv_workspace(n, c, h, w, dt, cat.device)
+            code = lib.ddpm_fuse_conv_bwd_data(_ptr(grad_out), _ptr(weight), _ptr(grad_cat),
+                                               _ptr(ws), nbytes, n, c, h, w, dt, _stream(cat))
+        _lib.check(code, "ddpm_fuse_conv_bwd_data")
+    need_w = needs[1]
+    need_b = has_bias and needs[2]
+    if need_w or need_b:
+        gw = torch.empty_like(weight)
+        gb = torch.empty((c,), dtype=weight.dtype, device=cat.device)
+        with _on(cat.device):
+            nbytes = _ws_bytes("ddpm_fuse_conv_bwd_weight_workspace_bytes", n, c, h, w, cat_code)
+            ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=cat.device)
+            code = lib.ddpm_fuse_conv_bwd_weight(_ptr(cat), _ptr(grad_out), _ptr(gw), _ptr(gb),
+                                                 _ptr(ws), nbytes, n, c, h, w, cat_code, _stream(cat))
+        if code == _lib.STATUS_UNSUPPORTED and cat_code != _PAIR_PLANES:
+            _, gw, gb = torch.ops.aten.convolution_backward(
+                grad_out, cat, weight, [c] if has_bias else None, [1, 1], [1, 1], [1, 1],
+                False, [0, 0], 1, [False, need_w, need_b])
+        else:
+            _lib.check(code, "ddpm_fuse_conv_bwd_weight")
+        grad_w = gw if need_w else None
+        grad_b = gb if need_b else None
+    return grad_cat, grad_w, grad_b
+
+
 class _FuseConv3x3(torch.autograd.Function):
     """``F.conv2d(cat, weight, bias, padding=1)`` for the DDPM fuse
     convolution as HIP MFMA kernels: forward and input gradient
@@ -485,17 +550,7 @@ class _FuseConv3x3(torch.autograd.Function):
     def forward(ctx, cat, weight, bias):
         cat = cat.contiguous()
         weight = weight.contiguous()
-        n, ci, h, w = cat.shape
-        c = weight.shape[0]
-        out = torch.empty((n, c, h, w), dtype=cat.dtype, device=cat.device)
-        dt = _dt(cat)
-        lib = _lib.load()
-        with _on(cat.device):
-            ws, nbytes = _fuse_conv_workspace(n, c, h, w, dt, cat.device)
-            code = lib.ddpm_fuse_conv_fwd(_ptr(cat), _ptr(weight),
-                                          _ptr(bias.contiguous()) if bias is not None else None,
-                                          _ptr(out), _ptr(ws), nbytes, n, c, h, w, dt, _stream(cat))
-        _lib.check(code, "ddpm_fuse_conv_fwd")
+        out = _fuse_conv_forward(cat, weight, bias, _dt(cat))
         ctx.save_for_backward(cat, weight)
         ctx.has_bias = bias is not None
         return out
@@ -503,40 +558,8 @@ class _FuseConv3x3(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         cat, weight = ctx.saved_tensors
-        grad_out = _as(grad_out, cat.dtype)
-        n, ci, h, w = cat.shape
-        c = weight.shape[0]
-        grad_cat = grad_w = grad_b = None
-        if ctx.needs_input_grad[0]:
-            grad_cat = torch.empty_like(cat)
-            dt = _dt(cat)
-            lib = _lib.load()
-            with _on(cat.device):
-                ws, nbytes = _fuse_conv_workspace(n, c, h, w, dt, cat.device)
-                code = lib.ddpm_fuse_conv_bwd_data(_ptr(grad_out), _ptr(weight), _ptr(grad_cat),
-                                                   _ptr(ws), nbytes, n, c, h, w, dt, _stream(cat))
-            _lib.check(code, "ddpm_fuse_conv_bwd_data")
-        need_w = ctx.needs_input_grad[1]
-        need_b = ctx.has_bias and ctx.needs_input_grad[2]
-        if need_w or need_b:
-            dt = _dt(cat)
-            lib = _lib.load()
-            gw = torch.empty_like(weight)
-            gb = torch.empty((c,), dtype=cat.dtype, device=cat.device)
-            with _on(cat.device):
-                nbytes = _ws_bytes("ddpm_fuse_conv_bwd_weight_workspace_bytes", n, c, h, w, dt)
-                ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=cat.device)
-                code = lib.ddpm_fuse_conv_bwd_weight(_ptr(cat), _ptr(grad_out), _ptr(gw), _ptr(gb),
-                                                     _ptr(ws), nbytes, n, c, h, w, dt, _stream(cat))
-            if code == _lib.STATUS_UNSUPPORTED:
-                _, gw, gb = torch.ops.aten.convolution_backward(
-                    grad_out, cat, weight, [c] if ctx.has_bias else None, [1, 1], [1, 1], [1, 1],
-                    False, [0, 0], 1, [False, need_w, need_b])
-            else:
-                _lib.check(code, "ddpm_fuse_conv_bwd_weight")
-            grad_w = gw if need_w else None
-            grad_b = gb if need_b else None
-        return grad_cat, grad_w, grad_b
+        return _fuse_conv_backward(cat, weight, ctx.has_bias, _as(grad_out, cat.dtype),
+                                   ctx.needs_input_grad, _dt(cat))
 
 
 def fuse_conv3x3(cat, weight, bias=None):
@@ -547,8 +570,106 @@ def fuse_conv3x3(cat, weight, bias=None):
     return torch.nn.functional.conv2d(cat, weight, bias, padding=1)
 
 
+# ---------------------------------------------------------------------------
+# Generator + filter + concat + fuse convolution, fp32 concat in pair planes
+# ---------------------------------------------------------------------------
+def fused_ddpm_supported(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, kernel_size,
+                         dilations) -> bool:
+    """Whether :func:`fused_ddpm` takes this call: fp32 throughout, a ROCm
+    device, the fused generator kernels' coverage (:func:`generator_supported`),
+    C % 16 == 0 (whole 32-plane chunks of the concat), the HIP fuse
+    convolution's coverage and weight shapes of DDPM(C, K)."""
+    if x.dtype != torch.float32 or x.ndim != 4 or not x.is_cuda:
+        return False
+    n, c, h, w = x.shape
+    k = int(kernel_size)
+    if c % 16 != 0 or tuple(y.shape) != tuple(x.shape) or y.device != x.device:
+        return False
+    g = 3 * c * k * k
+    if gen_bias is None or tuple(gen_weight.shape) != (g, c, 1, 1) or tuple(gen_bias.shape) != (g,):
+        return False
+    if tuple(fuse_weight.shape) != (c, 4 * c, 3, 3):
+        return False
+    if fuse_bias is not None and tuple(fuse_bias.shape) != (c,):
+        return False
+    if any(t is not None and (t.dtype != torch.float32 or t.device != x.device)
+           for t in (y, gen_weight, gen_bias, fuse_weight, fuse_bias)):
+        return False
+    if not generator_supported(c, k, dilations, x.shape, x.dtype):
+        return False
+    return 4 * c * h * w * 4 <= 2**31 - 1
+
+
+def _pair_forward(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, k, dil):
+    """ddpm_gen_fwd writing the concat as pair planes, then
+    ddpm_fuse_conv_fwd reading them; returns (out, concat)."""
+    n, c, h, w = x.shape
+    cat = torch.empty((n, 4 * c, h, w), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    with _on(x.device):
+        code = lib.ddpm_gen_fwd(_ptr(x), _ptr(y), _ptr(gen_weight), _ptr(gen_bias), _ptr(cat),
+                                n, c, h, w, k, *dil, _PAIR_PLANES, _stream(x))
+    _lib.check(code, "ddpm_gen_fwd")
+    return _fuse_conv_forward(cat, fuse_weight, fuse_bias, _PAIR_PLANES), cat
+
+
+class _FusedDDPM(torch.autograd.Function):
+    """The module's GPU forward for fp32 on the fused route: the generator
+    kernel writes the concat as pair planes, so neither the fuse convolution
+    nor its weight gradient splits fp32 concat values into bf16 halves per
+    use.  Backward: the fuse convolution's input gradient (a plain fp32
+    concat gradient) and weight / bias gradients, then the generator op's
+    four gradients by recompute, as the separate ops compute them."""
+
+    @staticmethod
+    def forward(ctx, x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, kernel_size, dilations):
+        out, cat = _pair_forward(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, kernel_size,
+                                 dilations)
+        ctx.save_for_backward(x, y, gen_weight, gen_bias, cat, fuse_weight)
+        ctx.has_bias = fuse_bias is not None
+        ctx.kernel_size = kernel_size
+        ctx.dilations = dilations
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, y, gen_weight, gen_bias, cat, fuse_weight = ctx.saved_tensors
+        needs = ctx.needs_input_grad
+        need_gen = any(needs[:4])
+        grad_cat, grad_fw, grad_fb = _fuse_conv_backward(
+            cat, fuse_weight, ctx.has_bias, _as(grad_out, torch.float32).contiguous(),
+            (need_gen, needs[4], needs[5]), _PAIR_PLANES)
+        del cat
+        grads = (None,) * 4
+        if need_gen:
+            grads = _generator_backward(x, y, gen_weight, gen_bias, grad_cat, ctx.kernel_size,
+                                        ctx.dilations, needs[:4])
+        return (*grads, grad_fw, grad_fb, None, None)
+
+
+def fused_ddpm(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, kernel_size, dilations):
+    """``fuse_conv3x3(fused_generator_dynamic_cat(x, y, ...), fuse_weight,
+    fuse_bias)`` for fp32 shapes of :func:`fused_ddpm_supported`, with the
+    concat kept in pair planes between the two (the result differs from the
+    separate ops only by the fuse convolution's summation order)."""
+    k = _check_kernel_size(kernel_size)
+    dil = _check_dilations(dilations)
+    if not fused_ddpm_supported(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, k, dil):
+        raise ValueError("fused_ddpm: shapes or dtypes outside fused_ddpm_supported")
+    x, y = x.contiguous(), y.contiguous()
+    gen_weight, gen_bias = gen_weight.contiguous(), gen_bias.contiguous()
+    fuse_weight = fuse_weight.contiguous()
+    fuse_bias = fuse_bias.contiguous() if fuse_bias is not None else None
+    tensors = (x, y, gen_weight, gen_bias, fuse_weight, fuse_bias)
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        return _FusedDDPM.apply(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, k, dil)
+    return _pair_forward(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, k, dil)[0]
+
+
 __all__ = [
     "fuse_conv3x3",
+    "fused_ddpm",
+    "fused_ddpm_supported",
     "fuse_conv_supported",
     "fused_dynamic_cat",
     "fused_generator_dynamic_cat",

@@ -13,7 +13,15 @@
  *   bias, grad_bias             [3*C*K*K]
  *   out / grad_out ("cat")      [N][4*C][H][W] = [x, d0, d1, d2]
  *
- * dtype codes: 0 = float32, 1 = bfloat16, 2 = float16.
+ * dtype codes: 0 = float32, 1 = bfloat16, 2 = float16; 3 = float32 whose
+ * concat ("cat") is stored as bf16 pair planes -- per 32-plane chunk, plane
+ * j < 16 holds the hi halves of channels (2j, 2j+1) (low / high 16 bits) and
+ * plane 16 + j their lo halves, hi = the top 16 bits of the fp32 pattern and
+ * lo = the remainder rounded to nearest even (the split the fp32 MFMA path
+ * makes of its operands).  Code 3 is taken where noted: by ddpm_gen_fwd
+ * (writes such a concat; c % 16 == 0), ddpm_fuse_conv_fwd and
+ * ddpm_fuse_conv_bwd_weight (read one; c % 8 == 0) and their workspace
+ * queries (as code 0); the other tensors of those calls are float32.
  * Dilations d0, d1, d2 are the three branch dilations ((1, 3, 5) in DDPM).
  * The neighbour of (h, w) for tap (ki, kj) at dilation d is
  * (h + (ki - K/2) d, w + (kj - K/2) d), zero outside the image.
@@ -38,7 +46,7 @@ extern "C" {
 #define DDPM_DTYPE_BF16 1
 #define DDPM_DTYPE_F16 2
 
-/* ABI version of this header (4). */
+/* ABI version of this header (5: dtype code 3). */
 int ddpm_abi_version(void);
 
 /* Text for any status code returned by this library (static storage). */
@@ -126,7 +134,8 @@ int ddpm_filter_bwd_k(const void* x, const void* grad_out, void* grad_kernels, i
 /* ---- fused generator (all tensors share `dtype`) ---------------------- */
 
 /* out = [x, d0, d1, d2] with the dynamic taps generated on chip
- * (gen = weight . y + bias, rounded to `dtype` for bf16/f16).
+ * (gen = weight . y + bias, rounded to `dtype` for bf16/f16); dtype 3 writes
+ * fp32 results as pair planes (c % 16 == 0, else kUnsupported).
  * Replaces _generator_dynamic_cat_fwd + _launch_generator_dynamic_cat
  * (_triton_kernels.py:268-420, 873-908). */
 int ddpm_gen_fwd(const void* x, const void* y, const void* weight, const void* bias, void* out,
@@ -246,6 +255,7 @@ int64_t ddpm_fuse_conv_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t 
  *                    cat[n][ci][h+ki-1][w+kj-1]  (zero padding), accumulated in
  * fp32 (fp32 operands as three bf16 MFMA products) and rounded once to
  * `dtype`.  cat: [n][4c][h][w]; weight: [c][4c][3][3]; bias: [c] or NULL.
+ * dtype 3: cat in pair planes (c % 8 == 0), fp32 weight, bias and out.
  * Replaces the cuDNN forward of self.fuse (triton_impl.py:294, 392). */
 int ddpm_fuse_conv_fwd(const void* cat, const void* weight, const void* bias, void* out,
                        void* workspace, int64_t workspace_bytes, int64_t n, int64_t c, int64_t h,
@@ -270,7 +280,8 @@ int64_t ddpm_fuse_conv_bwd_weight_workspace_bytes(int64_t n, int64_t c, int64_t 
  * grad_bias[co] = sum grad_out[n][co][h][w]; fp32 accumulation in at most 16
  * pixel splits summed in split order (deterministic), rounded once to
  * `dtype`; an empty batch writes zeros.  c <= 128 (kUnsupported beyond; above
- * 64 output planes workgroups take halves of 64).
+ * 64 output planes workgroups take halves of 64).  dtype 3: cat in pair
+ * planes (c % 8 == 0), bit-identical to code 0 on the same values.
  * Replaces the cuDNN backward-filter convolution of self.fuse (autograd of
  * nn.Conv2d, triton_impl.py:294, 392). */
 int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, void* grad_weight,
