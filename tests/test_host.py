@@ -120,6 +120,31 @@ def test_entry_points_validate_arguments_before_touching_the_device():
     # empty tensors are a no-op
     assert lib.ddpm_filter_fwd(null, null, null, 0, 4, 4, 4, 3, 1, 3, 5, 0, 0, null) == 0
     assert lib.ddpm_gen_kernels(null, null, null, null, 0, 64, 8, 8, 5, 1, null) == 0
+    # dtype code 3 (fp32 pair-plane concat): whole 32-plane chunks only, and
+    # only where an entry point documents it
+    assert lib.ddpm_gen_fwd(null, null, null, null, null, 1, 24, 4, 4, 3, 1, 3, 5, 3, null) == 10002
+    assert lib.ddpm_gen_fwd(null, null, null, null, null, 1, 32, 4, 4, 3, 1, 3, 5, 3, null) == 10001
+    assert lib.ddpm_fuse_conv_fwd(null, null, null, null, null, 0, 1, 12, 4, 4, 3, null) == 10002
+    assert lib.ddpm_fuse_conv_bwd_weight(null, null, null, null, null, 0, 1, 12, 4, 4, 3, null) == 10002
+    assert lib.ddpm_fuse_conv_workspace_bytes(1, 64, 32, 32, 3) == lib.ddpm_fuse_conv_workspace_bytes(1, 64, 32, 32, 0)
+    assert lib.ddpm_filter_fwd(null, null, null, 1, 1, 4, 4, 3, 1, 3, 5, 3, 3, null) == 10001
+
+
+def test_fused_ddpm_takes_rocm_fp32_only():
+    """ops.fused_ddpm (the module's fp32 pair-plane route) is refused for CPU
+    tensors and other dtypes; the module's CPU branch never reaches it."""
+    from dynamicconvolutionoperator_amd import ops
+
+    c, k = 16, 3
+    x = torch.randn(1, c, 8, 8)
+    gw, gb = torch.randn(3 * c * k * k, c, 1, 1), torch.randn(3 * c * k * k)
+    fw, fb = torch.randn(c, 4 * c, 3, 3), torch.randn(c)
+    assert not ops.fused_ddpm_supported(x, x, gw, gb, fw, fb, k, (1, 3, 5))
+    assert not ops.fused_ddpm_supported(x.bfloat16(), x.bfloat16(), gw, gb, fw, fb, k, (1, 3, 5))
+    with pytest.raises(ValueError):
+        ops.fused_ddpm(x, x, gw, gb, fw, fb, k, (1, 3, 5))
+    m = module.DDPM(c, k)
+    assert m(x, x).shape == x.shape
 
 
 class _FakeTensor:
