@@ -35,7 +35,7 @@ per-tile checkpoint at fp32, triton_impl.py:169-244,381-391; Unfold training
 at bf16, :373-376) and the Unfold oracle, warm-up 3 / repeats 20
 (bench.py:138-165 of the reference), each leg capped in time.
 
-Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 60]
 """
 
 from __future__ import annotations
@@ -59,7 +59,7 @@ def parse_args():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=60)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--quick", action="store_true", help="skip the secondary measurements")
     p.add_argument(
