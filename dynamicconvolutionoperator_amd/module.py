@@ -43,7 +43,7 @@ def _load_hip_ops():
 
     _lib.load()
     return (ops.fused_dynamic_cat, ops.fused_generator_dynamic_cat, ops.generator_supported,
-            ops._generate, ops.fuse_conv3x3, ops.fused_ddpm, ops.fused_ddpm_supported)
+            ops._generate, ops.fuse_conv3x3, ops._fused_ddpm_checked, ops.fused_ddpm_supported)
 
 
 def _check_inputs(x: torch.Tensor, y: torch.Tensor, channels: int) -> None:
@@ -196,7 +196,7 @@ class DDPM(nn.Module):
                 self.kernel_size, self.dilations)
         if not supported(*args) or self._route(x, y, ops[2]) != "fused":
             return None
-        return fused_ddpm(*args)
+        return fused_ddpm(*args)  # the arguments as checked just now
 
     def forward(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         _check_inputs(x, y, self.dim)

@@ -656,6 +656,12 @@ def fused_ddpm(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, kernel_size, 
     dil = _check_dilations(dilations)
     if not fused_ddpm_supported(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, k, dil):
         raise ValueError("fused_ddpm: shapes or dtypes outside fused_ddpm_supported")
+    return _fused_ddpm_checked(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, k, dil)
+
+
+def _fused_ddpm_checked(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, k, dil):
+    """:func:`fused_ddpm` for arguments :func:`fused_ddpm_supported` has
+    accepted (k an int, dil a tuple of three ints)."""
     x, y = x.contiguous(), y.contiguous()
     gen_weight, gen_bias = gen_weight.contiguous(), gen_bias.contiguous()
     fuse_weight = fuse_weight.contiguous()
