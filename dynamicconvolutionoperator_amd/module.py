@@ -13,11 +13,18 @@ with the GPU route backed by HIP kernels for gfx950:
 
 The final 3x3 ``fuse`` convolution is a plain ``nn.Conv2d`` (its parameters and
 state-dict keys are the reference's); on ROCm tensors its forward and
-gradients run as HIP MFMA kernels (``fuse_conv_backend = "library"`` selects
-MIOpen through ``self.fuse`` instead).  For fp32 on the fused route with
-C % 16 == 0, generator, filter, concat and fuse convolution run as one
-autograd op (``ops.fused_ddpm``) whose concat is stored as bf16 pair planes,
-already split the way the fuse convolution's fp32 MFMA products need it.
+gradients run as HIP MFMA kernels while ``self.fuse`` is that convolution
+unmodified (3x3, stride 1, zero padding 1, no dilation or groups, no hooks);
+anything else -- hooks such as the old ``weight_norm`` / ``spectral_norm``,
+another ``padding_mode``, a replaced module -- is honoured by calling
+``self.fuse(cat)`` as the reference always does (triton_impl.py:392).
+``fuse_conv_backend = "library"`` selects MIOpen through ``self.fuse`` always.
+The materialized route likewise calls ``self.generator(y)`` unless the
+generator is the constructor's unmodified 1x1 convolution
+(triton_impl.py:340-347).  For fp32 on the fused route with C % 16 == 0,
+generator, filter, concat and fuse convolution run as one pair of autograd
+ops (``ops.fused_ddpm``) whose concat is stored as bf16 pair planes, already
+split the way the fuse convolution's fp32 MFMA products need it.
 """
 
 from __future__ import annotations
@@ -44,6 +51,39 @@ def _load_hip_ops():
     _lib.load()
     return (ops.fused_dynamic_cat, ops.fused_generator_dynamic_cat, ops.generator_supported,
             ops._generate, ops.fuse_conv3x3, ops._fused_ddpm_checked, ops.fused_ddpm_supported)
+
+
+def _module_hooks_set(m: nn.Module) -> bool:
+    """Whether calling ``m`` would run a hook: its own forward / backward
+    hooks or the global module hooks."""
+    from torch.nn.modules import module as _m
+
+    return bool(
+        m._forward_hooks or m._forward_pre_hooks or m._backward_hooks or m._backward_pre_hooks
+        or _m._global_forward_hooks or _m._global_forward_pre_hooks
+        or _m._global_backward_hooks or _m._global_backward_pre_hooks
+    )
+
+
+def plain_conv(m: nn.Module, kernel_size: int) -> bool:
+    """Whether ``m`` computes exactly ``F.conv2d(t, m.weight, m.bias,
+    padding=kernel_size // 2)``, so a kernel may run that convolution from
+    ``m.weight`` / ``m.bias`` in place of calling ``m``: an ``nn.Conv2d``
+    whose forward is Conv2d's own (parametrized weights, as from
+    ``torch.nn.utils.parametrizations``, qualify: ``m.weight`` evaluates
+    them), a square ``kernel_size`` kernel, stride 1, zero padding of
+    ``kernel_size // 2``, no dilation or groups, and no hooks."""
+    if not isinstance(m, nn.Conv2d) or m.transposed:
+        return False
+    cls = type(m)
+    if cls.forward is not nn.Conv2d.forward or cls._conv_forward is not nn.Conv2d._conv_forward:
+        return False
+    pad = kernel_size // 2
+    if (m.kernel_size != (kernel_size, kernel_size) or m.stride != (1, 1)
+            or m.padding != (pad, pad) or m.dilation != (1, 1) or m.groups != 1
+            or m.padding_mode != "zeros"):
+        return False
+    return not _module_hooks_set(m)
 
 
 def _check_inputs(x: torch.Tensor, y: torch.Tensor, channels: int) -> None:
@@ -141,7 +181,7 @@ class DDPM(nn.Module):
         # the generator 1x1 convolution: the HIP MFMA kernel where it applies;
         # under autocast the Conv2d runs in the autocast dtype, as the
         # reference's does (the filter's output dtype follows the kernels')
-        if torch.is_autocast_enabled(y.device.type):
+        if torch.is_autocast_enabled(y.device.type) or not plain_conv(self.generator, 1):
             kernels = self.generator(y)
         else:
             kernels = generate(y, self.generator.weight, self.generator.bias, self.kernel_size)
@@ -174,21 +214,29 @@ class DDPM(nn.Module):
             self.recompute and self.training,
         )
 
+    def _hip_fuse(self) -> bool:
+        """Whether the HIP kernels may stand in for ``self.fuse``: the "hip"
+        backend and ``self.fuse`` the plain 3x3 zero-padded convolution
+        without hooks (:func:`plain_conv`); otherwise ``self.fuse`` is called,
+        as the reference does (triton_impl.py:392)."""
+        return self.fuse_conv_backend == "hip" and plain_conv(self.fuse, 3)
+
     def _cuda_fuse(self, cat_out: torch.Tensor) -> torch.Tensor:
-        """The fuse convolution of a ROCm concat: the HIP kernels unless the
-        backend is "library" or autocast is on (the Conv2d then runs in the
-        autocast dtype, as the reference's does)."""
-        if self.fuse_conv_backend == "hip" and not torch.is_autocast_enabled(cat_out.device.type):
+        """The fuse convolution of a ROCm concat: the HIP kernels where
+        :meth:`_hip_fuse` allows and autocast is off, else ``self.fuse``
+        (under autocast the Conv2d runs in the autocast dtype, as the
+        reference's does)."""
+        if self._hip_fuse() and not torch.is_autocast_enabled(cat_out.device.type):
             fuse_conv3x3 = _load_hip_ops()[4]
             return fuse_conv3x3(cat_out, self.fuse.weight, self.fuse.bias)
         return self.fuse(cat_out)
 
     def _cuda_pairs(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor | None:
         """fp32 on the fused route with the HIP fuse convolution: generator,
-        filter, concat and fuse convolution as one op whose concat is stored
-        as bf16 pair planes (``ops.fused_ddpm``); ``None`` where it does not
-        apply."""
-        if self.fuse_conv_backend != "hip" or x.dtype != torch.float32:
+        filter, concat and fuse convolution as one pair of ops whose concat is
+        stored as bf16 pair planes (``ops.fused_ddpm``); ``None`` where it
+        does not apply."""
+        if x.dtype != torch.float32 or not self._hip_fuse():
             return None
         ops = _load_hip_ops()
         fused_ddpm, supported = ops[5], ops[6]
@@ -212,4 +260,4 @@ class DDPM(nn.Module):
         return self.fuse(cat_out)
 
 
-__all__ = ["DDPM"]
+__all__ = ["DDPM", "plain_conv"]

@@ -258,6 +258,13 @@ def _generator_backward(x, y, weight, bias, grad_out, k, dil, needs):
     grad_x = grad_y = grad_w = grad_b = None
     need_x, need_y = needs[0], needs[1]
     need_wb = needs[2] or needs[3]
+    combined = need_x and need_y and need_wb
+
+    def alloc_y():
+        wsy_bytes = _ws_bytes("ddpm_gen_bwd_y_workspace_bytes", c, k)
+        return (torch.empty_like(y), torch.empty(wsy_bytes, dtype=torch.uint8, device=x.device),
+                wsy_bytes)
+
     with _on(x.device):
         if need_x:
             grad_x = torch.empty_like(x)
@@ -268,12 +275,9 @@ def _generator_backward(x, y, weight, bias, grad_out, k, dil, needs):
             grad_b = torch.empty_like(bias)
             ws_bytes = _ws_bytes("ddpm_gen_bwd_w_workspace_bytes", n, c, h, w, k, dt)
             ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
-        if need_y:
-            grad_y = torch.empty_like(y)
-            wsy_bytes = _ws_bytes("ddpm_gen_bwd_y_workspace_bytes", c, k)
-            wsy = torch.empty(wsy_bytes, dtype=torch.uint8, device=x.device)
         y_pending = need_y
-        if need_x and need_y and need_wb:
+        if combined:
+            grad_y, wsy, wsy_bytes = alloc_y()
             # one call: dY's weight packing and dX's halo reduction run on
             # the CUs dW leaves free
             _lib.check(
@@ -316,6 +320,8 @@ def _generator_backward(x, y, weight, bias, grad_out, k, dil, needs):
             if not needs[3]:
                 grad_b = None
         if y_pending:
+            # allocated once the dX and dW workspaces are released
+            grad_y, wsy, wsy_bytes = alloc_y()
             _lib.check(
                 lib.ddpm_gen_bwd_y(_ptr(x), _ptr(weight), _ptr(grad_out), _ptr(grad_y),
                                    _ptr(wsy), wsy_bytes, n, c, h, w, k, *dil, dt, stream),
@@ -600,9 +606,8 @@ def fused_ddpm_supported(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, ker
     return 4 * c * h * w * 4 <= 2**31 - 1
 
 
-def _pair_forward(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, k, dil):
-    """ddpm_gen_fwd writing the concat as pair planes, then
-    ddpm_fuse_conv_fwd reading them; returns (out, concat)."""
+def _pair_concat(x, y, gen_weight, gen_bias, k, dil):
+    """ddpm_gen_fwd writing the concat as pair planes (dtype code 3)."""
     n, c, h, w = x.shape
     cat = torch.empty((n, 4 * c, h, w), dtype=torch.float32, device=x.device)
     lib = _lib.load()
@@ -610,41 +615,51 @@ def _pair_forward(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, k, dil):
         code = lib.ddpm_gen_fwd(_ptr(x), _ptr(y), _ptr(gen_weight), _ptr(gen_bias), _ptr(cat),
                                 n, c, h, w, k, *dil, _PAIR_PLANES, _stream(x))
     _lib.check(code, "ddpm_gen_fwd")
-    return _fuse_conv_forward(cat, fuse_weight, fuse_bias, _PAIR_PLANES), cat
+    return cat
 
 
-class _FusedDDPM(torch.autograd.Function):
-    """The module's GPU forward for fp32 on the fused route: the generator
-    kernel writes the concat as pair planes, so neither the fuse convolution
-    nor its weight gradient splits fp32 concat values into bf16 halves per
-    use.  Backward: the fuse convolution's input gradient (a plain fp32
-    concat gradient) and weight / bias gradients, then the generator op's
-    four gradients by recompute, as the separate ops compute them."""
+class _PairConcat(torch.autograd.Function):
+    """Generator + filter + concat with the fp32 concat written as pair
+    planes.  The output is an encoding only :class:`_PairFuse` reads; the
+    gradient arriving for it is the plain fp32 gradient of the concat values,
+    so the backward is the generator op's (recompute from x, y, W, b)."""
 
     @staticmethod
-    def forward(ctx, x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, kernel_size, dilations):
-        out, cat = _pair_forward(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, kernel_size,
-                                 dilations)
-        ctx.save_for_backward(x, y, gen_weight, gen_bias, cat, fuse_weight)
-        ctx.has_bias = fuse_bias is not None
+    def forward(ctx, x, y, gen_weight, gen_bias, kernel_size, dilations):
+        cat = _pair_concat(x, y, gen_weight, gen_bias, kernel_size, dilations)
+        ctx.save_for_backward(x, y, gen_weight, gen_bias)
         ctx.kernel_size = kernel_size
         ctx.dilations = dilations
+        return cat
+
+    @staticmethod
+    def backward(ctx, grad_cat):
+        x, y, gen_weight, gen_bias = ctx.saved_tensors
+        grads = _generator_backward(x, y, gen_weight, gen_bias, _as(grad_cat, torch.float32),
+                                    ctx.kernel_size, ctx.dilations, ctx.needs_input_grad[:4])
+        return (*grads, None, None)
+
+
+class _PairFuse(torch.autograd.Function):
+    """The fuse convolution of a pair-plane concat: forward and weight / bias
+    gradients read the pair planes; the input gradient is a plain fp32
+    concat gradient.  A node of its own, so autograd releases the saved
+    concat as soon as this backward has run, before the generator's
+    backward allocates its buffers."""
+
+    @staticmethod
+    def forward(ctx, cat, fuse_weight, fuse_bias):
+        out = _fuse_conv_forward(cat, fuse_weight, fuse_bias, _PAIR_PLANES)
+        ctx.save_for_backward(cat, fuse_weight)
+        ctx.has_bias = fuse_bias is not None
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
-        x, y, gen_weight, gen_bias, cat, fuse_weight = ctx.saved_tensors
-        needs = ctx.needs_input_grad
-        need_gen = any(needs[:4])
-        grad_cat, grad_fw, grad_fb = _fuse_conv_backward(
-            cat, fuse_weight, ctx.has_bias, _as(grad_out, torch.float32).contiguous(),
-            (need_gen, needs[4], needs[5]), _PAIR_PLANES)
-        del cat
-        grads = (None,) * 4
-        if need_gen:
-            grads = _generator_backward(x, y, gen_weight, gen_bias, grad_cat, ctx.kernel_size,
-                                        ctx.dilations, needs[:4])
-        return (*grads, grad_fw, grad_fb, None, None)
+        cat, fuse_weight = ctx.saved_tensors
+        return _fuse_conv_backward(cat, fuse_weight, ctx.has_bias,
+                                   _as(grad_out, torch.float32), ctx.needs_input_grad,
+                                   _PAIR_PLANES)
 
 
 def fused_ddpm(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, kernel_size, dilations):
@@ -668,8 +683,10 @@ def _fused_ddpm_checked(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, k, d
     fuse_bias = fuse_bias.contiguous() if fuse_bias is not None else None
     tensors = (x, y, gen_weight, gen_bias, fuse_weight, fuse_bias)
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
-        return _FusedDDPM.apply(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, k, dil)
-    return _pair_forward(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, k, dil)[0]
+        cat = _PairConcat.apply(x, y, gen_weight, gen_bias, k, dil)
+        return _PairFuse.apply(cat, fuse_weight, fuse_bias)
+    cat = _pair_concat(x, y, gen_weight, gen_bias, k, dil)
+    return _fuse_conv_forward(cat, fuse_weight, fuse_bias, _PAIR_PLANES)
 
 
 __all__ = [

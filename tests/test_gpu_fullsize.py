@@ -3,7 +3,8 @@
 * 256x256 fused recompute training, fp32 and bf16, against the float64 CPU
   oracle (forward and all gradients);
 * 128x128 fused inference, fp32;
-* K=5 128x128 bf16 materialized inference and training, fp32 training;
+* K=5 128x128 bf16 materialized inference and training (output also
+  against the oracle run in bf16), fp32 training;
 * size-independent adjoint identities of the fused operator at 256x256:
   the fused op is linear in x and affine in y, W and b, so
   <F(x + v) - F(x), g> = <v, dX(g)> and likewise for y, W and b; both sides
@@ -16,7 +17,7 @@ import torch
 from dynamicconvolutionoperator_amd import ops
 from tests.gpu_helpers import (DEV, DIL, assert_max_abs, default_generator_params, max_abs_bound,
                                randn, record_errors, say)
-from tests.test_gpu_module import check_training, make_models
+from tests.test_gpu_module import check_bf16_output, check_training, make_models
 
 pytestmark = pytest.mark.gpu
 
@@ -53,8 +54,10 @@ def test_k5_128_bf16_materialized():
     with torch.inference_mode():
         expected = ref(x.double(), y.double())
         actual = cand(x.to(DEV), y.to(DEV))
-    stats = assert_max_abs(actual, expected, max_abs_bound(torch.bfloat16, 5), "out K5 bf16")
-    record_errors("infer N=1 C=64 128x128 K=5 bfloat16 materialized", {"out": stats})
+    errors = {"out": assert_max_abs(actual, expected, max_abs_bound(torch.bfloat16, 5),
+                                    "out K5 bf16")}
+    check_bf16_output(actual, x, y, 64, 5, errors)
+    record_errors("infer N=1 C=64 128x128 K=5 bfloat16 materialized", errors)
     check_training(64, 128, 128, 5, torch.bfloat16, fused=False, n=1, seed=23)
 
 

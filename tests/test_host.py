@@ -247,3 +247,66 @@ def test_gpu_tensors_fail_loudly_without_the_library(monkeypatch):
 def test_public_api_names():
     for name in ("DDPM", "fused_dynamic_cat", "fused_generator_dynamic_cat"):
         assert hasattr(dco, name)
+
+
+def test_plain_conv_guard():
+    """The HIP kernels stand in for self.fuse / self.generator only while they
+    are the constructor's plain convolutions without hooks; otherwise the
+    module calls them, as the reference does (triton_impl.py:340-347, 392)."""
+    import warnings
+
+    from torch import nn
+    from torch.nn.utils import parametrizations
+
+    m = module.DDPM(8, 3)
+    assert m._hip_fuse() and module.plain_conv(m.generator, 1)
+    m.fuse_conv_backend = "library"
+    assert not m._hip_fuse()
+    m.fuse_conv_backend = "hip"
+    # attributes of the convolution
+    for kwargs in ({"padding": 1, "padding_mode": "reflect"}, {"padding": 1, "padding_mode": "circular"},
+                   {"padding": 2, "dilation": 2}, {"padding": 1, "stride": 2},
+                   {"padding": 1, "groups": 4}, {"padding": 0}, {"padding": "same"}):
+        m.fuse = nn.Conv2d(32, 8, 3, **kwargs)
+        assert not m._hip_fuse(), kwargs
+    m.fuse = nn.Conv2d(32, 8, 3, 1, 1)
+    assert m._hip_fuse()
+    # hooks on the module
+    h = m.fuse.register_forward_hook(lambda *a: None)
+    assert not m._hip_fuse()
+    h.remove()
+    h = m.fuse.register_forward_pre_hook(lambda *a: None)
+    assert not m._hip_fuse()
+    h.remove()
+    h = m.fuse.register_full_backward_hook(lambda *a: None)
+    assert not m._hip_fuse()
+    h.remove()
+    assert m._hip_fuse()
+    # global module hooks
+    h = nn.modules.module.register_module_forward_hook(lambda *a: None)
+    try:
+        assert not m._hip_fuse()
+    finally:
+        h.remove()
+    # weight_norm: the old API is a forward pre-hook, the parametrization is not
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore", FutureWarning)
+        torch.nn.utils.weight_norm(m.fuse)
+    assert not m._hip_fuse()
+    m.fuse = parametrizations.weight_norm(nn.Conv2d(32, 8, 3, 1, 1))
+    assert m._hip_fuse()
+
+    # a subclass with its own forward, or another module entirely
+    class Scaled(nn.Conv2d):
+        def forward(self, t):
+            return super().forward(t) * 2
+
+    m.fuse = Scaled(32, 8, 3, 1, 1)
+    assert not m._hip_fuse()
+    m.fuse = nn.Sequential(nn.Conv2d(32, 8, 3, 1, 1))
+    assert not m._hip_fuse()
+    # the generator on the materialized route
+    m.generator.register_forward_hook(lambda *a: None)
+    assert not module.plain_conv(m.generator, 1)
+    assert not module.plain_conv(nn.Conv2d(8, 216, 3, padding=1), 1)
+    assert module.plain_conv(nn.Conv2d(8, 216, 1), 1)
