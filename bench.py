@@ -19,10 +19,13 @@ Also reported on the same line (``extra``):
     256x256, rotating buffer sets so repeats do not run out of the MALL);
   * 128x128 C=64 K=3 fp32 inference: filter-only ms and GB/s and fused
     end-to-end ms (gpu_bench.py:94-118);
-  * K=5 128x128 C=64 bf16 on the materialized route: inference and
-    forward+backward ms (gpu_bench.py:265-345);
+  * K=5 128x128 C=64 bf16: inference on the fused forward and on the
+    materialized route, forward+backward on the materialized route
+    (gpu_bench.py:265-345), and the materialized route's 256x256 training
+    step beside the fused one (fp32 and bf16);
   * peak temporary memory of the fused and Unfold training steps (C = 64 fp32
-    and bf16, C = 128 fp32), each route in its own child process started
+    and bf16, C = 128 fp32) and of K=5 128x128 bf16 inference (fused forward
+    vs materialized kernels), each route in its own child process started
     before this process uses the GPU, with gradients released before the
     baseline is read (gpu_memory_bench.py:47-76);
   * the Unfold route's GPU training-step and inference times (256x256 fp32
@@ -76,7 +79,9 @@ def parse_args():
                    "rotate through (2 keeps a 150 MB tensor from being re-read out of the MALL)")
     p.add_argument("--peak-mem", nargs=2, metavar=("ROUTE", "DTYPE"),
                    help="child mode: peak temporary memory of one training step of ROUTE "
-                   "(fused|unfold) in DTYPE (float32|bfloat16); prints one JSON line")
+                   "(fused|materialized|unfold) in DTYPE (float32|bfloat16), or of one K=5 "
+                   "128x128 inference (k5-infer-fused|k5-infer-materialized); prints one JSON "
+                   "line")
     p.add_argument("--channels", type=int, default=C, help="with --peak-mem: C")
     p.add_argument("--cpu-budget", type=float, default=12.0,
                    help="seconds per CPU-baseline leg at most (after its warm-up)")
@@ -362,16 +367,31 @@ def peak_mem_child(route, dtype_name, channels=C, warmup=2):
     import torch
 
     dtype = {"float32": torch.float32, "bfloat16": torch.bfloat16}[dtype_name]
-    module = make_module(dtype, channels=channels)
-    x, y = make_inputs(dtype, channels=channels)
-    params = list(module.parameters())
+    if route.startswith("k5-infer-"):
+        # K=5 128x128 inference: the fused forward vs the materialized route
+        from dynamicconvolutionoperator_amd import DDPM
 
-    def step():
-        module.zero_grad(set_to_none=True)
-        x.grad = None
-        y.grad = None
-        out = module(x, y) if route == "fused" else unfold_route_step(params, x, y)
-        out.square().mean().backward()
+        torch.manual_seed(21)
+        module = DDPM(channels, 5, fused_generator_inference=route == "k5-infer-fused")
+        module = module.cuda().to(dtype).eval()
+        torch.manual_seed(20)
+        x = torch.randn(1, channels, 128, 128, device="cuda", dtype=dtype)
+        y = torch.randn_like(x)
+
+        def step():
+            with torch.inference_mode():
+                module(x, y)
+    else:
+        module = make_module(dtype, channels=channels, fused=route != "materialized")
+        x, y = make_inputs(dtype, channels=channels)
+        params = list(module.parameters())
+
+        def step():
+            module.zero_grad(set_to_none=True)
+            x.grad = None
+            y.grad = None
+            out = module(x, y) if route != "unfold" else unfold_route_step(params, x, y)
+            out.square().mean().backward()
 
     for _ in range(warmup):
         step()
@@ -412,6 +432,17 @@ def peak_memory_children():
                                        "fused_over_unfold": res["fused"] / res["unfold"],
                                        "method": "own process per route, gradients released "
                                        "before the baseline (gpu_memory_bench.py:47-76)"}
+    # K=5 128x128 bf16 inference: fused forward vs materialized kernels
+    res = {}
+    for route in ("k5-infer-fused", "k5-infer-materialized"):
+        proc = subprocess.run(
+            [sys.executable, os.path.abspath(__file__), "--peak-mem", route, "bfloat16"],
+            capture_output=True, text=True, timeout=300,
+        )
+        if proc.returncode != 0:
+            raise RuntimeError(f"peak-memory child {route} failed:\n{proc.stderr[-2000:]}")
+        res[route[9:]] = json.loads(proc.stdout.strip().splitlines()[-1])["temporary_peak_mib"]
+    out["peak_temp_mib_k5_128_bf16_infer"] = res
     return out
 
 
@@ -737,9 +768,21 @@ def main():
         x, y = make_inputs(torch.bfloat16)
         extra["train_ms_bf16"] = time_loop(lambda: train_step(module, x, y), args.steps, args.warmup)
         extra["kernels_bf16_train"] = kernel_breakdown(lib, timer, module, x, y)
+        # the materialized route's training step at the same shape
+        # (fused_generator_training=False; gpu_bench.py:265-345 times the two
+        # routes side by side)
+        module.fused_generator_training = False
+        extra["materialized_train_ms_bf16"] = time_loop(lambda: train_step(module, x, y), args.steps,
+                                                        args.warmup)
+        module.fused_generator_training = True
         module.eval()
         with torch.inference_mode():
             extra["infer_ms_bf16"] = time_loop(lambda: module(x, y), args.steps, args.warmup)
+        del module, x, y
+        module = make_module(torch.float32, fused=False)
+        x, y = make_inputs(torch.float32)
+        extra["materialized_train_ms_fp32"] = time_loop(lambda: train_step(module, x, y), args.steps,
+                                                        args.warmup)
         del module, x, y
         module = make_module(torch.float32).eval()
         x, y = make_inputs(torch.float32, grad=False)
@@ -776,7 +819,9 @@ def main():
         hip_graph["128_fp32"] = graph_cases(module, x, y, args.steps, args.warmup)
         del module, x, y
 
-        # ---- K=5 128x128 C=64 bf16, materialized route: inference, fwd+bwd
+        # ---- K=5 128x128 C=64 bf16: training on the materialized route,
+        #      inference on the fused forward (the module's default) and on
+        #      the materialized route
         from dynamicconvolutionoperator_amd import DDPM
 
         torch.manual_seed(21)
@@ -787,7 +832,11 @@ def main():
         module.eval()
         with torch.inference_mode():
             c4["infer_ms"] = time_loop(lambda: module(x, y), args.steps, args.warmup)
-        c4["route"] = "materialized (HIP generator GEMMs + HIP filter)"
+            module.fused_generator_inference = False
+            c4["infer_ms_materialized"] = time_loop(lambda: module(x, y), args.steps, args.warmup)
+            module.fused_generator_inference = True
+        c4["route"] = ("training: materialized (HIP generator GEMMs + HIP filter); inference: fused "
+                       "generator forward (infer_ms) or materialized (infer_ms_materialized)")
         hip_graph["k5_128_bf16"] = graph_cases(module, x.detach(), y.detach(), args.steps, args.warmup)
         hip_graph["note"] = ("eager vs HIP-graph replay of the same module: inference, and forward + "
                              "backward from a fixed output gradient (no loss kernels); ms per call")

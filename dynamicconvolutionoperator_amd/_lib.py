@@ -27,6 +27,7 @@ SIGNATURES: dict[str, tuple[list, type]] = {
     "ddpm_abi_version": ([], _I),
     "ddpm_status_string": ([_I], ctypes.c_char_p),
     "ddpm_gen_supported": ([_L, _I, _I], _I),
+    "ddpm_gen_fwd_supported": ([_L, _I, _I], _I),
     "ddpm_gen_kernels_supported": ([_L, _L, _L, _L, _I, _I], _I),
     "ddpm_gen_kernels": ([_P, _P, _P, _P, _L, _L, _L, _L, _I, _I, _P], _I),
     "ddpm_gen_kernels_bwd_w_workspace_bytes": ([_L, _L, _L, _L, _I], _L),
@@ -57,7 +58,7 @@ SIGNATURES: dict[str, tuple[list, type]] = {
 }
 
 
-ABI_VERSION = 5  # include/ddpm_hip.h
+ABI_VERSION = 6  # include/ddpm_hip.h
 
 
 class HipLibraryError(RuntimeError):

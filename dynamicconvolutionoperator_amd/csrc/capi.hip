@@ -28,7 +28,7 @@ int allow_dynamic_lds(const void* fn, size_t bytes) {
 
 using namespace ddpm;
 
-extern "C" int ddpm_abi_version(void) { return 5; }
+extern "C" int ddpm_abi_version(void) { return 6; }
 
 extern "C" const char* ddpm_status_string(int code) {
   switch (code) {
@@ -61,6 +61,25 @@ extern "C" int ddpm_gen_supported(int64_t c, int kernel_size, int max_dilation) 
   if (max_dilation > kGenMaxDil) return 0;
   GenGeom gg;
   if (gen_make_geom(gg, 1, c, 1, 1, kernel_size, max_dilation, max_dilation, max_dilation) != kOk)
+    return 0;
+  TileGeom g;
+  size_t lds = 0;
+  return tile_geom(g, gg, 16, 2, 2, lds) == kOk ? 1 : 0;
+}
+
+// 1 when the fused generator forward alone (inference: ddpm_gen_fwd) handles
+// this channel count, kernel size (1, 3 or 5) and largest dilation, else 0:
+// its halo tile of (16+2R) x (32+2R) pixels x 16 channels (fp32 entries, R =
+// (K/2)*max_dilation) must fit the LDS of one workgroup next to two fp32
+// weight slices and the bias rows.  At K <= 3 and dilations <= 8 this equals
+// ddpm_gen_supported.
+extern "C" int ddpm_gen_fwd_supported(int64_t c, int kernel_size, int max_dilation) {
+  if (c < 1 || c > 128 || max_dilation < 1) return 0;
+  if (!(kernel_size == 1 || kernel_size == 3 || kernel_size == kGenFwdMaxK)) return 0;
+  if (kernel_size == 1) return 1;
+  GenGeom gg;
+  if (gen_make_geom(gg, 1, c, 1, 1, kernel_size, max_dilation, max_dilation, max_dilation,
+                    kGenFwdMaxK) != kOk)
     return 0;
   TileGeom g;
   size_t lds = 0;

@@ -12,10 +12,15 @@ struct GenGeom {
   int cblocks;  // ceil(C/16)
 };
 
-// Validates the shape for the fused kernels (K in {1,3}, C <= 64, dilations
-// >= 1) and fills the geometry.  Returns kOk, kBadArgument or kUnsupported.
+// Validates the shape for the fused kernels (odd K <= kmax: 3 for the
+// recompute backward, 5 for the forward; C <= 128, dilations >= 1) and fills
+// the geometry.  Returns kOk, kBadArgument or kUnsupported.
 int gen_make_geom(GenGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int k, int d0, int d1,
-                  int d2);
+                  int d2, int kmax = 3);
+
+// Largest kernel size of the fused forward (inference; training at larger K
+// materializes the kernels, as the reference's module does).
+constexpr int kGenFwdMaxK = 5;
 
 // Largest dilation the fused backward kernels stage (their column halo).
 constexpr int kGenMaxDil = 8;

@@ -248,10 +248,10 @@ int with_type(int dt, F&& f) {
 
 // Shared with the backward entry points.
 int gen_make_geom(GenGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int k, int d0, int d1,
-                  int d2) {
+                  int d2, int kmax) {
   if (n < 0 || c < 0 || h < 0 || w < 0) return kBadArgument;
   if (k < 1 || (k % 2) == 0 || d0 < 1 || d1 < 1 || d2 < 1) return kBadArgument;
-  if (k > 3 || c > 128) return kUnsupported;
+  if (k > kmax || c > 128) return kUnsupported;
   if (h > (1 << 20) || w > (1 << 20) || h * w > ((int64_t)1 << 31)) return kUnsupported;
   if (k == 1) d0 = d1 = d2 = 1;  // a 1x1 tap has no neighbour to dilate
   g.N = (int)n;
@@ -284,7 +284,7 @@ extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, co
   }
   if (dtype < kF32 || dtype > kF16) return kBadArgument;
   GenGeom gg;
-  int st = gen_make_geom(gg, n, c, h, w, kernel_size, d0, d1, d2);
+  int st = gen_make_geom(gg, n, c, h, w, kernel_size, d0, d1, d2, kGenFwdMaxK);
   if (st != kOk) return st;
   if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
   if (!x || !y || !weight || !bias || !out) return kBadArgument;
@@ -348,11 +348,11 @@ extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, co
         return nk == 1 ? launch(gen_fwd_kernel<T, KS, 1, 1, PP>) : launch(gen_fwd_kernel<T, KS, 2, 1, PP>);
       return nk == 1 ? launch(gen_fwd_kernel<T, KS, 1, 2, PP>) : launch(gen_fwd_kernel<T, KS, 2, 2, PP>);
     };
-    if (pp) {
-      if (kernel_size == 1) return pick(std::integral_constant<int, 1>(), std::true_type());
-      return pick(std::integral_constant<int, 3>(), std::true_type());
-    }
-    if (kernel_size == 1) return pick(std::integral_constant<int, 1>(), std::false_type());
-    return pick(std::integral_constant<int, 3>(), std::false_type());
+    auto by_k = [&](auto ppc) {
+      if (kernel_size == 1) return pick(std::integral_constant<int, 1>(), ppc);
+      if (kernel_size == 3) return pick(std::integral_constant<int, 3>(), ppc);
+      return pick(std::integral_constant<int, 5>(), ppc);
+    };
+    return pp ? by_k(std::true_type()) : by_k(std::false_type());
   });
 }

@@ -153,7 +153,9 @@ class DDPM(nn.Module):
     def _route(self, x: torch.Tensor, y: torch.Tensor, gen_supported) -> str:
         """Returns "fused" or "materialized" with the reference's rules
         (triton_impl.py:311-329); shapes outside the fused kernels' coverage
-        (``ops.generator_supported``) use the materialized route."""
+        (``ops.generator_supported``: the forward's alone without grad, where
+        K = 5 is fused as the reference fuses inference at any K) use the
+        materialized route."""
         tokens = x.shape[0] * x.shape[2] * x.shape[3]
         requested = self.fused_generator_training
         if requested is None:
@@ -168,7 +170,8 @@ class DDPM(nn.Module):
             and x.dtype == y.dtype == self.generator.weight.dtype
             and bias is not None
             and bias.dtype == x.dtype
-            and gen_supported(self.dim, self.kernel_size, self.dilations, x.shape, x.dtype)
+            and gen_supported(self.dim, self.kernel_size, self.dilations, x.shape, x.dtype,
+                              forward_only=not grad)
         )
         return "fused" if can_fuse else "materialized"
 

@@ -177,12 +177,15 @@ _FUSED_MAX_IMAGE_BYTES = 2**31 - 1
 
 
 def generator_supported(channels: int, kernel_size: int, dilations=(1, 3, 5), shape=None,
-                        dtype=None) -> bool:
-    """Whether the fused generator kernels handle this configuration
-    (``ddpm_gen_supported``: channel count, K in {1, 3}, largest dilation) and,
+                        dtype=None, forward_only: bool = False) -> bool:
+    """Whether the fused generator kernels handle this configuration and,
     given ``shape`` ``[N, C, H, W]`` and ``dtype``, whether one image's planes
-    fit their 32-bit offsets."""
-    if not _lib.load().ddpm_gen_supported(int(channels), int(kernel_size), int(max(dilations))):
+    fit their 32-bit offsets.  ``forward_only``: the forward alone (inference:
+    ``ddpm_gen_fwd_supported``, K in {1, 3, 5}); else forward and recompute
+    backward (``ddpm_gen_supported``, K in {1, 3})."""
+    lib = _lib.load()
+    query = lib.ddpm_gen_fwd_supported if forward_only else lib.ddpm_gen_supported
+    if not query(int(channels), int(kernel_size), int(max(dilations))):
         return False
     if shape is not None:
         esize = (dtype if dtype is not None else torch.float32).itemsize
@@ -451,16 +454,17 @@ def fused_generator_dynamic_cat(x, y, weight, bias, kernel_size, dilations):
     """Generator + dynamic filter + concat (_triton_kernels.py:1056-1065).
 
     Uses the autograd Function when grad is enabled and any input requires
-    grad, else a single forward launch.  Shapes outside the fused kernels'
-    coverage (:func:`generator_supported`) run the generator as a 1x1
-    convolution and the HIP materialized filter, with the same result and
-    autograd outputs.
+    grad, else a single forward launch (which also takes K = 5).  Shapes
+    outside the fused kernels' coverage (:func:`generator_supported`) run the
+    generator as a 1x1 convolution and the HIP materialized filter, with the
+    same result and autograd outputs.
     """
     k = _check_kernel_size(kernel_size)
     dil = _check_dilations(dilations)
-    if not generator_supported(x.shape[1], k, dil, x.shape, x.dtype):
+    needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in (x, y, weight, bias))
+    if not generator_supported(x.shape[1], k, dil, x.shape, x.dtype, forward_only=not needs_grad):
         return _materialized_generator_dynamic_cat(x, y, weight, bias, k, dil)
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (x, y, weight, bias)):
+    if needs_grad:
         return _GeneratorDynamicCat.apply(x, y, weight, bias, k, dil)
     return _launch_generator_dynamic_cat(x, y, weight, bias, k, dil)
 
@@ -582,7 +586,8 @@ def fuse_conv3x3(cat, weight, bias=None):
 def fused_ddpm_supported(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, kernel_size,
                          dilations) -> bool:
     """Whether :func:`fused_ddpm` takes this call: fp32 throughout, a ROCm
-    device, the fused generator kernels' coverage (:func:`generator_supported`),
+    device, the fused generator kernels' coverage (:func:`generator_supported`;
+    the forward's alone when no gradient is needed),
     C % 16 == 0 (whole 32-plane chunks of the concat), the HIP fuse
     convolution's coverage and weight shapes of DDPM(C, K)."""
     if x.dtype != torch.float32 or x.ndim != 4 or not x.is_cuda:
@@ -598,10 +603,12 @@ def fused_ddpm_supported(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, ker
         return False
     if fuse_bias is not None and tuple(fuse_bias.shape) != (c,):
         return False
-    if any(t is not None and (t.dtype != torch.float32 or t.device != x.device)
-           for t in (y, gen_weight, gen_bias, fuse_weight, fuse_bias)):
+    tensors = (y, gen_weight, gen_bias, fuse_weight, fuse_bias)
+    if any(t is not None and (t.dtype != torch.float32 or t.device != x.device) for t in tensors):
         return False
-    if not generator_supported(c, k, dilations, x.shape, x.dtype):
+    needs_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (x, *tensors))
+    if not generator_supported(c, k, dilations, x.shape, x.dtype, forward_only=not needs_grad):
         return False
     return 4 * c * h * w * 4 <= 2**31 - 1
 

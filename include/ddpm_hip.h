@@ -46,7 +46,8 @@ extern "C" {
 #define DDPM_DTYPE_BF16 1
 #define DDPM_DTYPE_F16 2
 
-/* ABI version of this header (5: dtype code 3). */
+/* ABI version of this header (5: dtype code 3; 6: ddpm_gen_fwd at K = 5 and
+ * ddpm_gen_fwd_supported). */
 int ddpm_abi_version(void);
 
 /* Text for any status code returned by this library (static storage). */
@@ -59,6 +60,15 @@ const char* ddpm_status_string(int code);
  * channel limit; callers route other shapes to the materialized entry points
  * (ddpm_filter_*), with identical results. */
 int ddpm_gen_supported(int64_t c, int kernel_size, int max_dilation);
+
+/* 1 when ddpm_gen_fwd alone -- the fused forward, for inference -- accepts
+ * this channel count, kernel size and largest dilation (C <= 128, K in {1, 3,
+ * 5}, the halo tile of radius (K/2)*max_dilation within one workgroup's LDS:
+ * max_dilation <= 12 at K = 3, <= 6 at K = 5), else 0; host-only.  The
+ * reference's module fuses inference at any K (triton_impl.py:317-338, the
+ * fused forward _triton_kernels.py:268-300); training above K = 3
+ * materializes the kernels there as here. */
+int ddpm_gen_fwd_supported(int64_t c, int kernel_size, int max_dilation);
 
 /* 1 when ddpm_gen_kernels and ddpm_gen_kernels_bwd_w accept this shape and
  * dtype (c <= 128, one image's generated planes within 2^31 - 1 bytes, grids
@@ -135,7 +145,9 @@ int ddpm_filter_bwd_k(const void* x, const void* grad_out, void* grad_kernels, i
 
 /* out = [x, d0, d1, d2] with the dynamic taps generated on chip
  * (gen = weight . y + bias, rounded to `dtype` for bf16/f16); dtype 3 writes
- * fp32 results as pair planes (c % 16 == 0, else kUnsupported).
+ * fp32 results as pair planes (c % 16 == 0, else kUnsupported).  K in
+ * {1, 3, 5} (shapes of ddpm_gen_fwd_supported; the backward entry points take
+ * K <= 3).
  * Replaces _generator_dynamic_cat_fwd + _launch_generator_dynamic_cat
  * (_triton_kernels.py:268-420, 873-908). */
 int ddpm_gen_fwd(const void* x, const void* y, const void* weight, const void* bias, void* out,

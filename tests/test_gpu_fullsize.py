@@ -3,8 +3,9 @@
 * 256x256 fused recompute training, fp32 and bf16, against the float64 CPU
   oracle (forward and all gradients);
 * 128x128 fused inference, fp32;
-* K=5 128x128 bf16 materialized inference and training (output also
-  against the oracle run in bf16), fp32 training;
+* K=5 128x128 bf16 inference on the fused and the materialized route (output
+  also against the oracle run in bf16), fp32 fused inference, bf16 and fp32
+  materialized training;
 * size-independent adjoint identities of the fused operator at 256x256:
   the fused op is linear in x and affine in y, W and b, so
   <F(x + v) - F(x), g> = <v, dX(g)> and likewise for y, W and b; both sides
@@ -43,9 +44,14 @@ def test_inference_128_fused_fp32():
     record_errors("infer N=1 C=64 128x128 K=3 float32 fused", {"out": stats})
 
 
-def test_k5_128_bf16_materialized():
-    say("full-size K=5 128x128 bf16 materialized inference + training")
-    ref, cand = make_models(64, 5, torch.bfloat16)
+@pytest.mark.parametrize("route", ["fused", "materialized"])
+def test_k5_128_bf16_inference(route):
+    """K=5 128x128 bf16 inference on the fused forward (the module's default,
+    as the reference's) and on the materialized route
+    (fused_generator_inference=False)."""
+    say(f"full-size K=5 128x128 bf16 inference, {route} route")
+    ref, cand = make_models(64, 5, torch.bfloat16,
+                            fused_generator_inference=route == "fused")
     ref.eval()
     cand.eval()
     torch.manual_seed(22)
@@ -57,7 +63,27 @@ def test_k5_128_bf16_materialized():
     errors = {"out": assert_max_abs(actual, expected, max_abs_bound(torch.bfloat16, 5),
                                     "out K5 bf16")}
     check_bf16_output(actual, x, y, 64, 5, errors)
-    record_errors("infer N=1 C=64 128x128 K=5 bfloat16 materialized", errors)
+    record_errors(f"infer N=1 C=64 128x128 K=5 bfloat16 {route}", errors)
+
+
+def test_k5_128_fp32_inference_fused():
+    """K=5 128x128 fp32 inference on the fused forward (pair-plane concat)."""
+    say("full-size K=5 128x128 fp32 fused inference")
+    ref, cand = make_models(64, 5, torch.float32)
+    ref.eval()
+    cand.eval()
+    torch.manual_seed(25)
+    x = torch.randn(1, 64, 128, 128)
+    y = torch.randn_like(x)
+    with torch.inference_mode():
+        expected = ref(x.double(), y.double())
+        actual = cand(x.to(DEV), y.to(DEV))
+    stats = assert_max_abs(actual, expected, max_abs_bound(torch.float32, 5), "out K5 fp32")
+    record_errors("infer N=1 C=64 128x128 K=5 float32 fused", {"out": stats})
+
+
+def test_k5_128_bf16_materialized_training():
+    say("full-size K=5 128x128 bf16 materialized training")
     check_training(64, 128, 128, 5, torch.bfloat16, fused=False, n=1, seed=23)
 
 

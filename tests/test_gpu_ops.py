@@ -167,6 +167,67 @@ def test_generator_wide_channels_match_oracle(shape, K, dtype):
 
 
 @pytest.mark.parametrize(
+    "shape,dil",
+    [
+        ((2, 24, 15, 17), (1, 3, 5)),   # non-aligned channels and width
+        ((1, 40, 37, 45), (1, 3, 5)),   # W % 4 != 0, several tiles
+        ((1, 24, 36, 72), (1, 3, 5)),   # W % 4 == 0 (vector halo staging)
+        ((1, 64, 32, 64), (2, 4, 6)),   # the largest K = 5 halo (radius 12)
+        ((1, 96, 20, 36), (1, 3, 5)),   # 65..128 channels: four K steps
+    ],
+)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_generator_forward_k5_matches_oracle(shape, dil, dtype):
+    """The fused forward at K = 5 (inference: no gradient needed), as the
+    reference fuses inference at any K (triton_impl.py:317-338)."""
+    n, c, h, w = shape
+    say(f"generator forward K=5 shape={shape} dil={dil} dtype={dtype}")
+    assert ops.generator_supported(c, 5, dil, forward_only=True)
+    assert not ops.generator_supported(c, 5, dil)
+    x = randn(shape, 50, dtype)
+    y = randn(shape, 51, dtype)
+    wt, b = default_generator_params(c, 5, 52, dtype)
+    calls = []
+    real = ops._launch_generator_dynamic_cat
+
+    def spy(*a, **k):
+        calls.append(1)
+        return real(*a, **k)
+
+    ops._launch_generator_dynamic_cat = spy
+    try:
+        with torch.no_grad():
+            out = ops.fused_generator_dynamic_cat(x.to(DEV), y.to(DEV), wt.to(DEV), b.to(DEV), 5, dil)
+    finally:
+        ops._launch_generator_dynamic_cat = real
+    assert calls, "K = 5 inference did not take the fused forward"
+    assert out.dtype == dtype
+    x64, y64, w64, b64 = (v.double() for v in (x, y, wt, b))
+    kern = ref.generated_kernels(y64, w64, b64, 5)
+    if dtype != torch.float32:
+        kern = kern.to(dtype).double()
+    atol, rtol = TOL["gen_fwd"][dtype]
+    assert_close(out, ref.dynamic_cat(x64, kern, 5, dil), atol, rtol, "gen K5 out")
+
+
+def test_generator_k5_with_grad_materializes():
+    """With gradients needed, K = 5 keeps the materialized route (the fused
+    backward covers K <= 3), with the fused forward's result."""
+    shape = (1, 16, 12, 20)
+    x = randn(shape, 53).to(DEV)
+    y = randn(shape, 54).to(DEV)
+    wt, b = default_generator_params(16, 5, 55, torch.float32)
+    wt, b = wt.to(DEV), b.to(DEV)
+    with torch.no_grad():
+        fused = ops.fused_generator_dynamic_cat(x, y, wt, b, 5, DIL)
+    xs = x.clone().requires_grad_()
+    out = ops.fused_generator_dynamic_cat(xs, y, wt, b, 5, DIL)
+    assert out.grad_fn is not None and "DynamicCat" in type(out.grad_fn).__name__
+    assert "Generator" not in type(out.grad_fn).__name__
+    assert_close(out, fused.cpu().double(), 2e-4, 1e-4, "materialized vs fused K5")
+
+
+@pytest.mark.parametrize(
     "K,dil,fused",
     [
         (3, (2, 7, 8), True),    # largest dilation the fused kernels stage

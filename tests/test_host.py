@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_host_only_queries():
     lib = _lib.load()
-    assert lib.ddpm_abi_version() == _lib.ABI_VERSION == 5
+    assert lib.ddpm_abi_version() == _lib.ABI_VERSION == 6
     assert b"invalid argument" in lib.ddpm_status_string(10001)
     assert lib.ddpm_gen_supported(64, 3, 5) == 1
     # up to 128 channels (four 32-channel K steps, 32-column tiles above 64)
@@ -46,6 +46,19 @@ def test_host_only_queries():
     assert lib.ddpm_gen_supported(64, 3, 8) == 1
     assert lib.ddpm_gen_supported(64, 3, 9) == 0
     assert lib.ddpm_gen_supported(64, 1, 50) == 1
+    # the forward alone (inference): K = 5, and larger halos, as far as the
+    # LDS holds the halo tile of a 32-column tile
+    assert lib.ddpm_gen_fwd_supported(64, 3, 5) == 1
+    assert lib.ddpm_gen_fwd_supported(64, 5, 5) == 1
+    assert lib.ddpm_gen_fwd_supported(128, 5, 5) == 1
+    assert lib.ddpm_gen_fwd_supported(64, 5, 6) == 1
+    assert lib.ddpm_gen_fwd_supported(64, 5, 7) == 0
+    assert lib.ddpm_gen_fwd_supported(64, 3, 9) == 1
+    assert lib.ddpm_gen_fwd_supported(64, 3, 12) == 1
+    assert lib.ddpm_gen_fwd_supported(64, 3, 13) == 0
+    assert lib.ddpm_gen_fwd_supported(64, 7, 1) == 0
+    assert lib.ddpm_gen_fwd_supported(129, 5, 5) == 0
+    assert lib.ddpm_gen_fwd_supported(64, 1, 50) == 1
     # at most 16 splits of 27 (branch, tap) x C x (C + 1) fp32 partials, at least
     # 4 steps (row segments of 128 columns) each: 16 at 256x256; the same
     # for every dtype (fp32 y is split into bf16 hi / lo while it is staged)
@@ -165,7 +178,8 @@ class _FakeTensor:
         ((1, 64, 64, 64), torch.float32, 3, True, True, False, "fused"),  # forced fused
         ((1, 64, 256, 256), torch.float32, 3, False, True, False, "materialized"),  # forced off
         ((1, 64, 256, 256), torch.float32, 5, True, True, False, "materialized"),  # K > 3
-        ((1, 64, 256, 256), torch.float32, 5, None, False, False, "materialized"),  # K > 3 inference
+        ((1, 64, 256, 256), torch.float32, 5, None, False, False, "fused"),  # K = 5 inference
+        ((1, 64, 256, 256), torch.float32, 7, None, False, False, "materialized"),  # K = 7 inference
         ((1, 64, 256, 256), torch.float32, 3, None, False, True, "materialized"),  # autocast
     ],
 )
@@ -174,7 +188,10 @@ def test_routing_rules(monkeypatch, tokens_shape, dtype, k, flag, grad, autocast
     m = module.DDPM(c, k, fused_generator_training=flag).to(dtype)
     x = _FakeTensor(tokens_shape, dtype)
     monkeypatch.setattr(torch, "is_autocast_enabled", lambda *a, **k: autocast)
-    supported = lambda ch, ks, dil, *shape_dtype: ks <= 3 and ch <= 64  # noqa: E731
+
+    def supported(ch, ks, dil, *shape_dtype, forward_only=False):
+        return ch <= 64 and (ks <= 3 or (forward_only and ks == 5))
+
     with torch.set_grad_enabled(grad):
         assert m._route(x, x, supported) == expect
 
@@ -183,7 +200,7 @@ def test_routing_dtype_mismatch_materializes():
     m = module.DDPM(8, 3)  # fp32 parameters
     x = _FakeTensor((1, 8, 64, 64), torch.bfloat16)
     with torch.no_grad():
-        assert m._route(x, x, lambda *a: True) == "materialized"
+        assert m._route(x, x, lambda *a, **k: True) == "materialized"
 
 
 def test_routing_respects_the_fused_kernels_offset_bound():
