@@ -83,6 +83,11 @@ def parse_args():
                    "128x128 inference (k5-infer-fused|k5-infer-materialized); prints one JSON "
                    "line")
     p.add_argument("--channels", type=int, default=C, help="with --peak-mem: C")
+    p.add_argument("--first-steps", type=int, default=0, metavar="N",
+                   help="probe mode: N fp32 training steps of a fresh process, each synchronized "
+                   "and bracketed by HIP events, no warm-up (the clock ramp); prints one JSON line")
+    p.add_argument("--settle-ms", type=float, default=0.0,
+                   help="with --first-steps: clock settle before the steps (0 = none)")
     p.add_argument("--cpu-budget", type=float, default=12.0,
                    help="seconds per CPU-baseline leg at most (after its warm-up)")
     return p.parse_args()
@@ -682,6 +687,29 @@ def kernel_mode(args):
         print(f"ran {name} x{args.reps} ({args.dtype}, K={k}, {hw}x{hw}, {len(sets)} input sets)", flush=True)
 
 
+def first_steps_mode(nsteps, settle_ms):
+    """Probe of a fresh process's first training steps: one untimed step (code
+    objects, allocator), an optional clock settle, then `nsteps` steps, each
+    synchronized and timed with HIP events."""
+    import torch
+
+    module = make_module(torch.float32)
+    x, y = make_inputs(torch.float32)
+    train_step(module, x, y)
+    torch.cuda.synchronize()
+    settled = settle_gpu_clocks(settle_ms) if settle_ms > 0 else 0.0
+    ms = []
+    for _ in range(nsteps):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        train_step(module, x, y)
+        end.record()
+        torch.cuda.synchronize()
+        ms.append(start.elapsed_time(end))
+    print(json.dumps({"settle_ms": settled, "step_ms": ms}))
+
+
 def kernel_breakdown(lib, timer, module, x, y, steps=10):
     """Per-entry-point HIP-event timing of the training step (a separate pass:
     the headline loop runs uninstrumented)."""
@@ -722,6 +750,9 @@ def main():
         sys.exit(2)
     if args.kernel:
         kernel_mode(args)
+        return
+    if args.first_steps:
+        first_steps_mode(args.first_steps, args.settle_ms)
         return
     extra = {}
     if not args.quick:

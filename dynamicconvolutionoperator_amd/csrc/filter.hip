@@ -16,9 +16,11 @@
 //   * dX is a gather (kernel planes read at the shifted source pixels): a lane
 //     owns 16 bytes of consecutive pixels and loads the two aligned 16-byte
 //     chunks around each tap's shifted window (realigned in registers by a
-//     wave-uniform shift) where the staged tiles fit two workgroups per CU;
-//     otherwise one pixel in each of U column blocks of 64, so every load of
-//     a kernel plane is 64 consecutive elements;
+//     wave-uniform shift), the branch gradients staged one branch at a time
+//     (double-buffered, each with its own dilation's halo), where those tiles
+//     fit two workgroups per CU; otherwise one pixel in each of U column
+//     blocks of 64, so every load of a kernel plane is 64 consecutive
+//     elements;
 //   * FP32 accumulation; outputs written once with non-temporal vector
 //     stores (streamed, not read back by the kernel), no Unfold buffers.
 
@@ -447,12 +449,69 @@ __device__ __forceinline__ void realign(const u32x4& c0, const u32x4& c1, int s,
   }
 }
 
+// One branch-gradient plane's part of the staged tile that the dilation d_b
+// reads -- staged rows [R - Rb, R + TH + Rb) and columns [CP - CPb, CP + TW +
+// CPb), Rb = (K/2) d_b and CPb = Rb rounded up to a multiple of V -- staged
+// in two halves: issue() requests it into registers (16-byte loads, zero
+// outside the image), commit() writes it to a tile buffer phase-split by V.
+// A thread handles at most NB items (row, V-wide column group); the host
+// checks that bound.
+template <typename T, int V, typename TS, int NB>
+struct BranchStage {
+  static_assert(V * sizeof(T) == 16, "16-byte groups");
+  u32x4 raw[NB];
+  int dst[NB];
+
+  __device__ __forceinline__ void issue(const T* __restrict__ plane, const FilterGeom& g, int h0,
+                                        int w0, int rb) {
+    const int cpb = (rb + V - 1) / V * V;
+    const int r0 = g.R - rb, c0 = (g.CP - cpb) / V;
+    const int groups = (g.TW + 2 * cpb) / V;
+    const int total = (g.TH + 2 * rb) * groups;
+    const BufRes res = make_buf(plane, (uint32_t)((int64_t)g.H * g.W * (int64_t)sizeof(T)));
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int item = (int)threadIdx.x + kFilterThreads * k;
+      const int i = item / groups, m = item - i * groups;
+      const int srow = r0 + i, sgrp = c0 + m;
+      const int gh = h0 - g.R + srow, gc = w0 - g.CP + sgrp * V;
+      const bool ok = item < total && (unsigned)gh < (unsigned)g.H && gc >= 0 && gc < g.W;
+      raw[k] = __builtin_amdgcn_raw_buffer_load_b128(
+          res, ok ? (uint32_t)((int64_t)gh * g.W + gc) * (uint32_t)sizeof(T) : kOob, 0, 0);
+      dst[k] = item < total ? srow * g.RS + sgrp : -1;
+    }
+  }
+
+  __device__ __forceinline__ void commit(TS* __restrict__ s, const FilterGeom& g) const {
+    typedef typename Vec<T, V>::type TV;
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      if (dst[k] >= 0) {
+        const TV t = __builtin_bit_cast(TV, raw[k]);
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          if constexpr (std::is_same<T, TS>::value)
+            s[dst[k] + e * g.PS] = t[e];  // staged in its own type: the bits as loaded
+          else
+            s[dst[k] + e * g.PS] = from_f<TS>(to_f(t[e]));
+        }
+      }
+    }
+  }
+};
+
+// Items per thread of BranchStage in filter_bwd_x_vec_kernel.
+constexpr int kDxStageItems = 6;
+
 // dX gather with V consecutive pixels per lane (16 bytes of kernel plane;
-// W % V == 0): the branch-gradient tiles are staged phase-split as in the
-// forward, and each tap's kernel values at the lane's shifted window come
+// W % V == 0): each tap's kernel values at the lane's shifted window come
 // from the two aligned 16-byte chunks around it -- two loads per V pixels
-// instead of V, every access aligned.  The K taps of a kernel row are
-// requested together, one row ahead of the FMAs.
+// instead of V, every access aligned; the K taps of a kernel row are
+// requested together, one row ahead of the FMAs.  The branch gradients are
+// staged one branch at a time into two tile buffers (phase-split as in the
+// forward), each with only the halo its own dilation reads: branch b+1's
+// loads are in flight while branch b's taps run, and the tile takes a third
+// of the LDS of staging all three at once, so more workgroups share a CU.
 template <typename TX, typename TK, int KS, int V>
 __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_vec_kernel(const TK* __restrict__ gout,
                                                                             const TK* __restrict__ kern,
@@ -462,8 +521,7 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_vec_kernel(const 
   constexpr int KK = KS * KS, r = KS / 2;
   constexpr uint32_t E = sizeof(TK);
   // the gradient planes are staged in their own type: 2-byte planes take
-  // half the LDS of fp32 ones (more workgroups per CU; the tall K = 5 tiles
-  // fit two per CU)
+  // half the LDS of fp32 ones
   typedef typename std::conditional<sizeof(TK) == 2, TK, float>::type TS;
   extern __shared__ __attribute__((aligned(16))) unsigned char gsm[];
   TS* __restrict__ gs = reinterpret_cast<TS*>(gsm);
@@ -509,24 +567,27 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_vec_kernel(const 
                                kr, ok1 ? (base + (uint32_t)(a0 + V)) * E : kOob, 0, 0);
     }
   };
+  auto halo = [&](int b) { return r * dil_of(b, g.d0, g.d1, g.d2); };
 
+  BranchStage<TK, V, TS, kDxStageItems> st;
   u32x4 nxt[KS][2];
   load_row(0, 0, nxt);
-#pragma unroll
-  for (int b = 0; b < 3; ++b) stage_plane<TK, V, TS>(gs + b * lplane, gp + (b + 1) * gstride, g, h0, w0);
-  __syncthreads();
-  if (!active) return;  // no barrier below
-
+  st.issue(gp + gstride, g, h0, w0, halo(0));
   float acc[V];
   {
-    const int64_t pix = (int64_t)gh * g.W + gw;
-    VecIO<TK, V>::load(gp + pix, acc);
+    // this lane's gO_x (zero for an inactive lane: it stores nothing)
+    const BufRes xr = make_buf(gp, (uint32_t)(HW * (int64_t)E));
+    buf_loadv<TK, V>(xr, active ? (uint32_t)((int64_t)gh * g.W + gw) * E : kOob, acc);
   }
-  const int jc = g.CP + V * cl;  // staged column of this lane's first pixel
+  st.commit(gs, g);
+  __syncthreads();
+  const int jc = g.CP + V * cl;             // staged column of this lane's first pixel
+  const int tr = active ? trow : 0;        // rows of inactive lanes stay inside the tile
   // a runtime loop: unrolled, the compiler would hoist every row's loads
 #pragma unroll 1
   for (int it = 0; it < 3 * KS; ++it) {
     const int b = it / KS, ki = it - b * KS;
+    if (ki == 0 && b < 2) st.issue(gp + (b + 2) * gstride, g, h0, w0, halo(b + 1));
     u32x4 cur[KS][2];
 #pragma unroll
     for (int kj = 0; kj < KS; ++kj) {
@@ -535,8 +596,8 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_vec_kernel(const 
     }
     if (it + 1 < 3 * KS) load_row((it + 1) / KS, (it + 1) % KS, nxt);
     const int d = dil_of(b, g.d0, g.d1, g.d2);
-    const TS* __restrict__ gb = gs + b * lplane;
-    const int rb = (trow + g.R - (ki - r) * d) * g.RS + jc / V;
+    const TS* __restrict__ gb = gs + (b & 1) * lplane;
+    const int rb = (tr + g.R - (ki - r) * d) * g.RS + jc / V;
 #pragma unroll
     for (int kj = 0; kj < KS; ++kj) {
       const int dw = (kj - r) * d;
@@ -546,8 +607,13 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_vec_kernel(const 
 #pragma unroll
       for (int v = 0; v < V; ++v) acc[v] = fmaf(kv[v], staged<V, TS>(gb, g, rb, v - dw), acc[v]);
     }
+    if (ki == KS - 1 && b < 2) {
+      // every wave is past branch b-1, whose buffer branch b+1 takes
+      st.commit(gs + ((b + 1) & 1) * lplane, g);
+      __syncthreads();
+    }
   }
-  VecIO<TX, V>::store_nt(gx + (int64_t)plane * HW + (int64_t)gh * g.W + gw, acc);
+  if (active) VecIO<TX, V>::store_nt(gx + (int64_t)plane * HW + (int64_t)gh * g.W + gw, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -661,7 +727,7 @@ int launch_ks(FilterOp op, const void* a, const void* b, void* o, const FilterGe
         constexpr int VK = 16 / (int)sizeof(TK);
         if (vec == VK)
           return launch_kernel(filter_bwd_x_vec_kernel<TX, TK, KS, VK>, g,
-                               (size_t)3 * g.LH * g.RS * (sizeof(TK) == 2 ? 2 : 4), stream,
+                               (size_t)2 * g.LH * g.RS * (sizeof(TK) == 2 ? 2 : 4), stream,
                                (const TK*)a, (const TK*)b, (TX*)o, g);
       }
       // 4 pixels per lane only for K <= 3 (larger K would not keep the
@@ -710,12 +776,14 @@ int run_filter(FilterOp op, const void* a, const void* b, void* o, int64_t n, in
     const bool kvec = (k == 1 || k == 3 || k == 5) && w % v == 0 && aligned(a, 16) &&
                       aligned(b, 16) && aligned(o, 16) &&
                       (int64_t)k * k * h * w * (int64_t)esize(k_dtype) <= 0x7fffffffLL;
-    // ... and the three staged tiles (fp32, or 2-byte for 2-byte gradients)
+    // ... and its two branch tiles (fp32, or 2-byte for 2-byte gradients)
     // leave room for two workgroups per CU (measured: at K = 5 with fp32
     // tiles of ~90 KB the vector gather was 30% slower than the
-    // one-pixel-per-lane one)
-    if (kvec && make_geom(g, n, c, h, w, k, d0, d1, d2, v, v, 3, true) == kOk &&
-        (size_t)3 * g.LH * g.RS * esize(k_dtype) <= kFilterMaxLds / 2) {
+    // one-pixel-per-lane one), and a branch's staging takes at most
+    // kDxStageItems 16-byte groups per thread
+    if (kvec && make_geom(g, n, c, h, w, k, d0, d1, d2, v, v, 2, true) == kOk &&
+        (size_t)2 * g.LH * g.RS * esize(k_dtype) <= kFilterMaxLds / 2 &&
+        (int64_t)g.LH * ((g.TW + 2 * g.CP) / v) <= (int64_t)kDxStageItems * kFilterThreads) {
       return with_type(x_dtype, [&](auto tx) {
         using TX = decltype(tx);
         return with_type(k_dtype, [&](auto tk) {

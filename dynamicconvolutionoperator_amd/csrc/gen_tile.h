@@ -614,15 +614,24 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
         const int chb = (b + 1) * C + c0;
         const BufRes pres = make_buf(out + ((int64_t)n * 4 * C + (chb & ~31)) * HW, 32u * HWE);
         const uint32_t pbase = (uint32_t)(((chb & 31) >> 1) + 2 * quad);
+        // the lane's column offsets, formed here (kept out of registers across
+        // the loop, as lofs is for the plain stores)
+        uint32_t pc[CB];
+#pragma unroll
+        for (int cp = 0; cp < CB; ++cp) {
+          const int gw = w0 + 16 * cp + col16;
+          pc[cp] = (gw < W && 4 * quad < nch) ? (uint32_t)gw * 4u : kOob;
+          asm volatile("" : "+v"(pc[cp]));
+        }
 #pragma unroll
         for (int blk = 0; blk < NBW; ++blk) {
-          const int gh = h0 + 2 * wave + blk / CB, gw = w0 + 16 * (blk % CB) + col16;
-          const bool ok = gh < H && gw < W && 4 * quad < nch;
+          const int gh = h0 + 2 * wave + blk / CB;
+          const bool ok = gh < H && pc[blk % CB] != kOob;
 #pragma unroll
           for (int kp = 0; kp < 2; ++kp) {
             uint32_t hh, ll;
             split_bf16x2(acc[blk][2 * kp], acc[blk][2 * kp + 1], hh, ll);
-            const uint32_t o = ok ? (uint32_t)(gh * W + gw) * 4u + (pbase + kp) * HWE : kOob;
+            const uint32_t o = ok ? pc[blk % CB] + (uint32_t)(gh * W) * 4u + (pbase + kp) * HWE : kOob;
             __builtin_amdgcn_raw_buffer_store_b32(hh, pres, o, 0, 0);
             __builtin_amdgcn_raw_buffer_store_b32(ll, pres, ok ? o + 16u * HWE : kOob, 0, 0);
           }
