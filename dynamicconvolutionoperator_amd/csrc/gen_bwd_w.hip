@@ -49,7 +49,8 @@ struct WGradGeom {
   int d0, d1, d2;
   int cblocks;         // ceil(C / 16)
   int ihalves;         // 1, or 2 when C > 64: a workgroup covers 16*MB input channels i
-  int col_blocks;      // ceil(W / kWgTW)
+  int tw;              // columns per step: kWgTW, or 2 * kWgTW (wg_step_cols)
+  int col_blocks;      // ceil(W / tw)
   int splits;
   int steps;           // N * H * col_blocks
   int steps_per_split;
@@ -78,25 +79,28 @@ struct WgTaps {
 //   g rows [16][kGD]          T elements, chunks swizzled the same way
 // The 16-byte fragment reads of 16 rows at one chunk index hit 16 distinct
 // bank groups.
-template <typename T, int KS, int MB>
+template <typename T, int KS, int MB, int SJ>
 struct WgLds {
   static constexpr int P = Mma<T>::P;
+  static constexpr int TW = kWgTW * SJ;                             // columns per step
+  static constexpr int LW = TW + 2 * kWgPad;                        // staged x columns
   static constexpr int kPerD = 4 / (int)sizeof(T);                  // elements per dword
-  static constexpr int kXD = kWgLW / kPerD;                         // dwords per staged x row
+  static constexpr int kXD = LW / kPerD;                            // dwords per staged x row
   static constexpr int kXI = (kXD + 63) / 64;                       // 64-dword copies per x row
   static constexpr int kXSD = kXD + (sizeof(T) == 4 ? 1 : 3);
   static_assert(kXSD % 2 == 1, "odd x-row pitch");
   static_assert(kXD % 4 == 0, "16-byte x copies move whole rows");
-  static constexpr int kYC = kWgTW / 8;                             // chunks per y row (16)
+  static constexpr int kYC = TW / 8;                                // chunks per y row (16 or 32)
   static constexpr int kYD = 4 * kYC;
-  static constexpr int kGC = kWgTW * (int)sizeof(T) / 16;           // chunks per g row
+  static constexpr int kGC = TW * (int)sizeof(T) / 16;              // chunks per g row
   static constexpr int kGD = 4 * kGC;
   static constexpr int kXRows = KS * 16;
   static constexpr int kYRows = P * MB * 16;
   static constexpr int kYOff = kXRows * kXSD;
   static constexpr int kGOff = kYOff + kYRows * kYD;
   static constexpr int kBuf = kGOff + 16 * kGD;
-  static_assert(kYC == 16 && kGC >= 16, "the chunk swizzle needs 16 chunks per row");
+  static_assert(kYC >= 16 && kYC % 16 == 0 && kGC >= 16, "the chunk swizzle needs 16 chunks per row");
+  static_assert(kXD / 4 <= 64, "one 16-byte x copy per lane and row");
 };
 
 template <typename T>
@@ -112,7 +116,7 @@ __device__ __forceinline__ float lds_elem(const uint32_t* __restrict__ base, int
 struct WgPos {
   int n, h, w0, cbk;
   __device__ __forceinline__ void advance(const WGradGeom& g) {
-    w0 += kWgTW;
+    w0 += g.tw;
     if (++cbk == g.col_blocks) {
       cbk = 0;
       w0 = 0;
@@ -164,7 +168,10 @@ __global__ __launch_bounds__(256) void gen_ysplit_kernel(const float* __restrict
 // kernel's weight packing (`yp`, none when yp.total is 0) and the input
 // gradient's halo reduction (`fin`) there, alongside, instead of as kernels of
 // their own.
-template <typename T, int KS, int MB>
+// SJ: 128-column subsegments per step (2 for 2-byte types on wide images:
+// twice the work per step and per barrier; each wave takes its 32-token
+// segment in both).
+template <typename T, int KS, int MB, int SJ>
 __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_partial_kernel(
     const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ gout,
     float* __restrict__ pw, float* __restrict__ pb, T* __restrict__ dw_out, T* __restrict__ db_out,
@@ -172,7 +179,8 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
   typedef Mma<T> M;
   typedef typename M::V V;
   typedef typename M::E ME;
-  typedef WgLds<T, KS, MB> L;
+  typedef WgLds<T, KS, MB, SJ> L;
+  constexpr int TW = L::TW, LW = L::LW;
   constexpr int KK = KS * KS;
   constexpr int r = KS / 2;
   constexpr int P = M::P;
@@ -336,8 +344,8 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
       // element-wise through registers (2-byte x with odd W or unaligned x)
       T* __restrict__ dst = reinterpret_cast<T*>(dstb);
       const BufRes xres = make_buf(x + (int64_t)p.n * CHW, (uint32_t)(CHW * E));
-      for (int idx = tid; idx < L::kXRows * kWgLW; idx += NT) {
-        const int pr = idx / kWgLW, j = idx - pr * kWgLW;
+      for (int idx = tid; idx < L::kXRows * LW; idx += NT) {
+        const int pr = idx / LW, j = idx - pr * LW;
         const int rr = pr >> 4, c = pr & 15;
         const int ch = cb * 16 + c, hh = p.h + (rr - r) * d, gw = p.w0 - kWgPad + j;
         const bool ok = ch < C && (unsigned)hh < (unsigned)H && (unsigned)gw < (unsigned)W;
@@ -372,7 +380,7 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
           }
         }
       };
-      if (p.w0 + kWgTW <= W)
+      if (p.w0 + TW <= W)
         copies(std::false_type{});
       else
         copies(std::true_type{});
@@ -380,10 +388,10 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
       // element-wise through registers
       uint16_t* __restrict__ dy = reinterpret_cast<uint16_t*>(dstb + L::kYOff);
       T* __restrict__ dg = reinterpret_cast<T*>(dstb + L::kGOff);
-      constexpr int PY = kYReg ? 0 : L::kYRows * kWgTW, PG = 16 * kWgTW;
+      constexpr int PY = kYReg ? 0 : L::kYRows * TW, PG = 16 * TW;
       for (int idx = tid; idx < PY + PG; idx += NT) {
         if (idx < PY) {
-          const int row = idx / kWgTW, j = idx - row * kWgTW;
+          const int row = idx / TW, j = idx - row * TW;
           const int i = row;
           const int w = p.w0 + j;
           const uint32_t off =
@@ -394,7 +402,7 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
               (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(yres, off, 0, 0);
         } else {
           const int k2 = idx - PY;
-          const int row = k2 / kWgTW, j = k2 - row * kWgTW;
+          const int row = k2 / TW, j = k2 - row * TW;
           const int ch = cb * 16 + row, w = p.w0 + j;
           const uint32_t off =
               (ch < C && w < W) ? ((uint32_t)ch * (uint32_t)HW + rowel + (uint32_t)w) * E : kOob;
@@ -412,7 +420,7 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
   //      two 8-byte halves of the row's chunk (u % 32) / 2, swizzled as the
   //      LDS-direct copies place them.  Columns past the image and channels
   //      >= C read zero.
-  constexpr int YU = kYReg ? MB * 16 * (kWgTW / 4) : 1;  // 4-column pieces per step
+  constexpr int YU = kYReg ? MB * 16 * (TW / 4) : 1;  // 4-column pieces per step
   constexpr int YUT = (YU + NT - 1) / NT;
   f32x4 yreg[YUT];
   auto yload = [&](const WgPos& p) {
@@ -477,7 +485,7 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
   {
     const int row = step_beg / g.col_blocks;
     nxt.cbk = step_beg - row * g.col_blocks;
-    nxt.w0 = nxt.cbk * kWgTW;
+    nxt.w0 = nxt.cbk * TW;
     nxt.n = row / H;
     nxt.h = row - nxt.n * H;
   }
@@ -489,8 +497,7 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  const int wl = 32 * sg + 8 * quad;  // this lane's first token within the step
-  const int ky = (wl >> 3) ^ col16;   // its chunk position in rows with (row & 15) = col16
+  const int wl = 32 * sg + 8 * quad;  // this lane's first token within a 128-column subsegment
   // element index (from the buffer start) of the lane's first x value per tap
   int xel[TPH];
 #pragma unroll
@@ -508,71 +515,77 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
       nxt.advance(g);
     }
     const uint32_t* __restrict__ bb = wsm + buf * L::kBuf;
-    V bfr[MB][P];
 #pragma unroll
-    for (int ib = 0; ib < MB; ++ib)
+    for (int j = 0; j < SJ; ++j) {
+      // subsegment j: this lane's tokens wl + 128 j
+      const int wlj = wl + kWgTW * j;
+      const int kyj = (wlj >> 3) ^ col16;
+      V bfr[MB][P];
 #pragma unroll
-      for (int pp = 0; pp < P; ++pp)
-        bfr[ib][pp] = __builtin_bit_cast(
-            V, *reinterpret_cast<const u32x4*>(bb + L::kYOff + ((pp * MB + ib) * 16 + col16) * L::kYD +
-                                               4 * ky));
-    // branch gradient of channel col16 at the lane's 8 tokens
-    float gv[8];
-    {
-      const uint32_t* __restrict__ gr = bb + L::kGOff + col16 * L::kGD;
-      if constexpr (E == 4) {
-        const int kg = wl >> 2;
-        const u32x4 a0 = *reinterpret_cast<const u32x4*>(gr + 4 * (kg ^ col16));
-        const u32x4 a1 = *reinterpret_cast<const u32x4*>(gr + 4 * ((kg + 1) ^ col16));
+      for (int ib = 0; ib < MB; ++ib)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          gv[e] = __uint_as_float(a0[e]);
-          gv[4 + e] = __uint_as_float(a1[e]);
-        }
-      } else {
-        typedef T T8 __attribute__((ext_vector_type(8)));
-        const T8 t8 = __builtin_bit_cast(T8, *reinterpret_cast<const u32x4*>(gr + 4 * ky));
+        for (int pp = 0; pp < P; ++pp)
+          bfr[ib][pp] = __builtin_bit_cast(
+              V, *reinterpret_cast<const u32x4*>(bb + L::kYOff + ((pp * MB + ib) * 16 + col16) * L::kYD +
+                                                 4 * kyj));
+      // branch gradient of channel col16 at the lane's 8 tokens
+      float gv[8];
+      {
+        const uint32_t* __restrict__ gr = bb + L::kGOff + col16 * L::kGD;
+        if constexpr (E == 4) {
+          const int kg = wlj >> 2;
+          const u32x4 a0 = *reinterpret_cast<const u32x4*>(gr + 4 * (kg ^ col16));
+          const u32x4 a1 = *reinterpret_cast<const u32x4*>(gr + 4 * ((kg + 1) ^ col16));
 #pragma unroll
-        for (int e = 0; e < 8; ++e) gv[e] = to_f(t8[e]);
-      }
-    }
-    // The A fragment of tap tt+1 (x reads, products, bf16 split) is formed
-    // while tap tt's MFMAs run: the scheduling groups below put its LDS reads
-    // first and then interleave each MFMA with 3 VALU instructions (measured
-    // 3-5% faster than the compiler's clustering, which left the MFMA pipe
-    // idle during each tap's VALU stretch)
-    auto make_afr = [&](int tt, V (&af)[P]) {
-      float dk[8];
+          for (int e = 0; e < 4; ++e) {
+            gv[e] = __uint_as_float(a0[e]);
+            gv[4 + e] = __uint_as_float(a1[e]);
+          }
+        } else {
+          typedef T T8 __attribute__((ext_vector_type(8)));
+          const T8 t8 = __builtin_bit_cast(T8, *reinterpret_cast<const u32x4*>(gr + 4 * kyj));
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dk[e] = gv[e] * lds_elem<T>(bb, xel[tt] + e);
-      M::pack(dk, af);
-      if constexpr (kVBias)
-        dbs[tt] += ((dk[0] + dk[1]) + (dk[2] + dk[3])) + ((dk[4] + dk[5]) + (dk[6] + dk[7]));
-    };
-    V afc[P];
-    make_afr(0, afc);
-#pragma unroll
-    for (int tt = 0; tt < TPH; ++tt) {
-      const int t = th * TPH + tt;  // wave-uniform
-      if (KK % NH != 0 && t >= KK) break;
-      V afn[P];
-      if (tt + 1 < TPH) make_afr(tt + 1, afn);
-#pragma unroll
-      for (int ib = 0; ib < MB; ++ib) acc[tt][ib] = M::mac(afc, bfr[ib], acc[tt][ib]);
-      if constexpr (!kVBias) {
-#pragma unroll
-        for (int pp = 0; pp < P; ++pp) accb[tt] = M::mac1(afc[pp], ones, accb[tt]);
-      }
-      if (tt + 1 < TPH) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // LDS reads
-#pragma unroll
-        for (int i = 0; i < MB * (P == 2 ? 3 : 1) + (kVBias ? 0 : P); ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+          for (int e = 0; e < 8; ++e) gv[e] = to_f(t8[e]);
         }
       }
+      // The A fragment of tap tt+1 (x reads, products, bf16 split) is formed
+      // while tap tt's MFMAs run: the scheduling groups below put its LDS reads
+      // first and then interleave each MFMA with 3 VALU instructions (measured
+      // 3-5% faster than the compiler's clustering, which left the MFMA pipe
+      // idle during each tap's VALU stretch)
+      auto make_afr = [&](int tt, V (&af)[P]) {
+        float dk[8];
 #pragma unroll
-      for (int pp = 0; pp < P; ++pp) afc[pp] = afn[pp];
+        for (int e = 0; e < 8; ++e) dk[e] = gv[e] * lds_elem<T>(bb, xel[tt] + kWgTW * j + e);
+        M::pack(dk, af);
+        if constexpr (kVBias)
+          dbs[tt] += ((dk[0] + dk[1]) + (dk[2] + dk[3])) + ((dk[4] + dk[5]) + (dk[6] + dk[7]));
+      };
+      V afc[P];
+      make_afr(0, afc);
+#pragma unroll
+      for (int tt = 0; tt < TPH; ++tt) {
+        const int t = th * TPH + tt;  // wave-uniform
+        if (KK % NH != 0 && t >= KK) break;
+        V afn[P];
+        if (tt + 1 < TPH) make_afr(tt + 1, afn);
+#pragma unroll
+        for (int ib = 0; ib < MB; ++ib) acc[tt][ib] = M::mac(afc, bfr[ib], acc[tt][ib]);
+        if constexpr (!kVBias) {
+#pragma unroll
+          for (int pp = 0; pp < P; ++pp) accb[tt] = M::mac1(afc[pp], ones, accb[tt]);
+        }
+        if (tt + 1 < TPH) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // LDS reads
+#pragma unroll
+          for (int i = 0; i < MB * (P == 2 ? 3 : 1) + (kVBias ? 0 : P); ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+          }
+        }
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp) afc[pp] = afn[pp];
+      }
     }
     if (more) ystore(buf ^ 1);
     __builtin_amdgcn_s_waitcnt(0);
@@ -767,7 +780,13 @@ int wg_with_mb(int mb, F&& f) {
 
 // Splits: kWgMaxSplits, or fewer so that each has kWgMinSteps steps; one
 // split means grad_weight / grad_bias are written directly.
-void wgrad_geom(WGradGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int d0, int d1, int d2) {
+// Columns per step: 256 for 2-byte types on images whose width is a multiple
+// of 256 (twice the MFMA work per step and per barrier), else 128; a
+// function of the dtype and the width only, so the workspace query agrees.
+int wg_step_cols(int64_t w, int esz) { return (esz == 2 && w % (2 * kWgTW) == 0) ? 2 * kWgTW : kWgTW; }
+
+void wgrad_geom(WGradGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int d0, int d1, int d2,
+                int tw) {
   g.N = (int)n;
   g.C = (int)c;
   g.H = (int)h;
@@ -777,7 +796,8 @@ void wgrad_geom(WGradGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int d0
   g.d2 = d2;
   g.cblocks = (int)((c + 15) / 16);
   g.ihalves = c > 64 ? 2 : 1;
-  g.col_blocks = (int)((w + kWgTW - 1) / kWgTW);
+  g.tw = tw;
+  g.col_blocks = (int)((w + tw - 1) / tw);
   const int64_t steps = n * h * g.col_blocks;
   int64_t splits = kWgMaxSplits;
   if (splits > (steps + kWgMinSteps - 1) / kWgMinSteps) splits = (steps + kWgMinSteps - 1) / kWgMinSteps;
@@ -810,7 +830,7 @@ extern "C" int64_t ddpm_gen_bwd_w_workspace_bytes(int64_t n, int64_t c, int64_t 
   if (dtype < kF32 || dtype > kF16) return 0;
   if (n * h * ((w + kWgTW - 1) / kWgTW) > 0x7fffffffLL) return 0;
   WGradGeom g;
-  wgrad_geom(g, n, c, h, w, 1, 1, 1);
+  wgrad_geom(g, n, c, h, w, 1, 1, 1, wg_step_cols(w, dtype == kF32 ? 4 : 2));
   return wg_partial_bytes(g, c, kernel_size);
 }
 
@@ -845,7 +865,7 @@ int bw_run(const void* x, const void* y, const void* grad_out, void* grad_weight
   // 32-bit indices of the split reduction
   if ((int64_t)3 * kernel_size * kernel_size * c * (c + 1) > 0x7fffffffLL) return kUnsupported;
   WGradGeom g;
-  wgrad_geom(g, n, c, h, w, gg.d0, gg.d1, gg.d2);
+  wgrad_geom(g, n, c, h, w, gg.d0, gg.d1, gg.d2, wg_step_cols(w, esz));
   const int64_t need = wg_partial_bytes(g, c, kernel_size);
   if (need > 0 && (!workspace || workspace_bytes < need)) return kWorkspaceTooSmall;
   // LDS-direct dword copies of x rows need every row to start on a dword boundary
@@ -870,19 +890,20 @@ int bw_run(const void* x, const void* y, const void* grad_out, void* grad_weight
   float* pb = g.direct ? nullptr : pw + (int64_t)g.splits * 3 * kk * c * c;
   return wg_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
-    auto launch = [&](auto ks, auto mbc) {
+    auto launch = [&](auto ks, auto mbc, auto sjc) {
       constexpr int KS = decltype(ks)::value;
       constexpr int MB = decltype(mbc)::value;
+      constexpr int SJ = decltype(sjc)::value;
       constexpr int KKc = KS * KS;
-      typedef WgLds<T, KS, MB> L;
+      typedef WgLds<T, KS, MB, SJ> L;
       const size_t stage = (size_t)2 * L::kBuf * 4;
       const size_t red = (size_t)(kWgSegs * KKc * 16 * (MB * 16 + 1) + KKc * kWgSegs * 16) * sizeof(float);
       const size_t lds = stage > red ? stage : red;
       const dim3 grid((unsigned)(g.dw_blocks + helpers));
       const int ae = allow_dynamic_lds(
-          reinterpret_cast<const void*>(&gen_bwd_w_partial_kernel<T, KS, MB>), lds);
+          reinterpret_cast<const void*>(&gen_bwd_w_partial_kernel<T, KS, MB, SJ>), lds);
       if (ae != 0) return ae;
-      hipLaunchKernelGGL((gen_bwd_w_partial_kernel<T, KS, MB>), grid,
+      hipLaunchKernelGGL((gen_bwd_w_partial_kernel<T, KS, MB, SJ>), grid,
                          dim3(64 * kWgSegs * WgTaps<KS>::kGroups), lds, stream, (const T*)x,
                          (const T*)y, (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g,
                          helpers > 0 && fin ? *fin : none, helpers > 0 && yp ? *yp : nopack);
@@ -908,8 +929,14 @@ int bw_run(const void* x, const void* y, const void* grad_out, void* grad_weight
       return (int)hipGetLastError();
     };
     return wg_with_mb(mb, [&](auto mbc) {
-      if (kernel_size == 1) return launch(std::integral_constant<int, 1>(), mbc);
-      return launch(std::integral_constant<int, 3>(), mbc);
+      auto by_k = [&](auto sjc) {
+        if (kernel_size == 1) return launch(std::integral_constant<int, 1>(), mbc, sjc);
+        return launch(std::integral_constant<int, 3>(), mbc, sjc);
+      };
+      if constexpr (sizeof(T) == 2) {
+        if (g.tw == 2 * kWgTW) return by_k(std::integral_constant<int, 2>());
+      }
+      return by_k(std::integral_constant<int, 1>());
     });
   });
 }
