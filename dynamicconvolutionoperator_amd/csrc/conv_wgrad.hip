@@ -39,7 +39,6 @@ namespace ddpm {
 constexpr int kCwSegs = 4;                  // 32-token segments per step
 constexpr int kCwTW = 32 * kCwSegs;         // columns per step
 constexpr int kCwPad = 8;                   // staged column halo (16 bytes of 2-byte values)
-constexpr int kCwLW = kCwTW + 2 * kCwPad;   // staged cat columns
 constexpr int kCwNW = 3 * kCwSegs;          // waves: segments x kernel rows
 constexpr int kCwThreads = 64 * kCwNW;
 constexpr int kCwMaxSplits = 16;
@@ -49,7 +48,8 @@ struct CwGeom {
   int N, C, CI, H, W;   // C output planes (co), CI = 4C input planes (ci)
   int cblocks;          // ceil(CI / 16)
   int ohalves;          // 1, or 2 when C > 64: a workgroup covers 64 output planes co
-  int col_blocks;       // ceil(W / kCwTW)
+  int tw;               // columns per step: kCwTW, or 2 * kCwTW (cw_step_cols)
+  int col_blocks;       // ceil(W / tw)
   int splits, steps, steps_per_split;
   int direct;
   int x16;              // cat rows hold whole 16-byte chunks: one 16-byte copy per row
@@ -63,13 +63,15 @@ struct CwGeom {
 //   gO rows  [P][MB*16][kYD] 2-byte elements (grad_out, or the bf16 hi / lo
 //                           rows of an fp32 grad_out): 16 chunks of 16
 //                           bytes, chunk k of row i at position k ^ (i & 15)
-template <typename T, int MB>
+template <typename T, int MB, int SJ>
 struct CwLds {
   static constexpr int P = Mma<T>::P;
+  static constexpr int TW = kCwTW * SJ;  // columns per step
+  static constexpr int LW = TW + 2 * kCwPad;
   static constexpr int kPerD = 4 / (int)sizeof(T);
-  static constexpr int kXD = kCwLW / kPerD;
+  static constexpr int kXD = LW / kPerD;
   static constexpr int kXSD = kXD + (sizeof(T) == 4 ? 1 : 3);
-  static constexpr int kYC = kCwTW / 8;  // 16-byte chunks per gO row (16)
+  static constexpr int kYC = TW / 8;  // 16-byte chunks per gO row (16 or 32)
   static constexpr int kYD = 4 * kYC;
   static constexpr int kXRows = 3 * 16;
   static constexpr int kYRows = P * MB * 16;
@@ -77,7 +79,8 @@ struct CwLds {
   static constexpr int kBuf = kYOff + kYRows * kYD;
   static_assert(kXSD % 2 == 1, "odd cat-row pitch");
   static_assert(kXD % 4 == 0, "16-byte copies move whole rows");
-  static_assert(kYC == 16, "the chunk swizzle needs 16 chunks per row");
+  static_assert(kYC % 16 == 0, "the chunk swizzle needs 16 chunks per row");
+  static_assert(kXD / 4 <= 64, "one 16-byte cat copy per lane and row");
 };
 
 template <typename T>
@@ -99,7 +102,7 @@ __device__ __forceinline__ int cw_pair_plane(int cb, int c) {
 struct CwPos {
   int n, h, w0, cbk;
   __device__ __forceinline__ void advance(const CwGeom& g) {
-    w0 += kCwTW;
+    w0 += g.tw;
     if (++cbk == g.col_blocks) {
       cbk = 0;
       w0 = 0;
@@ -113,15 +116,19 @@ struct CwPos {
 
 // PP (fp32): `cat` holds pair planes (kF32Pairs); staged row c < 8 of a
 // 16-plane block holds the hi plane of its channels (2c, 2c+1), row 8 + c
-// their lo plane.
-template <typename T, int MB, bool PP = false>
+// their lo plane.  SJ: 128-column subsegments per step (2 for 2-byte types on
+// wide images: twice the work per step and per barrier; each wave takes its
+// 32-token segment in both).
+template <typename T, int MB, bool PP = false, int SJ = 1>
 __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
     const T* __restrict__ cat, const T* __restrict__ gout, float* __restrict__ pw,
     float* __restrict__ pb, T* __restrict__ dw_out, T* __restrict__ db_out, CwGeom g) {
   typedef Mma<T> M;
   typedef typename M::V V;
   typedef typename M::E ME;
-  typedef CwLds<T, MB> L;
+  typedef CwLds<T, MB, SJ> L;
+  constexpr int TW = L::TW, LW = L::LW;
+  static_assert(!PP || SJ == 1, "pair planes: 128-column steps");
   constexpr int P = M::P;
   constexpr int E = (int)sizeof(T);
   // fp32: grad_out goes through registers and is split into bf16 hi / lo rows
@@ -199,8 +206,8 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
     } else {
       // element-wise through registers (W not a multiple of a 16-byte chunk)
       T* __restrict__ dst = reinterpret_cast<T*>(dstb);
-      for (int idx = tid; idx < L::kXRows * kCwLW; idx += kCwThreads) {
-        const int pr = idx / kCwLW, j = idx - pr * kCwLW;
+      for (int idx = tid; idx < L::kXRows * LW; idx += kCwThreads) {
+        const int pr = idx / LW, j = idx - pr * LW;
         const int rr = pr >> 4, c = pr & 15;
         const int ch = PP ? cw_pair_plane(cb, c) : cb * 16 + c;
         const int hh = p.h + rr - 1, gw = p.w0 - kCwPad + j;
@@ -214,7 +221,7 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
     const uint32_t rowel = (uint32_t)(p.h * W);
     if (g.g16) {
       const uint32_t ystep = (rowel + (uint32_t)p.w0) * 2u;
-      const bool full = p.w0 + kCwTW <= W;
+      const bool full = p.w0 + TW <= W;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int ii = wave + kCwNW * j;
@@ -227,9 +234,9 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
       }
     } else {
       uint16_t* __restrict__ dy = reinterpret_cast<uint16_t*>(dstb + L::kYOff);
-      constexpr int PY = kYReg ? 0 : L::kYRows * kCwTW;
+      constexpr int PY = kYReg ? 0 : L::kYRows * TW;
       for (int idx = tid; idx < PY; idx += kCwThreads) {
-        const int row = idx / kCwTW, j = idx - row * kCwTW;
+        const int row = idx / TW, j = idx - row * TW;
         const int i = row;
         const int w = p.w0 + j;
         const uint32_t off =
@@ -248,7 +255,7 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
   //      the gO rows of LDS buffer `buf` (ystore, after them), as the two
   //      8-byte halves of the row's chunk (u % 32) / 2 in the swizzled layout.
   //      Columns past the image and planes >= C read zero.
-  constexpr int YU = kYReg ? MB * 16 * (kCwTW / 4) : 1;
+  constexpr int YU = kYReg ? MB * 16 * (TW / 4) : 1;
   constexpr int YUT = (YU + kCwThreads - 1) / kCwThreads;
   f32x4 yreg[YUT];
   auto yload = [&](const CwPos& p) {
@@ -306,7 +313,7 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
   {
     const int row = step_beg / g.col_blocks;
     nxt.cbk = step_beg - row * g.col_blocks;
-    nxt.w0 = nxt.cbk * kCwTW;
+    nxt.w0 = nxt.cbk * TW;
     nxt.n = row / H;
     nxt.h = row - nxt.n * H;
   }
@@ -318,8 +325,7 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  const int wl = 32 * sg + 8 * quad;  // this lane's first token within the step
-  const int ky = (wl >> 3) ^ col16;   // its chunk position in rows with (row & 15) = col16
+  const int wl = 32 * sg + 8 * quad;  // this lane's first token within a 128-column subsegment
   // element index of the lane's first cat value per tap kj (row ki, plane col16)
   int xel[3];
 #pragma unroll
@@ -338,55 +344,60 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
       nxt.advance(g);
     }
     const uint32_t* __restrict__ bb = csm + buf * L::kBuf;
-    V bfr[MB][P];
 #pragma unroll
-    for (int ib = 0; ib < MB; ++ib)
-#pragma unroll
-      for (int pp = 0; pp < P; ++pp)
-        bfr[ib][pp] = __builtin_bit_cast(
-            V, *reinterpret_cast<const u32x4*>(bb + L::kYOff + ((pp * MB + ib) * 16 + col16) * L::kYD +
-                                               4 * ky));
-    if (do_bias) {
-      // grad_bias partials: ones x gO block bib (every row of D gets the sum)
+    for (int j = 0; j < SJ; ++j) {
+      // subsegment j: this lane's tokens wl + 128 j
+      const int kyj = ((wl + kCwTW * j) >> 3) ^ col16;
+      V bfr[MB][P];
 #pragma unroll
       for (int ib = 0; ib < MB; ++ib)
-        if (ib == bib)
 #pragma unroll
-          for (int pp = 0; pp < P; ++pp) accb = M::mac1(ones, bfr[ib][pp], accb);
-    }
+        for (int pp = 0; pp < P; ++pp)
+          bfr[ib][pp] = __builtin_bit_cast(
+              V, *reinterpret_cast<const u32x4*>(bb + L::kYOff + ((pp * MB + ib) * 16 + col16) * L::kYD +
+                                                 4 * kyj));
+      if (do_bias) {
+        // grad_bias partials: ones x gO block bib (every row of D gets the sum)
 #pragma unroll
-    for (int kj = 0; kj < 3; ++kj) {
-      V afr[P];
-      if constexpr (PP) {
-        uint32_t dh[8], dl[8];
+        for (int ib = 0; ib < MB; ++ib)
+          if (ib == bib)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          dh[e] = bb[ppel + kj + e];
-          dl[e] = bb[ppel + 8 * L::kXSD + kj + e];
-        }
-        u32x4 h4, l4;
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          h4[jj] = __builtin_amdgcn_perm(dh[2 * jj + 1], dh[2 * jj], ppsel);
-          l4[jj] = __builtin_amdgcn_perm(dl[2 * jj + 1], dl[2 * jj], ppsel);
-        }
-        afr[0] = __builtin_bit_cast(V, h4);
-        afr[1] = __builtin_bit_cast(V, l4);
-      } else if constexpr (sizeof(T) == 4) {
-        float xv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xv[e] = cw_lds_elem<T>(bb, xel[kj] + e);
-        M::pack(xv, afr);
-      } else {
-        // the 8 two-byte values as staged, paired into dwords (no fp32 round trip)
-        const uint16_t* __restrict__ xb = reinterpret_cast<const uint16_t*>(bb) + xel[kj];
-        u32x4 wv;
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) wv[e2] = (uint32_t)xb[2 * e2] | ((uint32_t)xb[2 * e2 + 1] << 16);
-        afr[0] = __builtin_bit_cast(V, wv);
+            for (int pp = 0; pp < P; ++pp) accb = M::mac1(ones, bfr[ib][pp], accb);
       }
 #pragma unroll
-      for (int ib = 0; ib < MB; ++ib) acc[kj][ib] = M::mac(afr, bfr[ib], acc[kj][ib]);
+      for (int kj = 0; kj < 3; ++kj) {
+        V afr[P];
+        if constexpr (PP) {
+          uint32_t dh[8], dl[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            dh[e] = bb[ppel + kCwTW * j + kj + e];
+            dl[e] = bb[ppel + 8 * L::kXSD + kCwTW * j + kj + e];
+          }
+          u32x4 h4, l4;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            h4[jj] = __builtin_amdgcn_perm(dh[2 * jj + 1], dh[2 * jj], ppsel);
+            l4[jj] = __builtin_amdgcn_perm(dl[2 * jj + 1], dl[2 * jj], ppsel);
+          }
+          afr[0] = __builtin_bit_cast(V, h4);
+          afr[1] = __builtin_bit_cast(V, l4);
+        } else if constexpr (sizeof(T) == 4) {
+          float xv[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) xv[e] = cw_lds_elem<T>(bb, xel[kj] + kCwTW * j + e);
+          M::pack(xv, afr);
+        } else {
+          // the 8 two-byte values as staged, paired into dwords (no fp32 round trip)
+          const uint16_t* __restrict__ xb = reinterpret_cast<const uint16_t*>(bb) + xel[kj] + kCwTW * j;
+          u32x4 wv;
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) wv[e2] = (uint32_t)xb[2 * e2] | ((uint32_t)xb[2 * e2 + 1] << 16);
+          afr[0] = __builtin_bit_cast(V, wv);
+        }
+#pragma unroll
+        for (int ib = 0; ib < MB; ++ib) acc[kj][ib] = M::mac(afr, bfr[ib], acc[kj][ib]);
+      }
     }
     if (more) ystore(buf ^ 1);
     __builtin_amdgcn_s_waitcnt(0);
@@ -522,7 +533,12 @@ int cw_with_mb(int mb, F&& f) {
   }
 }
 
-void cw_geom(CwGeom& g, int64_t n, int64_t c, int64_t h, int64_t w) {
+// Columns per step: 256 for 2-byte types on images whose width is a multiple
+// of 256, else 128; a function of the dtype and the width only, so the
+// workspace query agrees.
+int cw_step_cols(int64_t w, int esz) { return (esz == 2 && w % (2 * kCwTW) == 0) ? 2 * kCwTW : kCwTW; }
+
+void cw_geom(CwGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int tw) {
   g.N = (int)n;
   g.C = (int)c;
   g.CI = (int)(4 * c);
@@ -530,7 +546,8 @@ void cw_geom(CwGeom& g, int64_t n, int64_t c, int64_t h, int64_t w) {
   g.W = (int)w;
   g.cblocks = (int)((4 * c + 15) / 16);
   g.ohalves = c > 64 ? 2 : 1;
-  g.col_blocks = (int)((w + kCwTW - 1) / kCwTW);
+  g.tw = tw;
+  g.col_blocks = (int)((w + tw - 1) / tw);
   const int64_t steps = n * h * g.col_blocks;
   int64_t splits = kCwMaxSplits;
   if (splits > (steps + kCwMinSteps - 1) / kCwMinSteps) splits = (steps + kCwMinSteps - 1) / kCwMinSteps;
@@ -560,7 +577,7 @@ extern "C" int64_t ddpm_fuse_conv_bwd_weight_workspace_bytes(int64_t n, int64_t 
   if (n <= 0 || c <= 0 || h <= 0 || w <= 0 || dtype < kF32 || dtype > kF16) return 0;
   if (n * h * ((w + kCwTW - 1) / kCwTW) > 0x7fffffffLL) return 0;
   CwGeom g;
-  cw_geom(g, n, c, h, w);
+  cw_geom(g, n, c, h, w, cw_step_cols(w, dtype == kF32 ? 4 : 2));
   return cw_partial_bytes(g);
 }
 
@@ -597,7 +614,7 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
   // 32-bit buffer offsets inside one image's planes
   if (4 * c * h * w * esz > 0x7fffffffLL) return kUnsupported;
   CwGeom g;
-  cw_geom(g, n, c, h, w);
+  cw_geom(g, n, c, h, w, pp ? kCwTW : cw_step_cols(w, esz));
   const int64_t need = cw_partial_bytes(g);
   if (need > 0 && (!workspace || workspace_bytes < need)) return kWorkspaceTooSmall;
   g.x16 = (w % (16 / esz) == 0) && ((uintptr_t)cat % 16 == 0);
@@ -608,13 +625,15 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
   const int mb = c > 64 ? 4 : (int)((c + 15) / 16);  // 16-plane blocks of co per workgroup
   return cw_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
-    return cw_with_mb(mb, [&](auto mbc) {
+    auto launch = [&](auto mbc, auto sjc) {
       constexpr int MB = decltype(mbc)::value;
-      typedef CwLds<T, MB> L;
+      constexpr int SJ = decltype(sjc)::value;
+      typedef CwLds<T, MB, SJ> L;
       const size_t stage = (size_t)2 * L::kBuf * 4;
       const size_t red = (size_t)(kCwSegs * 9 * 16 * (MB * 16 + 1) + kCwSegs * 16) * sizeof(float);
       const size_t lds = stage > red ? stage : red;
-      auto kern = pp ? conv_wgrad_partial_kernel<T, MB, sizeof(T) == 4> : conv_wgrad_partial_kernel<T, MB>;
+      auto kern = pp ? conv_wgrad_partial_kernel<T, MB, sizeof(T) == 4 && SJ == 1, SJ>
+                     : conv_wgrad_partial_kernel<T, MB, false, SJ>;
       const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
       if (ae != 0) return ae;
       hipLaunchKernelGGL(kern, dim3((unsigned)(g.splits * g.cblocks * g.ohalves)), dim3(kCwThreads), lds, stream,
@@ -626,6 +645,12 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
                          dim3(256), 0, stream, (const float*)pw, (const float*)pb, (T*)grad_weight,
                          (T*)grad_bias, (int)c, (int)(4 * c), g.splits);
       return (int)hipGetLastError();
+    };
+    return cw_with_mb(mb, [&](auto mbc) {
+      if constexpr (sizeof(T) == 2) {
+        if (g.tw == 2 * kCwTW) return launch(mbc, std::integral_constant<int, 2>());
+      }
+      return launch(mbc, std::integral_constant<int, 1>());
     });
   });
 }

@@ -39,7 +39,6 @@ namespace ddpm {
 constexpr int kWgSegs = 4;                   // 32-token segments per step
 constexpr int kWgTW = 32 * kWgSegs;          // columns per step
 constexpr int kWgPad = 8;                    // staged column halo (>= dilation), even
-constexpr int kWgLW = kWgTW + 2 * kWgPad;    // staged x columns
 constexpr int kWgMaxDil = kWgPad;
 constexpr int kWgMaxSplits = 16;             // fp32 partials at most (the reference's bound)
 constexpr int kWgMinSteps = 4;               // steps per split at least
