@@ -59,9 +59,9 @@ __global__ __launch_bounds__(256) void gen_pack_wt_kernel(const T* __restrict__ 
   if (idx < total) yt_pack_item<T, KS, MB>(wt, pk, C, nc32, idx);
 }
 
-// One LDS staging buffer (dwords): x rows [32 channels][kXS] then the
-// weight slice [KS taps][MB][P][64 lanes][4 dwords].
-template <typename T, int KS, int MB>
+// One LDS staging buffer (dwords): x rows [CH * 32 channels][kXS] then the
+// weight slices [CH chunks][KS taps][MB][P][64 lanes][4 dwords].
+template <typename T, int KS, int MB, int CH>
 struct YtLds {
   static constexpr int kE = (int)sizeof(T);
   static constexpr int kPerD = 4 / kE;
@@ -71,19 +71,23 @@ struct YtLds {
   static constexpr int kXS = kXD + ((16 - kXD % 64) + 64) % 64;
   static constexpr int kXChunks = kXD / 4;                       // 16-byte chunks per row
   static constexpr int kXOff = 0;
-  static constexpr int kAOff = 32 * kXS;
-  static constexpr int kAUnits = KS * MB * yt_parts<T>() * 64;   // 16-byte units
+  static constexpr int kAOff = 32 * CH * kXS;
+  static constexpr int kAUnits1 = KS * MB * yt_parts<T>() * 64;  // 16-byte units of one chunk
+  static constexpr int kAUnits = CH * kAUnits1;
   static constexpr int kBuf = kAOff + 4 * kAUnits;
 };
 
-template <typename T, int KS, int MB>
+// CH: 32-channel chunks per stage (2 for 2-byte types when the chunk count
+// is even: twice the MFMA work per stage and per barrier, LDS 122 KB at
+// C = 64).
+template <typename T, int KS, int MB, int CH>
 __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restrict__ x,
                                                                const uint32_t* __restrict__ pk,
                                                                const T* __restrict__ gout,
                                                                T* __restrict__ gy, YGeom g) {
   typedef Mma<T> M;
   typedef typename M::V V;
-  typedef YtLds<T, KS, MB> L;
+  typedef YtLds<T, KS, MB, CH> L;
   constexpr int KK = KS * KS;
   constexpr int r = KS / 2;
   constexpr int P = M::P;
@@ -102,27 +106,28 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int col16 = lane & 15, quad = lane >> 4;
-  const int nstage = 3 * g.nc32 * KS;  // (b, cc, ki)
+  const int ncg = g.nc32 / CH;        // groups of CH chunks (CH divides nc32)
+  const int nstage = 3 * ncg * KS;    // (b, chunk group, ki)
 
   // x planes of image n (per-row resources cost ~20 scalar instructions per
   // row and stage; measured bf16 44.9 -> 41.6 us)
   const BufRes xres = make_buf(x + (int64_t)n * C * HW, (uint32_t)(C * HW * (int64_t)E));
-  // ---- stage s = ((b * nc32) + cc) * KS + ki -> LDS buffer `buf`
+  // ---- stage s = ((b * ncg) + cg) * KS + ki -> LDS buffer `buf`
   auto stage = [&](int s, int buf) {
     const int ki = s % KS;
-    const int bc = s / KS;
-    const int cc = bc % g.nc32, b = bc / g.nc32;
+    const int bg = s / KS;
+    const int cg = bg % ncg, b = bg / ncg;
     const int d = dil_of(b, g.d0, g.d1, g.d2);
     const int hh = h + (ki - r) * d;
     uint32_t* __restrict__ dstb = ysm + buf * L::kBuf;
-    // x rows: 32 channels of row hh, columns w0 - pad .. w0 + TW + pad
+    // x rows: 32 * CH channels of row hh, columns w0 - pad .. w0 + TW + pad
     if (g.x4) {
       // one resource for the image; a chunk outside the image (column, row or
       // channel) reads zero through its offset (W % 8 == 0: chunks are whole)
 #pragma unroll
-      for (int j = 0; j < 32 / kYtWaves; ++j) {
+      for (int j = 0; j < 32 * CH / kYtWaves; ++j) {
         const int cr = wave + kYtWaves * j;
-        const int ch = cc * 32 + cr;
+        const int ch = cg * CH * 32 + cr;
         const bool ok = ch < C && (unsigned)hh < (unsigned)H;
         const uint32_t rowel = (uint32_t)ch * (uint32_t)HW + (uint32_t)(hh * W);
 #pragma unroll
@@ -140,46 +145,57 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
     } else {
       // element-wise copy through registers (W % 8 != 0 or unaligned x)
       T* __restrict__ dst = reinterpret_cast<T*>(dstb);
-      for (int idx = tid; idx < 32 * kYtLW; idx += kYtThreads) {
+      for (int idx = tid; idx < 32 * CH * kYtLW; idx += kYtThreads) {
         const int cr = idx / kYtLW, j = idx - cr * kYtLW;
-        const int ch = cc * 32 + cr, gw = w0 - kYtPad + j;
+        const int ch = cg * CH * 32 + cr, gw = w0 - kYtPad + j;
         float v = 0.f;
         if (ch < C && (unsigned)hh < (unsigned)H && (unsigned)gw < (unsigned)W)
           v = to_f(x[((int64_t)n * C + ch) * HW + (int64_t)hh * W + gw]);
         dst[(L::kXOff + cr * L::kXS) * L::kPerD + j] = from_f<T>(v);
       }
     }
-    // weight slice of the stage's K taps: contiguous in the packed weight
-    const uint32_t* src = pk + (int64_t)(((ih * 3 * g.nc32 + bc) * KK + ki * KS) * MB * P * 64) * 4;
-    const BufRes pres = make_buf(src, (uint32_t)(L::kAUnits * 16));
+    // weight slices of the stage's K taps, one per chunk: each contiguous
+    // in the packed weight
 #pragma unroll
-    for (int j = 0; j < (L::kAUnits / 64 + kYtWaves - 1) / kYtWaves; ++j) {
-      const int u = wave + kYtWaves * j;
-      if ((L::kAUnits / 64) % kYtWaves == 0 || u < L::kAUnits / 64)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            pres, (__attribute__((address_space(3))) void*)(dstb + L::kAOff + 256 * u), 16,
-            (uint32_t)(u * 64 + lane) * 16u, 0, 0, 0);
+    for (int c = 0; c < CH; ++c) {
+      const int cc = cg * CH + c;
+      const uint32_t* src =
+          pk + (int64_t)(((ih * 3 * g.nc32 + b * g.nc32 + cc) * KK + ki * KS) * MB * P * 64) * 4;
+      const BufRes pres = make_buf(src, (uint32_t)(L::kAUnits1 * 16));
+#pragma unroll
+      for (int j = 0; j < (L::kAUnits1 / 64 + kYtWaves - 1) / kYtWaves; ++j) {
+        const int u = wave + kYtWaves * j;
+        if ((L::kAUnits1 / 64) % kYtWaves == 0 || u < L::kAUnits1 / 64)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              pres,
+              (__attribute__((address_space(3))) void*)(dstb + L::kAOff + 4 * c * L::kAUnits1 + 256 * u),
+              16, (uint32_t)(u * 64 + lane) * 16u, 0, 0, 0);
+      }
     }
   };
 
-  // ---- branch-gradient values of this lane: channel cc*32 + 4e + quad at
-  //      its two pixels (held for the KS stages of one (b, cc))
+  // ---- branch-gradient values of this lane: channel cc*32 + 4e + quad of
+  //      each chunk cc of the group at its two pixels (held for the KS
+  //      stages of one (b, chunk group))
   const int px0 = 32 * wave + col16;  // pixel of block 0 within the tile; block 1 is +16
-  float gv[2][8];
-  auto load_g = [&](int bc) {
-    const int cc = bc % g.nc32, b = bc / g.nc32;
+  float gv[CH][2][8];
+  auto load_g = [&](int bg) {
+    const int cg = bg % ncg, b = bg / ncg;
     const BufRes gres = make_buf(gout + ((int64_t)n * 4 * C + (int64_t)(b + 1) * C) * HW,
                                  (uint32_t)(C * HW * (int64_t)E));
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      const int w = w0 + px0 + 16 * blk;
+    for (int c = 0; c < CH; ++c)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int ch = cc * 32 + 4 * e + quad;
-        const uint32_t off = (ch < C && w < W) ? (uint32_t)((int64_t)ch * HW + (int64_t)h * W + w) * E : kOob;
-        gv[blk][e] = buf_load1<T>(gres, off);
+      for (int blk = 0; blk < 2; ++blk) {
+        const int w = w0 + px0 + 16 * blk;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int ch = (cg * CH + c) * 32 + 4 * e + quad;
+          const uint32_t off =
+              (ch < C && w < W) ? (uint32_t)((int64_t)ch * HW + (int64_t)h * W + w) * E : kOob;
+          gv[c][blk][e] = buf_load1<T>(gres, off);
+        }
       }
-    }
   };
 
   f32x4 acc[2][MB];
@@ -196,44 +212,47 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
     const int buf = s & 1;
     if (s + 1 < nstage) stage(s + 1, buf ^ 1);
     const int ki = s % KS;
-    const int bc = s / KS;
-    const int b = bc / g.nc32;
+    const int bg = s / KS;
+    const int b = bg / ncg;
     const int d = dil_of(b, g.d0, g.d1, g.d2);
     const uint32_t* __restrict__ bb = ysm + buf * L::kBuf;
-    // this lane's x elements: channel 4e + quad, column pad + px + dw
-    const uint32_t* __restrict__ xq = bb + L::kXOff + quad * L::kXS;
 #pragma unroll
-    for (int kj = 0; kj < KS; ++kj) {
-      const int dw = (kj - r) * d;
-      V afr[MB][P];
+    for (int c = 0; c < CH; ++c) {
+      // this lane's x elements: channel 32c + 4e + quad, column pad + px + dw
+      const uint32_t* __restrict__ xq = bb + L::kXOff + (32 * c + quad) * L::kXS;
 #pragma unroll
-      for (int ib = 0; ib < MB; ++ib)
+      for (int kj = 0; kj < KS; ++kj) {
+        const int dw = (kj - r) * d;
+        V afr[MB][P];
 #pragma unroll
-        for (int pp = 0; pp < P; ++pp)
-          afr[ib][pp] = __builtin_bit_cast(
-              V, *reinterpret_cast<const u32x4*>(bb + L::kAOff +
-                                                 4 * ((((kj * MB) + ib) * P + pp) * 64 + lane)));
+        for (int ib = 0; ib < MB; ++ib)
 #pragma unroll
-      for (int blk = 0; blk < 2; ++blk) {
-        const int col = kYtPad + px0 + 16 * blk + dw;
-        float dk[8];
+          for (int pp = 0; pp < P; ++pp)
+            afr[ib][pp] = __builtin_bit_cast(
+                V, *reinterpret_cast<const u32x4*>(
+                       bb + L::kAOff + 4 * (c * L::kAUnits1 + (((kj * MB) + ib) * P + pp) * 64 + lane)));
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float xv;
-          if constexpr (sizeof(T) == 4)
-            xv = __uint_as_float(xq[4 * e * L::kXS + col]);
-          else
-            xv = to_f(reinterpret_cast<const T*>(xq + 4 * e * L::kXS)[col]);
-          dk[e] = gv[blk][e] * xv;
+        for (int blk = 0; blk < 2; ++blk) {
+          const int col = kYtPad + px0 + 16 * blk + dw;
+          float dk[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float xv;
+            if constexpr (sizeof(T) == 4)
+              xv = __uint_as_float(xq[4 * e * L::kXS + col]);
+            else
+              xv = to_f(reinterpret_cast<const T*>(xq + 4 * e * L::kXS)[col]);
+            dk[e] = gv[c][blk][e] * xv;
+          }
+          V bfr[P];
+          M::pack(dk, bfr);
+#pragma unroll
+          for (int ib = 0; ib < MB; ++ib) acc[blk][ib] = M::mac(afr[ib], bfr, acc[blk][ib]);
         }
-        V bfr[P];
-        M::pack(dk, bfr);
-#pragma unroll
-        for (int ib = 0; ib < MB; ++ib) acc[blk][ib] = M::mac(afr[ib], bfr, acc[blk][ib]);
       }
     }
-    // the next (b, cc) needs new branch-gradient values
-    if (ki == KS - 1 && s + 1 < nstage) load_g(bc + 1);
+    // the next (b, chunk group) needs new branch-gradient values
+    if (ki == KS - 1 && s + 1 < nstage) load_g(bg + 1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
@@ -469,9 +488,10 @@ int yt_launch(const void* x, const void* weight, const void* grad_out, void* gra
     using T = decltype(tag);
     return yt_with_mb(mb, [&](auto mbc) {
       constexpr int MB = decltype(mbc)::value;
-      auto launch = [&](auto ks) {
+      auto launch = [&](auto ks, auto chc) {
         constexpr int KS = decltype(ks)::value;
-        typedef YtLds<T, KS, MB> L;
+        constexpr int CH = decltype(chc)::value;
+        typedef YtLds<T, KS, MB, CH> L;
         if (pack) {
           const int units = g.ihalves * 3 * g.nc32 * KS * KS * MB * 64;
           hipLaunchKernelGGL((gen_pack_wt_kernel<T, KS, MB>), dim3((units + 255) / 256), dim3(256),
@@ -482,15 +502,22 @@ int yt_launch(const void* x, const void* weight, const void* grad_out, void* gra
         }
         const size_t lds = (size_t)2 * L::kBuf * 4;
         const int ae =
-            allow_dynamic_lds(reinterpret_cast<const void*>(&gen_bwd_y_kernel<T, KS, MB>), lds);
+            allow_dynamic_lds(reinterpret_cast<const void*>(&gen_bwd_y_kernel<T, KS, MB, CH>), lds);
         if (ae != 0) return ae;
-        hipLaunchKernelGGL((gen_bwd_y_kernel<T, KS, MB>), dim3((unsigned)tiles), dim3(kYtThreads), lds,
+        hipLaunchKernelGGL((gen_bwd_y_kernel<T, KS, MB, CH>), dim3((unsigned)tiles), dim3(kYtThreads), lds,
                            stream, (const T*)x, (const uint32_t*)workspace, (const T*)grad_out,
                            (T*)grad_y, g);
         return (int)hipGetLastError();
       };
-      if (kernel_size == 1) return launch(std::integral_constant<int, 1>());
-      if (kernel_size == 3) return launch(std::integral_constant<int, 3>());
+      auto by_ch = [&](auto ks) {
+        // 2-byte types with an even chunk count: two chunks per stage
+        if constexpr (sizeof(T) == 2) {
+          if (g.nc32 % 2 == 0) return launch(ks, std::integral_constant<int, 2>());
+        }
+        return launch(ks, std::integral_constant<int, 1>());
+      };
+      if (kernel_size == 1) return by_ch(std::integral_constant<int, 1>());
+      if (kernel_size == 3) return by_ch(std::integral_constant<int, 3>());
       return (int)kUnsupported;
     });
   });
