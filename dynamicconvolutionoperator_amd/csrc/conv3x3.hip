@@ -110,29 +110,32 @@ __global__ __launch_bounds__(256) void conv3x3_pack_kernel(const T* __restrict__
   for (int part = 0; part < P; ++part) dst[unit + part * 64] = __builtin_bit_cast(u32x4, o[part]);
 }
 
-// One LDS staging buffer (dwords): input rows [32 planes][kXS] -- a plane
-// holds its RS segment rows back to back, g.seg elements each -- then the A
-// slice [3 taps][MB][P][64 lanes][4 dwords].  The plane pitch is a
+// One LDS staging buffer (dwords): input rows [CH * 32 planes][kXS] -- a
+// plane holds its RS segment rows back to back, g.seg elements each -- then
+// the A slices [CH chunks][3 taps][MB][P][64 lanes][4 dwords].  The plane pitch is a
 // compile-time constant, so that the operand reads take their plane offsets
 // as immediates: the staged plane of one-row segments (WIDE: 272 elements)
 // or the largest over the segment shapes (8 rows x 48 columns), rounded to
 // 16 (mod 64) dwords so that a lane's 8 plane reads hit distinct banks.
-template <typename T, int MB, bool WIDE>
+template <typename T, int MB, bool WIDE, int CH = 1>
 struct CvLds {
   static constexpr int kE = (int)sizeof(T);
   static constexpr int kPerD = 4 / kE;
   static constexpr int kPC = 16 / kE;  // elements per 16-byte chunk
   static constexpr int kXD = (WIDE ? kCvPix + 2 * kCvPad : 8 * (32 + 2 * kCvPad)) / kPerD;
   static constexpr int kXS = kXD + ((16 - kXD % 64) + 64) % 64;
-  static constexpr int kAOff = 32 * kXS;
-  static constexpr int kAUnits = 3 * MB * cv_parts<T>() * 64;  // 16-byte units
+  static constexpr int kAOff = 32 * CH * kXS;
+  static constexpr int kAUnits1 = 3 * MB * cv_parts<T>() * 64;  // 16-byte units of one chunk
+  static constexpr int kAUnits = CH * kAUnits1;
   static constexpr int kBuf = kAOff + 4 * kAUnits;
   static_assert(kCvPix == 256, "segments hold at most kXD dwords per plane");
 };
 
 // out: the result in T (ks = 1), or with K split (ks > 1) the fp32 partial
 // sums part[ksplit][n][M][H*W] (no bias) that conv3x3_reduce_kernel adds up.
-template <typename T, bool BIAS, int MB, bool WIDE, bool PAIR = false>
+// CH: 32-plane chunks per stage (2 for 2-byte types when a K split's chunk
+// count is even: twice the MFMA work per stage and per barrier).
+template <typename T, bool BIAS, int MB, bool WIDE, bool PAIR = false, int CH = 1>
 __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict__ in,
                                                              const uint32_t* __restrict__ pk,
                                                              const T* __restrict__ bias,
@@ -140,7 +143,8 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
                                                              float* __restrict__ part, ConvGeom g) {
   typedef Mma<T> M;
   typedef typename M::V V;
-  typedef CvLds<T, MB, WIDE> L;
+  typedef CvLds<T, MB, WIDE, CH> L;
+  static_assert(!PAIR || CH == 1, "pair planes: one chunk per stage");
   constexpr int P = M::P;
   constexpr int E = (int)sizeof(T);
   extern __shared__ __attribute__((aligned(16))) uint32_t csm[];
@@ -161,11 +165,11 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int col16 = lane & 15, quad = lane >> 4;
-  // stages (cc, ki) of this workgroup's K split: s0 .. s0 + nstage - 1
+  // stages (group of CH chunks from cc0, ki) of this workgroup's K split
+  // (CH divides its chunk count)
   const int cc0 = ksplit * g.cc_per;
   const int cc1 = cc0 + g.cc_per < g.nc32 ? cc0 + g.cc_per : g.nc32;
-  const int s0 = 3 * cc0;
-  const int nstage = cc1 > cc0 ? 3 * (cc1 - cc0) : 0;
+  const int nstage = cc1 > cc0 ? 3 * ((cc1 - cc0) / CH) : 0;
   // this wave's 32 pixels: segment row wseg (wave-uniform), columns pcol0 ..
   const int wseg = (32 * wave) / g.sw;
   const int pcol0 = 32 * wave - wseg * g.sw;
@@ -187,18 +191,18 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
     cpos[part] = 4 * pc;                                     // dword offset in the plane
   }
   const int nparts = (cpp + 63) / 64;
-  // ---- stage s = cc * 3 + ki -> LDS buffer `buf`
+  // ---- stage s = (chunk group) * 3 + ki -> LDS buffer `buf`
   auto stage = [&](int s, int buf) {
     const int ki = s % 3;
-    const int cc = s / 3;
+    const int ccb = cc0 + (s / 3) * CH;  // first chunk of the group
     uint32_t* __restrict__ dstb = csm + buf * L::kBuf;
     if (g.x4) {
       // one resource for the image; a chunk outside the image (column, row or
       // plane) reads zero through its offset (W % 8 == 0: chunks are whole)
 #pragma unroll
-      for (int j = 0; j < 32 / kCvWaves; ++j) {
+      for (int j = 0; j < 32 * CH / kCvWaves; ++j) {
         const int cr = wave + kCvWaves * j;
-        const int ch = cc * 32 + cr;
+        const int ch = ccb * 32 + cr;
 #pragma unroll
         for (int part = 0; part < kParts; ++part) {
           if (part >= nparts) break;
@@ -218,25 +222,30 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
       // element-wise copy through registers (W % 8 != 0 or unaligned input)
       T* __restrict__ dst = reinterpret_cast<T*>(dstb);
       const int plen = g.rs * g.seg;
-      for (int idx = tid; idx < 32 * plen; idx += kCvThreads) {
+      for (int idx = tid; idx < 32 * CH * plen; idx += kCvThreads) {
         const int cr = idx / plen, j = idx - cr * plen;
         const int sgr = j / g.seg, col = j - sgr * g.seg;
-        const int ch = cc * 32 + cr, hh = h0 + sgr + ki - 1, gw = w0 - kCvPad + col;
+        const int ch = ccb * 32 + cr, hh = h0 + sgr + ki - 1, gw = w0 - kCvPad + col;
         const bool ok = ch < g.K && (unsigned)hh < (unsigned)H && (unsigned)gw < (unsigned)W;
         const uint32_t off = ok ? ((uint32_t)ch * (uint32_t)HW + (uint32_t)(hh * W + gw)) * E : kOob;
         dst[cr * L::kXS * L::kPerD + j] = from_f<T>(buf_load1<T>(xres, off));
       }
     }
-    // A slice of the stage's 3 taps: contiguous in the packed weight
-    const uint32_t* src = pk + ((((int64_t)mg * g.nc32 + cc) * 9 + ki * 3) * MB * P * 64) * 4;
-    const BufRes pres = make_buf(src, (uint32_t)(L::kAUnits * 16));
+    // A slices of the stage's 3 taps, one per chunk: each contiguous in the
+    // packed weight
 #pragma unroll
-    for (int j = 0; j < (L::kAUnits / 64 + kCvWaves - 1) / kCvWaves; ++j) {
-      const int u = wave + kCvWaves * j;
-      if ((L::kAUnits / 64) % kCvWaves == 0 || u < L::kAUnits / 64)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            pres, (__attribute__((address_space(3))) void*)(dstb + L::kAOff + 256 * u), 16,
-            (uint32_t)(u * 64 + lane) * 16u, 0, 0, 0);
+    for (int c = 0; c < CH; ++c) {
+      const uint32_t* src = pk + ((((int64_t)mg * g.nc32 + ccb + c) * 9 + ki * 3) * MB * P * 64) * 4;
+      const BufRes pres = make_buf(src, (uint32_t)(L::kAUnits1 * 16));
+#pragma unroll
+      for (int j = 0; j < (L::kAUnits1 / 64 + kCvWaves - 1) / kCvWaves; ++j) {
+        const int u = wave + kCvWaves * j;
+        if ((L::kAUnits1 / 64) % kCvWaves == 0 || u < L::kAUnits1 / 64)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              pres,
+              (__attribute__((address_space(3))) void*)(dstb + L::kAOff + 4 * c * L::kAUnits1 + 256 * u),
+              16, (uint32_t)(u * 64 + lane) * 16u, 0, 0, 0);
+      }
     }
   };
 
@@ -249,60 +258,63 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
   // staged element of this lane's block-0 pixel at tap column 0: segment row
   // wseg, column pad + pcol0 + col16
   const int el0 = wseg * g.seg + kCvPad + pcol0 + col16;
-  if (nstage > 0) stage(s0, 0);
+  if (nstage > 0) stage(0, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int s = 0; s < nstage; ++s) {
     const int buf = s & 1;
-    if (s + 1 < nstage) stage(s0 + s + 1, buf ^ 1);
+    if (s + 1 < nstage) stage(s + 1, buf ^ 1);
     const uint32_t* __restrict__ bb = csm + buf * L::kBuf;
-    // this lane's input elements: plane 4e + quad, element el0 + 16 blk + dw
-    const uint32_t* __restrict__ xq = bb + quad * L::kXS;
 #pragma unroll
-    for (int kj = 0; kj < 3; ++kj) {
-      const int dw = kj - 1;
-      V afr[MB][P];
+    for (int c = 0; c < CH; ++c) {
+      // this lane's input elements: plane 32c + 4e + quad, element el0 + 16 blk + dw
+      const uint32_t* __restrict__ xq = bb + (32 * c + quad) * L::kXS;
 #pragma unroll
-      for (int ib = 0; ib < MB; ++ib)
+      for (int kj = 0; kj < 3; ++kj) {
+        const int dw = kj - 1;
+        V afr[MB][P];
 #pragma unroll
-        for (int pp = 0; pp < P; ++pp)
-          afr[ib][pp] = __builtin_bit_cast(
-              V, *reinterpret_cast<const u32x4*>(bb + L::kAOff +
-                                                 4 * ((((kj * MB) + ib) * P + pp) * 64 + lane)));
+        for (int ib = 0; ib < MB; ++ib)
 #pragma unroll
-      for (int blk = 0; blk < 2; ++blk) {
-        const int col = el0 + 16 * blk + dw;
-        V bfr[P];
-        if constexpr (PAIR) {
-          // pair planes: dword jj of the hi / lo fragment is staged plane
-          // quad + 4jj / 16 + quad + 4jj (the pair 8jj + 2quad, +1), already split
-          u32x4 h4, l4;
+          for (int pp = 0; pp < P; ++pp)
+            afr[ib][pp] = __builtin_bit_cast(
+                V, *reinterpret_cast<const u32x4*>(
+                       bb + L::kAOff + 4 * (c * L::kAUnits1 + (((kj * MB) + ib) * P + pp) * 64 + lane)));
 #pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            h4[jj] = xq[4 * jj * L::kXS + col];
-            l4[jj] = xq[(16 + 4 * jj) * L::kXS + col];
+        for (int blk = 0; blk < 2; ++blk) {
+          const int col = el0 + 16 * blk + dw;
+          V bfr[P];
+          if constexpr (PAIR) {
+            // pair planes: dword jj of the hi / lo fragment is staged plane
+            // quad + 4jj / 16 + quad + 4jj (the pair 8jj + 2quad, +1), already split
+            u32x4 h4, l4;
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+              h4[jj] = xq[4 * jj * L::kXS + col];
+              l4[jj] = xq[(16 + 4 * jj) * L::kXS + col];
+            }
+            bfr[0] = __builtin_bit_cast(V, h4);
+            bfr[1] = __builtin_bit_cast(V, l4);
+          } else if constexpr (sizeof(T) == 4) {
+            float bv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bv[e] = __uint_as_float(xq[4 * e * L::kXS + col]);
+            M::pack(bv, bfr);
+          } else {
+            // the 8 two-byte values as loaded, paired into dwords (no fp32 round trip)
+            const uint16_t* __restrict__ xb = reinterpret_cast<const uint16_t*>(xq);
+            u32x4 wv;
+#pragma unroll
+            for (int e2 = 0; e2 < 4; ++e2) {
+              const uint32_t lo = xb[2 * (8 * e2) * L::kXS + col];
+              const uint32_t hi = xb[2 * (8 * e2 + 4) * L::kXS + col];
+              wv[e2] = lo | (hi << 16);
+            }
+            bfr[0] = __builtin_bit_cast(V, wv);
           }
-          bfr[0] = __builtin_bit_cast(V, h4);
-          bfr[1] = __builtin_bit_cast(V, l4);
-        } else if constexpr (sizeof(T) == 4) {
-          float bv[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) bv[e] = __uint_as_float(xq[4 * e * L::kXS + col]);
-          M::pack(bv, bfr);
-        } else {
-          // the 8 two-byte values as loaded, paired into dwords (no fp32 round trip)
-          const uint16_t* __restrict__ xb = reinterpret_cast<const uint16_t*>(xq);
-          u32x4 wv;
-#pragma unroll
-          for (int e2 = 0; e2 < 4; ++e2) {
-            const uint32_t lo = xb[2 * (8 * e2) * L::kXS + col];
-            const uint32_t hi = xb[2 * (8 * e2 + 4) * L::kXS + col];
-            wv[e2] = lo | (hi << 16);
-          }
-          bfr[0] = __builtin_bit_cast(V, wv);
+          for (int ib = 0; ib < MB; ++ib) acc[blk][ib] = M::mac(afr[ib], bfr, acc[blk][ib]);
         }
-#pragma unroll
-        for (int ib = 0; ib < MB; ++ib) acc[blk][ib] = M::mac(afr[ib], bfr, acc[blk][ib]);
       }
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -503,7 +515,18 @@ int cv_run(const void* in, const void* wt, const void* bias, void* out, void* wo
     auto pick = [&](auto b, auto pr) {
       constexpr bool B = decltype(b)::value;
       constexpr bool PR = decltype(pr)::value && sizeof(T) == 4;
-      // one-row segments (wide images) with the narrower staging pitch
+      // one-row segments (wide images) with the narrower staging pitch; 2-byte
+      // types take two chunks per stage where every K split's chunk count is
+      // even and the grid has one workgroup per CU at most (the 122 KB of LDS
+      // leave no room for a second: with more workgroups, as the input
+      // gradient's 1024 at 256x256, measured 37 -> 50 us; forward 41.1 ->
+      // 40.2 us)
+      if constexpr (sizeof(T) == 2) {
+        if (g.mb == 4 && g.rs == 1 && g.cc_per % 2 == 0 && g.nc32 % g.cc_per == 0 &&
+            (int64_t)grid.x <= kCvFillWGs)
+          return launch(conv3x3_kernel<T, B, 4, true, false, 2>,
+                        (size_t)2 * CvLds<T, 4, true, 2>::kBuf * 4);
+      }
       if (g.mb == 4 && g.rs == 1)
         return launch(conv3x3_kernel<T, B, 4, true, PR>, (size_t)2 * CvLds<T, 4, true>::kBuf * 4);
       if (g.mb == 4)
