@@ -70,7 +70,8 @@ def parse_args():
         help="comma-separated C-ABI entry points (or 'copy') to run alone at the headline "
         "shape, for rocprofv3 counter runs; no timing line is printed",
     )
-    p.add_argument("--dtype", choices=("f32", "bf16"), default="f32", help="with --kernel")
+    p.add_argument("--dtype", choices=("f32", "bf16"), default="f32",
+                   help="with --kernel and --first-steps")
     p.add_argument("--reps", type=int, default=3, help="launches per entry point with --kernel")
     p.add_argument("--kernel-size", type=int, default=K, help="with --kernel: K (filter entry points "
                    "take any odd K; the fused ones 1 or 3)")
@@ -84,7 +85,7 @@ def parse_args():
                    "line")
     p.add_argument("--channels", type=int, default=C, help="with --peak-mem: C")
     p.add_argument("--first-steps", type=int, default=0, metavar="N",
-                   help="probe mode: N fp32 training steps of a fresh process, each synchronized "
+                   help="probe mode: N training steps (--dtype) of a fresh process, each synchronized "
                    "and bracketed by HIP events, no warm-up (the clock ramp); prints one JSON line")
     p.add_argument("--settle-ms", type=float, default=0.0,
                    help="with --first-steps: clock settle before the steps (0 = none)")
@@ -687,14 +688,15 @@ def kernel_mode(args):
         print(f"ran {name} x{args.reps} ({args.dtype}, K={k}, {hw}x{hw}, {len(sets)} input sets)", flush=True)
 
 
-def first_steps_mode(nsteps, settle_ms):
+def first_steps_mode(nsteps, settle_ms, dtype_name="f32"):
     """Probe of a fresh process's first training steps: one untimed step (code
     objects, allocator), an optional clock settle, then `nsteps` steps, each
     synchronized and timed with HIP events."""
     import torch
 
-    module = make_module(torch.float32)
-    x, y = make_inputs(torch.float32)
+    dtype = {"f32": torch.float32, "bf16": torch.bfloat16}[dtype_name]
+    module = make_module(dtype)
+    x, y = make_inputs(dtype)
     train_step(module, x, y)
     torch.cuda.synchronize()
     settled = settle_gpu_clocks(settle_ms) if settle_ms > 0 else 0.0
@@ -752,7 +754,7 @@ def main():
         kernel_mode(args)
         return
     if args.first_steps:
-        first_steps_mode(args.first_steps, args.settle_ms)
+        first_steps_mode(args.first_steps, args.settle_ms, args.dtype)
         return
     extra = {}
     if not args.quick:
