@@ -135,7 +135,11 @@ struct CvLds {
 // sums part[ksplit][n][M][H*W] (no bias) that conv3x3_reduce_kernel adds up.
 // CH: 32-plane chunks per stage (2 for 2-byte types when a K split's chunk
 // count is even: twice the MFMA work per stage and per barrier).
-template <typename T, bool BIAS, int MB, bool WIDE, bool PAIR = false, int CH = 1>
+// AL: aligned layout -- one-row segments of 256 columns on an image whose
+// width is a multiple of 256, 16-byte input rows, whole 32-plane chunks: the
+// copies take their offsets from per-lane parts formed once and scalar parts
+// formed per stage, without per-copy tests.
+template <typename T, bool BIAS, int MB, bool WIDE, bool PAIR = false, int CH = 1, bool AL = false>
 __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict__ in,
                                                              const uint32_t* __restrict__ pk,
                                                              const T* __restrict__ bias,
@@ -191,12 +195,46 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
     cpos[part] = 4 * pc;                                     // dword offset in the plane
   }
   const int nparts = (cpp + 63) / 64;
+  // aligned layout: the lane's column byte offset per copy part (kOob for the
+  // halo chunks left of column 0 and right of the last column)
+  uint32_t alcol[kParts];
+  if constexpr (AL) {
+#pragma unroll
+    for (int part = 0; part < kParts; ++part) {
+      const int gw = w0 + ccol[part];
+      alcol[part] = (unsigned)gw < (unsigned)W ? (uint32_t)gw * (uint32_t)E : kOob;
+    }
+  }
+  const BufRes xnul = make_buf(in, 0u);
   // ---- stage s = (chunk group) * 3 + ki -> LDS buffer `buf`
   auto stage = [&](int s, int buf) {
     const int ki = s % 3;
     const int ccb = cc0 + (s / 3) * CH;  // first chunk of the group
     uint32_t* __restrict__ dstb = csm + buf * L::kBuf;
-    if (g.x4) {
+    if constexpr (AL) {
+      // one image row per stage (a row outside the image copies through a
+      // resource with no records); plane offset and row offset are scalar
+      const int hh = h0 + ki - 1;
+      const bool rok = (unsigned)hh < (unsigned)H;
+      const BufRes rs = rok ? xres : xnul;
+      const uint32_t roff = rok ? (uint32_t)(hh * W) * (uint32_t)E : 0u;
+      // 16-byte chunks of a staged row: 68 (fp32, two overlapping copies) or
+      // 34 (2-byte types, one copy of 34 lanes)
+      constexpr int kCpp = (kCvPix + 2 * kCvPad) * E / 16;
+      constexpr int kNp = (kCpp + 63) / 64;
+      if (kCpp >= 64 || lane < kCpp) {
+#pragma unroll
+        for (int j = 0; j < 32 * CH / kCvWaves; ++j) {
+          const int cr = wave + kCvWaves * j;
+          const uint32_t so = (uint32_t)(ccb * 32 + cr) * (uint32_t)HW * (uint32_t)E + roff;
+#pragma unroll
+          for (int part = 0; part < kNp; ++part)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void*)(dstb + cr * L::kXS + cpos[part]), 16,
+                alcol[part], so, 0, 0);
+        }
+      }
+    } else if (g.x4) {
       // one resource for the image; a chunk outside the image (column, row or
       // plane) reads zero through its offset (W % 8 == 0: chunks are whole)
 #pragma unroll
@@ -521,14 +559,26 @@ int cv_run(const void* in, const void* wt, const void* bias, void* out, void* wo
       // leave no room for a second: with more workgroups, as the input
       // gradient's 1024 at 256x256, measured 37 -> 50 us; forward 41.1 ->
       // 40.2 us)
+      // aligned layout: 256-column segments on whole image rows, 16-byte rows,
+      // whole 32-plane chunks in every K split
+      const bool al = g.rs == 1 && g.sw == kCvPix && w % kCvPix == 0 && g.x4 && k % 32 == 0 &&
+                      g.nc32 % g.cc_per == 0;
       if constexpr (sizeof(T) == 2) {
         if (g.mb == 4 && g.rs == 1 && g.cc_per % 2 == 0 && g.nc32 % g.cc_per == 0 &&
-            (int64_t)grid.x <= kCvFillWGs)
+            (int64_t)grid.x <= kCvFillWGs) {
+          if (al)
+            return launch(conv3x3_kernel<T, B, 4, true, false, 2, true>,
+                          (size_t)2 * CvLds<T, 4, true, 2>::kBuf * 4);
           return launch(conv3x3_kernel<T, B, 4, true, false, 2>,
                         (size_t)2 * CvLds<T, 4, true, 2>::kBuf * 4);
+        }
       }
-      if (g.mb == 4 && g.rs == 1)
+      if (g.mb == 4 && g.rs == 1) {
+        if (al)
+          return launch(conv3x3_kernel<T, B, 4, true, PR, 1, true>,
+                        (size_t)2 * CvLds<T, 4, true>::kBuf * 4);
         return launch(conv3x3_kernel<T, B, 4, true, PR>, (size_t)2 * CvLds<T, 4, true>::kBuf * 4);
+      }
       if (g.mb == 4)
         return launch(conv3x3_kernel<T, B, 4, false, PR>, (size_t)2 * CvLds<T, 4, false>::kBuf * 4);
       if (g.mb == 2)

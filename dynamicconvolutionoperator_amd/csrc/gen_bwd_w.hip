@@ -170,7 +170,7 @@ __global__ __launch_bounds__(256) void gen_ysplit_kernel(const float* __restrict
 // SJ: 128-column subsegments per step (2 for 2-byte types on wide images:
 // twice the work per step and per barrier; each wave takes its 32-token
 // segment in both).
-template <typename T, int KS, int MB, int SJ>
+template <typename T, int KS, int MB, int SJ, bool AL>
 __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_partial_kernel(
     const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ gout,
     float* __restrict__ pw, float* __restrict__ pb, T* __restrict__ dw_out, T* __restrict__ db_out,
@@ -277,11 +277,62 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
     }
   }
 
+  // Buffer resources of one image's x, y and gradient planes, formed again
+  // only when a step enters another image
+  BufRes rx = make_buf(x, 0u), ry = make_buf(y, 0u), rg = make_buf(gbase, 0u);
+  int rn = -1;
+  auto image = [&](int n) {
+    if (n != rn) {
+      rn = n;
+      rx = make_buf(x + (int64_t)n * CHW, (uint32_t)(CHW * E));
+      ry = make_buf(y + (int64_t)n * CHW, (uint32_t)(CHW * E));
+      rg = make_buf(gbase + (int64_t)n * 4 * CHW, (uint32_t)(CHW * E));
+    }
+  };
+
   // ---- operands of step `p` -> LDS buffer `buf`
   auto stage = [&](const WgPos& p, int buf) {
     uint32_t* __restrict__ dstb = wsm + buf * L::kBuf;
     const uint32_t rowel = (uint32_t)(p.h * W);
-    if (g.x16) {
+    if constexpr (AL) {
+      // x rows, aligned layout: the offsets and resources of the step's KS
+      // kernel rows are formed once (a row outside the image copies through
+      // a resource with no records), each wave copies channel rows c = wave,
+      // wave + NW, .. for every kernel row, under one lane mask
+      const BufRes xnul = make_buf(x, 0u);
+      uint32_t roff[KS];
+      BufRes rres[KS];
+#pragma unroll
+      for (int rr = 0; rr < KS; ++rr) {
+        const int hh = p.h + (rr - r) * d;
+        const bool ok = (unsigned)hh < (unsigned)H;
+        roff[rr] = ok ? (uint32_t)(hh * W) * E : 0u;
+        rres[rr] = ok ? rx : xnul;
+      }
+      const uint32_t colb = (uint32_t)(p.w0 - kWgPad + 4 * L::kPerD * lane) * E;
+      const bool left = p.w0 == 0 && lane < kWgPad / (4 * L::kPerD);  // the halo left of column 0
+      const bool right = p.w0 + TW == W && 4 * L::kPerD * lane >= TW + kWgPad;
+      const uint32_t colv = left || right ? kOob : colb;
+      if (lane < L::kXD / 4) {
+#pragma unroll
+        for (int jc = 0; jc < (16 + NW - 1) / NW; ++jc) {
+          const int c = wave + NW * jc;
+          if (16 % NW != 0 && c >= 16) break;
+          const int ch = cb * 16 + c;  // < C: the aligned layout has whole channel blocks
+          const uint32_t cho = (uint32_t)ch * (uint32_t)HW * E;
+#pragma unroll
+          for (int rr = 0; rr < KS; ++rr) {
+            const BufRes rs = rres[rr];
+            // (the scalar offset goes through a named variable: written as an
+            // expression in the call, the host pass drops the kernel's stub)
+            const uint32_t so = cho + roff[rr];
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void*)(dstb + (rr * 16 + c) * L::kXSD), 16,
+                colv, so, 0, 0);
+          }
+        }
+      }
+    } else if (g.x16) {
       // x rows: one copy per row, lane l < kXD/4 moving the row's 16-byte
       // chunk l (three times fewer copy instructions, and their scalar set-up,
       // than dword copies: fp32 85.6 -> 82.1 us at 256x256); a row outside the
@@ -354,9 +405,9 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
     }
     // y rows (P parts x MB*16 channels) and branch-gradient rows (16
     // channels) in the swizzled chunk layout; channels >= C read zero
-    const BufRes yres = make_buf(y + (int64_t)p.n * CHW, (uint32_t)(CHW * E));
-    const BufRes gres = make_buf(gbase + (int64_t)p.n * 4 * CHW, (uint32_t)(CHW * E));
-    if (g.x4) {
+    const BufRes yres = AL ? ry : make_buf(y + (int64_t)p.n * CHW, (uint32_t)(CHW * E));
+    const BufRes gres = AL ? rg : make_buf(gbase + (int64_t)p.n * 4 * CHW, (uint32_t)(CHW * E));
+    if (AL || g.x4) {
       // 1 KB copies: lane l moves one 16-byte chunk; the step's byte offset
       // is the scalar offset, and lanes past the image's right edge are
       // masked only in a partial column block
@@ -379,7 +430,7 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
           }
         }
       };
-      if (p.w0 + TW <= W)
+      if (AL || p.w0 + TW <= W)
         copies(std::false_type{});
       else
         copies(std::true_type{});
@@ -422,8 +473,25 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
   constexpr int YU = kYReg ? MB * 16 * (TW / 4) : 1;  // 4-column pieces per step
   constexpr int YUT = (YU + NT - 1) / NT;
   f32x4 yreg[YUT];
+  // aligned layout: the lane's byte offset of piece j within a step's rows
+  uint32_t ylo[AL ? YUT : 1];
+  if constexpr (AL && kYReg) {
+#pragma unroll
+    for (int j = 0; j < YUT; ++j) {
+      const int u = tid + NT * j;
+      ylo[j] = ((uint32_t)(i0 + (u >> 5)) * (uint32_t)HW + 4u * (uint32_t)(u & 31)) * 4u;
+    }
+  }
   auto yload = [&](const WgPos& p) {
-    if constexpr (kYReg) {
+    if constexpr (AL && kYReg) {
+      const uint32_t ys = ((uint32_t)(p.h * W) + (uint32_t)p.w0) * 4u;
+#pragma unroll
+      for (int j = 0; j < YUT; ++j) {
+        const int u = tid + NT * j;
+        if (YU % NT != 0 && u >= YU) break;  // wave-uniform
+        yreg[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ry, ylo[j], ys, 0));
+      }
+    } else if constexpr (kYReg) {
       const BufRes yres = make_buf(y + (int64_t)p.n * CHW, (uint32_t)(CHW * E));
       const uint32_t rowel = (uint32_t)(p.h * W);
 #pragma unroll
@@ -433,9 +501,10 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
         const int i = u >> 5, w = p.w0 + 4 * (u & 31);
         const bool okc = i0 + i < C;
         const uint32_t base = ((uint32_t)(i0 + i) * (uint32_t)HW + rowel + (uint32_t)w) * 4u;
-        if (g.y4) {
+        if (AL || g.y4) {
           yreg[j] = __builtin_bit_cast(
-              f32x4, __builtin_amdgcn_raw_buffer_load_b128(yres, okc && w < W ? base : kOob, 0, 0));
+              f32x4,
+              __builtin_amdgcn_raw_buffer_load_b128(yres, okc && (AL || w < W) ? base : kOob, 0, 0));
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
@@ -489,6 +558,7 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
     nxt.h = row - nxt.n * H;
   }
   if (steps > 0) {
+    image(nxt.n);
     yload(nxt);
     stage(nxt, 0);
     nxt.advance(g);
@@ -509,6 +579,7 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
     const int buf = s & 1;
     const bool more = s + 1 < steps;
     if (more) {
+      image(nxt.n);
       yload(nxt);
       stage(nxt, buf ^ 1);
       nxt.advance(g);
@@ -889,10 +960,11 @@ int bw_run(const void* x, const void* y, const void* grad_out, void* grad_weight
   float* pb = g.direct ? nullptr : pw + (int64_t)g.splits * 3 * kk * c * c;
   return wg_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
-    auto launch = [&](auto ks, auto mbc, auto sjc) {
+    auto launch = [&](auto ks, auto mbc, auto sjc, auto alc) {
       constexpr int KS = decltype(ks)::value;
       constexpr int MB = decltype(mbc)::value;
       constexpr int SJ = decltype(sjc)::value;
+      constexpr bool AL = decltype(alc)::value;
       constexpr int KKc = KS * KS;
       typedef WgLds<T, KS, MB, SJ> L;
       const size_t stage = (size_t)2 * L::kBuf * 4;
@@ -900,9 +972,9 @@ int bw_run(const void* x, const void* y, const void* grad_out, void* grad_weight
       const size_t lds = stage > red ? stage : red;
       const dim3 grid((unsigned)(g.dw_blocks + helpers));
       const int ae = allow_dynamic_lds(
-          reinterpret_cast<const void*>(&gen_bwd_w_partial_kernel<T, KS, MB, SJ>), lds);
+          reinterpret_cast<const void*>(&gen_bwd_w_partial_kernel<T, KS, MB, SJ, AL>), lds);
       if (ae != 0) return ae;
-      hipLaunchKernelGGL((gen_bwd_w_partial_kernel<T, KS, MB, SJ>), grid,
+      hipLaunchKernelGGL((gen_bwd_w_partial_kernel<T, KS, MB, SJ, AL>), grid,
                          dim3(64 * kWgSegs * WgTaps<KS>::kGroups), lds, stream, (const T*)x,
                          (const T*)y, (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g,
                          helpers > 0 && fin ? *fin : none, helpers > 0 && yp ? *yp : nopack);
@@ -928,9 +1000,18 @@ int bw_run(const void* x, const void* y, const void* grad_out, void* grad_weight
       return (int)hipGetLastError();
     };
     return wg_with_mb(mb, [&](auto mbc) {
+      // aligned layout (16-byte x, y and gradient rows, whole steps, whole
+      // 16-channel blocks): the copies take their fast forms without runtime
+      // tests
+      const bool al = g.x16 && g.x4 && (esz == 2 || g.y4) && w % g.tw == 0 && c % 16 == 0 &&
+                      (c <= 64 || c == 128);
       auto by_k = [&](auto sjc) {
-        if (kernel_size == 1) return launch(std::integral_constant<int, 1>(), mbc, sjc);
-        return launch(std::integral_constant<int, 3>(), mbc, sjc);
+        auto by_al = [&](auto ks) {
+          if (al) return launch(ks, mbc, sjc, std::true_type{});
+          return launch(ks, mbc, sjc, std::false_type{});
+        };
+        if (kernel_size == 1) return by_al(std::integral_constant<int, 1>());
+        return by_al(std::integral_constant<int, 3>());
       };
       if constexpr (sizeof(T) == 2) {
         if (g.tw == 2 * kWgTW) return by_k(std::integral_constant<int, 2>());
