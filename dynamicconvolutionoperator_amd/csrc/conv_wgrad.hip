@@ -119,7 +119,10 @@ struct CwPos {
 // their lo plane.  SJ: 128-column subsegments per step (2 for 2-byte types on
 // wide images: twice the work per step and per barrier; each wave takes its
 // 32-token segment in both).
-template <typename T, int MB, bool PP = false, int SJ = 1>
+// AL: aligned layout (16-byte cat and grad_out rows, whole steps, whole
+// 16-plane blocks of ci and co): copy offsets from per-lane parts formed once
+// and scalar parts formed per step, without per-copy tests.
+template <typename T, int MB, bool PP = false, int SJ = 1, bool AL = false>
 __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
     const T* __restrict__ cat, const T* __restrict__ gout, float* __restrict__ pw,
     float* __restrict__ pb, T* __restrict__ dw_out, T* __restrict__ db_out, CwGeom g) {
@@ -179,11 +182,61 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
     }
   }
 
+  // Buffer resources of one image's cat and grad_out planes, formed again only
+  // when a step enters another image (aligned layout)
+  BufRes rx = make_buf(cat, 0u), ry = make_buf(gout, 0u);
+  int rn = -1;
+  auto image = [&](int n) {
+    if (AL && n != rn) {
+      rn = n;
+      rx = make_buf(cat + (int64_t)n * CI * HW, (uint32_t)(CI * HW * E));
+      ry = make_buf(gout + (int64_t)n * C * HW, (uint32_t)(C * HW * E));
+    }
+  };
+
   // ---- operands of step `p` -> LDS buffer `buf`
   auto stage = [&](const CwPos& p, int buf) {
     uint32_t* __restrict__ dstb = csm + buf * L::kBuf;
-    const BufRes xres = make_buf(cat + (int64_t)p.n * CI * HW, (uint32_t)(CI * HW * E));
-    if (g.x16) {
+    const BufRes xres = AL ? rx : make_buf(cat + (int64_t)p.n * CI * HW, (uint32_t)(CI * HW * E));
+    if constexpr (AL) {
+      // cat rows: offsets and resources of the step's 3 image rows formed
+      // once (a row outside the image copies through a resource with no
+      // records); each wave copies the planes c = wave, wave + 12, .. for all
+      // three rows under one lane mask
+      const BufRes xnul = make_buf(cat, 0u);
+      uint32_t roff[3];
+      BufRes rres[3];
+#pragma unroll
+      for (int rr = 0; rr < 3; ++rr) {
+        const int hh = p.h + rr - 1;
+        const bool ok = (unsigned)hh < (unsigned)H;
+        roff[rr] = ok ? (uint32_t)(hh * W) * E : 0u;
+        rres[rr] = ok ? xres : xnul;
+      }
+      const uint32_t colb = (uint32_t)(p.w0 - kCwPad + 4 * L::kPerD * lane) * E;
+      const bool left = p.w0 == 0 && lane < kCwPad / (4 * L::kPerD);  // the halo left of column 0
+      const bool right = p.w0 + TW == W && 4 * L::kPerD * lane >= TW + kCwPad;
+      const uint32_t colv = left || right ? kOob : colb;
+      if (lane < L::kXD / 4) {
+#pragma unroll
+        for (int jc = 0; jc < (16 + kCwNW - 1) / kCwNW; ++jc) {
+          const int c = wave + kCwNW * jc;
+          if (16 % kCwNW != 0 && c >= 16) break;
+          const int ch = PP ? cw_pair_plane(cb, c) : cb * 16 + c;  // < CI: whole blocks
+          const uint32_t cho = (uint32_t)ch * (uint32_t)HW * E;
+#pragma unroll
+          for (int rr = 0; rr < 3; ++rr) {
+            const BufRes rs = rres[rr];
+            // (the scalar offset goes through a named variable: written as an
+            // expression in the call, the host pass drops the kernel's stub)
+            const uint32_t so = cho + roff[rr];
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void*)(dstb + (rr * 16 + c) * L::kXSD), 16,
+                colv, so, 0, 0);
+          }
+        }
+      }
+    } else if (g.x16) {
       // cat rows: one copy per row, lane l < kXD/4 moving the row's 16-byte chunk l
       const BufRes xnul = make_buf(cat, 0u);
       const int gw = p.w0 - kCwPad + 4 * L::kPerD * lane;
@@ -217,11 +270,11 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
       }
     }
     // gO rows (P parts x MB*16 planes) in the swizzled chunk layout; planes >= C read zero
-    const BufRes yres = make_buf(gout + (int64_t)p.n * C * HW, (uint32_t)(C * HW * E));
+    const BufRes yres = AL ? ry : make_buf(gout + (int64_t)p.n * C * HW, (uint32_t)(C * HW * E));
     const uint32_t rowel = (uint32_t)(p.h * W);
-    if (g.g16) {
+    if (AL || g.g16) {
       const uint32_t ystep = (rowel + (uint32_t)p.w0) * 2u;
-      const bool full = p.w0 + TW <= W;
+      const bool full = AL || p.w0 + TW <= W;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int ii = wave + kCwNW * j;
@@ -258,8 +311,25 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
   constexpr int YU = kYReg ? MB * 16 * (TW / 4) : 1;
   constexpr int YUT = (YU + kCwThreads - 1) / kCwThreads;
   f32x4 yreg[YUT];
+  // aligned layout: the lane's byte offset of piece j within a step's rows
+  uint32_t ylo[AL ? YUT : 1];
+  if constexpr (AL && kYReg) {
+#pragma unroll
+    for (int j = 0; j < YUT; ++j) {
+      const int u = tid + kCwThreads * j;
+      ylo[j] = ((uint32_t)(co0 + (u >> 5)) * (uint32_t)HW + 4u * (uint32_t)(u & 31)) * 4u;
+    }
+  }
   auto yload = [&](const CwPos& p) {
-    if constexpr (kYReg) {
+    if constexpr (AL && kYReg) {
+      const uint32_t ys = ((uint32_t)(p.h * W) + (uint32_t)p.w0) * 4u;
+#pragma unroll
+      for (int j = 0; j < YUT; ++j) {
+        const int u = tid + kCwThreads * j;
+        if (YU % kCwThreads != 0 && u >= YU) break;  // wave-uniform
+        yreg[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ry, ylo[j], ys, 0));
+      }
+    } else if constexpr (kYReg) {
       const BufRes yres = make_buf(gout + (int64_t)p.n * C * HW, (uint32_t)(C * HW * E));
       const uint32_t rowel = (uint32_t)(p.h * W);
 #pragma unroll
@@ -318,6 +388,7 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
     nxt.h = row - nxt.n * H;
   }
   if (steps > 0) {
+    image(nxt.n);
     yload(nxt);
     stage(nxt, 0);
     nxt.advance(g);
@@ -339,6 +410,7 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
     const int buf = s & 1;
     const bool more = s + 1 < steps;
     if (more) {
+      image(nxt.n);
       yload(nxt);
       stage(nxt, buf ^ 1);
       nxt.advance(g);
@@ -632,8 +704,14 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
       const size_t stage = (size_t)2 * L::kBuf * 4;
       const size_t red = (size_t)(kCwSegs * 9 * 16 * (MB * 16 + 1) + kCwSegs * 16) * sizeof(float);
       const size_t lds = stage > red ? stage : red;
-      auto kern = pp ? conv_wgrad_partial_kernel<T, MB, sizeof(T) == 4 && SJ == 1, SJ>
-                     : conv_wgrad_partial_kernel<T, MB, false, SJ>;
+      // aligned layout: 16-byte rows, whole steps, whole 16-plane blocks of
+      // ci (4C) and of co (one workgroup's MB blocks, or two halves of 64)
+      const bool al = g.x16 && (esz == 4 ? g.y4 : g.g16) && w % g.tw == 0 && c % 4 == 0 &&
+                      (c <= 64 ? c % 16 == 0 : c == 128);
+      auto kern = pp ? (al ? conv_wgrad_partial_kernel<T, MB, sizeof(T) == 4 && SJ == 1, SJ, true>
+                           : conv_wgrad_partial_kernel<T, MB, sizeof(T) == 4 && SJ == 1, SJ>)
+                     : (al ? conv_wgrad_partial_kernel<T, MB, false, SJ, true>
+                           : conv_wgrad_partial_kernel<T, MB, false, SJ>);
       const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
       if (ae != 0) return ae;
       hipLaunchKernelGGL(kern, dim3((unsigned)(g.splits * g.cblocks * g.ohalves)), dim3(kCwThreads), lds, stream,

@@ -80,7 +80,11 @@ struct YtLds {
 // CH: 32-channel chunks per stage (2 for 2-byte types when the chunk count
 // is even: twice the MFMA work per stage and per barrier, LDS 122 KB at
 // C = 64).
-template <typename T, int KS, int MB, int CH>
+// AL: aligned layout (16-byte x rows, whole 32-channel chunks): the x copies
+// take the lane's column offset formed once per workgroup (kOob for the halo
+// chunks outside the image) and a scalar row offset per stage, without
+// per-copy tests.
+template <typename T, int KS, int MB, int CH, bool AL = false>
 __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restrict__ x,
                                                                const uint32_t* __restrict__ pk,
                                                                const T* __restrict__ gout,
@@ -112,6 +116,17 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
   // x planes of image n (per-row resources cost ~20 scalar instructions per
   // row and stage; measured bf16 44.9 -> 41.6 us)
   const BufRes xres = make_buf(x + (int64_t)n * C * HW, (uint32_t)(C * HW * (int64_t)E));
+  const BufRes xnul = make_buf(x, 0u);
+  constexpr int kXP = (L::kXChunks + 63) / 64;  // copies per staged row
+  uint32_t alcol[kXP];
+  if constexpr (AL) {
+#pragma unroll
+    for (int part = 0; part < kXP; ++part) {
+      const int pc = 64 * part < L::kXChunks - 64 ? 64 * part : (L::kXChunks > 64 ? L::kXChunks - 64 : 0);
+      const int gw = w0 - kYtPad + (pc + lane) * 4 * L::kPerD;
+      alcol[part] = (unsigned)gw < (unsigned)W ? (uint32_t)gw * (uint32_t)E : kOob;
+    }
+  }
   // ---- stage s = ((b * ncg) + cg) * KS + ki -> LDS buffer `buf`
   auto stage = [&](int s, int buf) {
     const int ki = s % KS;
@@ -121,7 +136,29 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
     const int hh = h + (ki - r) * d;
     uint32_t* __restrict__ dstb = ysm + buf * L::kBuf;
     // x rows: 32 * CH channels of row hh, columns w0 - pad .. w0 + TW + pad
-    if (g.x4) {
+    if constexpr (AL) {
+      // a row outside the image copies through a resource with no records
+      const bool rok = (unsigned)hh < (unsigned)H;
+      const BufRes rs = rok ? xres : xnul;
+      const uint32_t roff = rok ? (uint32_t)(hh * W) * (uint32_t)E : 0u;
+      if (L::kXChunks >= 64 || lane < L::kXChunks) {
+#pragma unroll
+        for (int j = 0; j < 32 * CH / kYtWaves; ++j) {
+          const int cr = wave + kYtWaves * j;
+          // (the offsets go through named variables: written as expressions
+          // in the call, the host pass drops the kernel's stub)
+          const uint32_t so = (uint32_t)(cg * CH * 32 + cr) * (uint32_t)HW * (uint32_t)E + roff;
+#pragma unroll
+          for (int part = 0; part < kXP; ++part) {
+            const int pc = 64 * part < L::kXChunks - 64 ? 64 * part : (L::kXChunks > 64 ? L::kXChunks - 64 : 0);
+            const uint32_t vo = alcol[part];
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void*)(dstb + L::kXOff + cr * L::kXS + 4 * pc),
+                16, vo, so, 0, 0);
+          }
+        }
+      }
+    } else if (g.x4) {
       // one resource for the image; a chunk outside the image (column, row or
       // channel) reads zero through its offset (W % 8 == 0: chunks are whole)
 #pragma unroll
@@ -501,12 +538,13 @@ int yt_launch(const void* x, const void* weight, const void* grad_out, void* gra
           if (e != 0) return e;
         }
         const size_t lds = (size_t)2 * L::kBuf * 4;
-        const int ae =
-            allow_dynamic_lds(reinterpret_cast<const void*>(&gen_bwd_y_kernel<T, KS, MB, CH>), lds);
+        // aligned layout: 16-byte x rows and whole 32-channel chunks
+        auto kern = g.x4 && c % 32 == 0 ? gen_bwd_y_kernel<T, KS, MB, CH, true>
+                                        : gen_bwd_y_kernel<T, KS, MB, CH>;
+        const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
         if (ae != 0) return ae;
-        hipLaunchKernelGGL((gen_bwd_y_kernel<T, KS, MB, CH>), dim3((unsigned)tiles), dim3(kYtThreads), lds,
-                           stream, (const T*)x, (const uint32_t*)workspace, (const T*)grad_out,
-                           (T*)grad_y, g);
+        hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(kYtThreads), lds, stream, (const T*)x,
+                           (const uint32_t*)workspace, (const T*)grad_out, (T*)grad_y, g);
         return (int)hipGetLastError();
       };
       auto by_ch = [&](auto ks) {
