@@ -679,13 +679,21 @@ def kernel_mode(args):
     for name in names:
         if name not in calls:
             raise SystemExit(f"unknown --kernel {name}; choose from {', '.join(calls)}")
+    # a one-element fill before each entry point and after the last: its
+    # dispatch (torch's FillFunctor kernel) separates the entry points in a
+    # kernel trace or counter collection of this run
+    mark = torch.zeros(1, device="cuda")
+    torch.cuda.synchronize()
     for name in names:
+        mark.fill_(1.0)
         for i in range(args.reps):
             rc = calls[name](sets[i % len(sets)])
             if rc:
                 raise SystemExit(f"{name} failed with status {rc}")
         torch.cuda.synchronize()
         print(f"ran {name} x{args.reps} ({args.dtype}, K={k}, {hw}x{hw}, {len(sets)} input sets)", flush=True)
+    mark.fill_(1.0)
+    torch.cuda.synchronize()
 
 
 def first_steps_mode(nsteps, settle_ms, dtype_name="f32"):
