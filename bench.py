@@ -67,8 +67,9 @@ def parse_args():
     p.add_argument("--quick", action="store_true", help="skip the secondary measurements")
     p.add_argument(
         "--kernel",
-        help="comma-separated C-ABI entry points (or 'copy') to run alone at the headline "
-        "shape, for rocprofv3 counter runs; no timing line is printed",
+        help="comma-separated C-ABI entry points (or 'copy', 'fill', 'add': torch's 1 GiB "
+        "streaming kernels) to run alone at the headline shape, for rocprofv3 counter runs; "
+        "no timing line is printed",
     )
     p.add_argument("--dtype", choices=("f32", "bf16"), default="f32",
                    help="with --kernel and --first-steps")
@@ -595,6 +596,7 @@ def make_calls(lib, dt, k, hw, nsets):
     wsyb = max(int(lib.ddpm_gen_bwd_y_workspace_bytes(C, k)), 1)
     wsy = torch.empty(wsyb, dtype=torch.uint8, device="cuda")
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    add_out = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     shp = (B, C, hw, hw, k, *DIL)
@@ -632,6 +634,12 @@ def make_calls(lib, dt, k, hw, nsets):
                                                                              ptr(dcw), ptr(dcb), ptr(ws),
                                                                              wsb, B, C, hw, hw, code, s),
         "copy": lambda t: (dst.copy_(src), 0)[1],
+        # the device's own streaming rates for comparison: a 1 GiB fill (writes
+        # only) and an elementwise add of two 1 GiB fp32 tensors into a third
+        # (two reads, one write), torch's kernels
+        "fill": lambda t: (dst.fill_(1), 0)[1],
+        "add": lambda t: (torch.add(src.view(torch.float32), dst.view(torch.float32),
+                                    out=add_out), 0)[1],
     }
     return calls, sets
 
@@ -666,7 +674,8 @@ def kernel_mode(args):
     the arguments; dilations 1/3/5) on seeded inputs, rotating through `sets`
     input sets, and 'copy' as a plain device copy of COPY_BYTES, so that
     rocprofv3 can read each kernel's duration and HBM counters (FETCH_SIZE /
-    WRITE_SIZE) and the copy calibrates them."""
+    WRITE_SIZE) and the copy calibrates them; 'fill' and 'add' give the
+    device's own streaming rates for comparison."""
     import torch
 
     from dynamicconvolutionoperator_amd import _lib
@@ -679,20 +688,20 @@ def kernel_mode(args):
     for name in names:
         if name not in calls:
             raise SystemExit(f"unknown --kernel {name}; choose from {', '.join(calls)}")
-    # a one-element fill before each entry point and after the last: its
-    # dispatch (torch's FillFunctor kernel) separates the entry points in a
-    # kernel trace or counter collection of this run
-    mark = torch.zeros(1, device="cuda")
+    # a one-element negation before each entry point and after the last: its
+    # dispatch (torch's neg kernel) separates the entry points in a kernel
+    # trace or counter collection of this run
+    mark = torch.ones(1, device="cuda")
     torch.cuda.synchronize()
     for name in names:
-        mark.fill_(1.0)
+        mark.neg_()
         for i in range(args.reps):
             rc = calls[name](sets[i % len(sets)])
             if rc:
                 raise SystemExit(f"{name} failed with status {rc}")
         torch.cuda.synchronize()
         print(f"ran {name} x{args.reps} ({args.dtype}, K={k}, {hw}x{hw}, {len(sets)} input sets)", flush=True)
-    mark.fill_(1.0)
+    mark.neg_()
     torch.cuda.synchronize()
 
 

@@ -460,11 +460,22 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
           for (int e = 0; e < 8; ++e) xv[e] = cw_lds_elem<T>(bb, xel[kj] + kCwTW * j + e);
           M::pack(xv, afr);
         } else {
-          // the 8 two-byte values as staged, paired into dwords (no fp32 round trip)
-          const uint16_t* __restrict__ xb = reinterpret_cast<const uint16_t*>(bb) + xel[kj] + kCwTW * j;
+          // the 8 two-byte values as staged, already the fragment's element
+          // pairs: 4 dword reads where the window starts on a dword (kj = 1),
+          // else 5 realigned by one element (the shift kj - 1 is odd; the row
+          // pitch, the pad and the lane's token offset are even)
+          const uint32_t* __restrict__ xp = bb + ((xel[kj] + kCwTW * j) >> 1);
           u32x4 wv;
+          if (kj != 1) {
+            uint32_t d5[5];
 #pragma unroll
-          for (int e2 = 0; e2 < 4; ++e2) wv[e2] = (uint32_t)xb[2 * e2] | ((uint32_t)xb[2 * e2 + 1] << 16);
+            for (int k = 0; k < 5; ++k) d5[k] = xp[k];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) wv[k] = __builtin_amdgcn_alignbyte(d5[k + 1], d5[k], 2);
+          } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) wv[k] = xp[k];
+          }
           afr[0] = __builtin_bit_cast(V, wv);
         }
 #pragma unroll

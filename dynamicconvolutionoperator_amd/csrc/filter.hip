@@ -456,7 +456,9 @@ __device__ __forceinline__ void realign(const u32x4& c0, const u32x4& c1, int s,
 // outside the image), commit() writes it to a tile buffer phase-split by V.
 // A thread handles at most NB items (row, V-wide column group); the host
 // checks that bound.
-template <typename T, int V, typename TS, int NB>
+// CONTIG: rows stored contiguously (column j at row offset j, one 16-byte
+// LDS write per group) instead of phase-split by V.
+template <typename T, int V, typename TS, int NB, bool CONTIG = false>
 struct BranchStage {
   static_assert(V * sizeof(T) == 16, "16-byte groups");
   u32x4 raw[NB];
@@ -478,12 +480,19 @@ struct BranchStage {
       const bool ok = item < total && (unsigned)gh < (unsigned)g.H && gc >= 0 && gc < g.W;
       raw[k] = __builtin_amdgcn_raw_buffer_load_b128(
           res, ok ? (uint32_t)((int64_t)gh * g.W + gc) * (uint32_t)sizeof(T) : kOob, 0, 0);
-      dst[k] = item < total ? srow * g.RS + sgrp : -1;
+      dst[k] = item < total ? srow * g.RS + (CONTIG ? sgrp * V : sgrp) : -1;
     }
   }
 
   __device__ __forceinline__ void commit(TS* __restrict__ s, const FilterGeom& g) const {
     typedef typename Vec<T, V>::type TV;
+    if constexpr (CONTIG) {
+      static_assert(std::is_same<T, TS>::value, "contiguous rows hold the plane's own type");
+#pragma unroll
+      for (int k = 0; k < NB; ++k)
+        if (dst[k] >= 0) *reinterpret_cast<u32x4*>(s + dst[k]) = raw[k];
+      return;
+    }
 #pragma unroll
     for (int k = 0; k < NB; ++k) {
       if (dst[k] >= 0) {
@@ -512,7 +521,10 @@ constexpr int kDxStageItems = 6;
 // forward), each with only the halo its own dilation reads: branch b+1's
 // loads are in flight while branch b's taps run, and the tile takes a third
 // of the LDS of staging all three at once, so more workgroups share a CU.
-template <typename TX, typename TK, int KS, int V>
+// CONTIG: the branch-gradient tiles hold contiguous rows and a lane reads
+// its tap window as the two aligned 16-byte chunks around it, realigned like
+// the kernel chunks (two LDS reads per V pixels instead of V).
+template <typename TX, typename TK, int KS, int V, bool CONTIG = false>
 __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_vec_kernel(const TK* __restrict__ gout,
                                                                             const TK* __restrict__ kern,
                                                                             TX* __restrict__ gx,
@@ -569,7 +581,7 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_vec_kernel(const 
   };
   auto halo = [&](int b) { return r * dil_of(b, g.d0, g.d1, g.d2); };
 
-  BranchStage<TK, V, TS, kDxStageItems> st;
+  BranchStage<TK, V, TS, kDxStageItems, CONTIG> st;
   u32x4 nxt[KS][2];
   load_row(0, 0, nxt);
   st.issue(gp + gstride, g, h0, w0, halo(0));
@@ -597,15 +609,27 @@ __global__ __launch_bounds__(kFilterThreads) void filter_bwd_x_vec_kernel(const 
     if (it + 1 < 3 * KS) load_row((it + 1) / KS, (it + 1) % KS, nxt);
     const int d = dil_of(b, g.d0, g.d1, g.d2);
     const TS* __restrict__ gb = gs + (b & 1) * lplane;
-    const int rb = (tr + g.R - (ki - r) * d) * g.RS + jc / V;
+    const int rb = (tr + g.R - (ki - r) * d) * g.RS + (CONTIG ? jc : jc / V);
 #pragma unroll
     for (int kj = 0; kj < KS; ++kj) {
       const int dw = (kj - r) * d;
       const int s = ((-dw) % V + V) % V;
       float kv[V];
       realign<TK, V>(cur[kj][0], cur[kj][1], s, kv);
+      if constexpr (CONTIG) {
+        // the window [jc - dw, +V) of the lane's staged row: chunks at
+        // jc - dw - s and V further (the second only for a shift within a chunk)
+        const u32x4* __restrict__ gc = reinterpret_cast<const u32x4*>(gb + rb - dw - s);
+        const u32x4 g0 = gc[0];
+        const u32x4 g1 = s == 0 ? u32x4{0u, 0u, 0u, 0u} : gc[1];
+        float gv[V];
+        realign<TK, V>(g0, g1, s, gv);
 #pragma unroll
-      for (int v = 0; v < V; ++v) acc[v] = fmaf(kv[v], staged<V, TS>(gb, g, rb, v - dw), acc[v]);
+        for (int v = 0; v < V; ++v) acc[v] = fmaf(kv[v], gv[v], acc[v]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc[v] = fmaf(kv[v], staged<V, TS>(gb, g, rb, v - dw), acc[v]);
+      }
     }
     if (ki == KS - 1 && b < 2) {
       // every wave is past branch b-1, whose buffer branch b+1 takes
@@ -726,7 +750,7 @@ int launch_ks(FilterOp op, const void* a, const void* b, void* o, const FilterGe
       if constexpr (KS >= 1 && 16 % sizeof(TK) == 0) {
         constexpr int VK = 16 / (int)sizeof(TK);
         if (vec == VK)
-          return launch_kernel(filter_bwd_x_vec_kernel<TX, TK, KS, VK>, g,
+          return launch_kernel(filter_bwd_x_vec_kernel<TX, TK, KS, VK, true>, g,
                                (size_t)2 * g.LH * g.RS * (sizeof(TK) == 2 ? 2 : 4), stream,
                                (const TK*)a, (const TK*)b, (TX*)o, g);
       }

@@ -625,8 +625,35 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
       // idle during each tap's VALU stretch)
       auto make_afr = [&](int tt, V (&af)[P]) {
         float dk[8];
+        if constexpr (E == 2) {
+          // the lane's 8 consecutive 2-byte x values by dword reads: 4 dwords
+          // when the window starts on a dword, else 5 realigned by one element.
+          // The parity is the tap shift's, (kj - r) * d: the row pitch, the pad
+          // and the lane's token offset are even (wave-uniform branch)
+          const int t = th * TPH + tt;
+          const int kj = t - (t / KS) * KS;
+          const int el = xel[tt] + kWgTW * j;
+          const uint32_t* __restrict__ xp = bb + (el >> 1);
+          uint32_t w[4];
+          if (((kj - r) * d) & 1) {
+            uint32_t d5[5];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dk[e] = gv[e] * lds_elem<T>(bb, xel[tt] + kWgTW * j + e);
+            for (int k = 0; k < 5; ++k) d5[k] = xp[k];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) w[k] = __builtin_amdgcn_alignbyte(d5[k + 1], d5[k], 2);
+          } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) w[k] = xp[k];
+          }
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            dk[2 * k] = gv[2 * k] * to_f(__builtin_bit_cast(T, (unsigned short)(w[k] & 0xffffu)));
+            dk[2 * k + 1] = gv[2 * k + 1] * to_f(__builtin_bit_cast(T, (unsigned short)(w[k] >> 16)));
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dk[e] = gv[e] * lds_elem<T>(bb, xel[tt] + kWgTW * j + e);
+        }
         M::pack(dk, af);
         if constexpr (kVBias)
           dbs[tt] += ((dk[0] + dk[1]) + (dk[2] + dk[3])) + ((dk[4] + dk[5]) + (dk[6] + dk[7]));
