@@ -593,6 +593,9 @@ def make_calls(lib, dt, k, hw, nsets):
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
     wsxb = max(int(lib.ddpm_gen_bwd_x_workspace_bytes(B, C, hw, hw, k, *DIL)), 1)
     wsx = torch.empty(wsxb, dtype=torch.uint8, device="cuda")
+    wskb = max(int(lib.ddpm_gen_kernels_bwd_w_workspace_bytes(B, C, hw, hw, k)),
+               int(lib.ddpm_gen_kernels_bwd_y_workspace_bytes(B, C, hw, hw, k)), 1)
+    wsk = torch.empty(wskb, dtype=torch.uint8, device="cuda")
     wsyb = max(int(lib.ddpm_gen_bwd_y_workspace_bytes(C, k)), 1)
     wsy = torch.empty(wsyb, dtype=torch.uint8, device="cuda")
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
@@ -618,6 +621,13 @@ def make_calls(lib, dt, k, hw, nsets):
         # the generator 1x1 convolution of the materialized route writes the kernel tensor
         "ddpm_gen_kernels": lambda t: lib.ddpm_gen_kernels(ptr(t["y"]), ptr(wt), ptr(bs), ptr(t["kern"]), B, C,
                                                            hw, hw, k, code, s),
+        # its weight / bias and input gradients from a kernel-tensor gradient
+        "ddpm_gen_kernels_bwd_w": lambda t: lib.ddpm_gen_kernels_bwd_w(ptr(t["y"]), ptr(t["kern"]), ptr(dw),
+                                                                       ptr(db), ptr(wsk), wskb, B, C, hw,
+                                                                       hw, k, code, s),
+        "ddpm_gen_kernels_bwd_y": lambda t: lib.ddpm_gen_kernels_bwd_y(ptr(wt), ptr(t["kern"]), ptr(dy),
+                                                                       ptr(wsk), wskb, B, C, hw, hw, k,
+                                                                       code, s),
         "ddpm_filter_fwd": lambda t: lib.ddpm_filter_fwd(ptr(t["x"]), ptr(t["kern"]), ptr(out), *shp, code,
                                                          code, s),
         "ddpm_filter_bwd_x": lambda t: lib.ddpm_filter_bwd_x(ptr(t["go"]), ptr(t["kern"]), ptr(dx), *shp,

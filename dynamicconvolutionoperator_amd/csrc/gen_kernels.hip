@@ -841,16 +841,28 @@ __global__ __launch_bounds__(256) void gk_bwd_y_kernel(const T* __restrict__ gk,
           }
           M::pack(v, bf);
         } else {
-          uint32_t wd[4];
+          // two transposing LDS reads (ds_read_b64_tr_b16): lane 16q + 4a + b
+          // receives element b of the 8-byte reads of lanes 16q + a + 4e,
+          // e = 0..3, so lane 16q + a + 4e reads pixels 4a .. 4a+3 of the
+          // block in row 32kc + 8q + 4h + e, and the fragment's rows 8q + 4h
+          // .. +3 arrive at every pixel lane (h = 0, 1: the two halves)
+          typedef short s16x4 __attribute__((ext_vector_type(4)));
+          const int sa = lane & 3, se = (lane >> 2) & 3;
+          const int spl = 32 * wave + 16 * pb + 4 * sa;
+          const int sc = spl / L::CPX, sw = (spl % L::CPX) * (int)E;
+          u32x4 wd;
 #pragma unroll
-          for (int e2 = 0; e2 < 4; ++e2) {
-            const int r0 = 32 * kc + 8 * quad + 2 * e2;  // rows r0, r0 + 1 share (r >> 3)
-            const int sw = 16 * (c ^ (((r0 >> 3) & 3) * L::SWZ)) + within;
-            const uint32_t lo = *reinterpret_cast<const uint16_t*>(bb + r0 * L::ROWB + sw);
-            const uint32_t hi = *reinterpret_cast<const uint16_t*>(bb + (r0 + 1) * L::ROWB + sw);
-            wd[e2] = lo | (hi << 16);
+          for (int h = 0; h < 2; ++h) {
+            const int row = 32 * kc + 8 * quad + 4 * h + se;
+            const char* a = bb + row * L::ROWB + 16 * (sc ^ (((row >> 3) & 3) * L::SWZ)) + sw;
+            const s16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4*)(a));
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            const u32x2 d2 = __builtin_bit_cast(u32x2, t);
+            wd[2 * h] = d2[0];
+            wd[2 * h + 1] = d2[1];
           }
-          bf[0] = __builtin_bit_cast(V, (u32x4){wd[0], wd[1], wd[2], wd[3]});
+          bf[0] = __builtin_bit_cast(V, wd);
         }
 #pragma unroll
         for (int ib = 0; ib < MB; ++ib) acc[pb][ib] = M::mac(af[ib], bf, acc[pb][ib]);
