@@ -67,12 +67,13 @@ __host__ __device__ constexpr int cv_parts() {
 
 // Packed A: 16-byte units [mg][cc][ki][kj][ib][part][lane] (ib < g.mb), lane
 // (m = (mg*mb + ib)*16 + (lane & 15), q = lane >> 4) holding
-// A[m][cc*32 + 4e + q][ki][kj], e = 0..7.  `rot` selects the input-gradient
-// form (transposed, rotated).
+// A[m][cc*32 + 4e + q][ki][kj], e = 0..7 (`nat`: A[m][cc*32 + 8q + e][ki][kj],
+// the slot order of the transposing B reads).  `rot` selects the
+// input-gradient form (transposed, rotated).
 template <typename T, int MB>
 __global__ __launch_bounds__(256) void conv3x3_pack_kernel(const T* __restrict__ wt,
                                                            uint32_t* __restrict__ pk, ConvGeom g,
-                                                           int rot, int pairs) {
+                                                           int rot, int pairs, int nat) {
   constexpr int P = cv_parts<T>();
   // 32-bit indices: the host bounds the packed units below 2^31
   const int total = g.mgroups * g.nc32 * 9 * MB * 64;
@@ -92,7 +93,7 @@ __global__ __launch_bounds__(256) void conv3x3_pack_kernel(const T* __restrict__
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     // pair planes (kF32Pairs input): slot 8q + e holds channel 2(q + 4(e/2)) + e%2
-    const int k = cc * 32 + (pairs ? 2 * q + 8 * (e >> 1) + (e & 1) : 4 * e + q);
+    const int k = cc * 32 + (pairs ? 2 * q + 8 * (e >> 1) + (e & 1) : nat ? 8 * q + e : 4 * e + q);
     float a = 0.f;
     if (m < g.M && k < g.K) {
       // forward: weight[m][k][ki][kj]; input gradient: weight[k][m][2-ki][2-kj]
@@ -296,6 +297,25 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
   // staged element of this lane's block-0 pixel at tap column 0: segment row
   // wseg, column pad + pcol0 + col16
   const int el0 = wseg * g.seg + kCvPad + pcol0 + col16;
+  // transposing B reads (2-byte aligned layout): lane 16q + 4a + b receives
+  // element b of the 8-byte reads of lanes 16q + a + 4e, e = 0..3, so lane
+  // 16q + a + 4e reads columns 4a .. 4a+3 of a 16-column block in plane
+  // 32c + 8q + 4h + e, and each pixel lane gets its column's planes 8q + 4h
+  // .. +3 (h = 0, 1: the fragment's halves).  Blocks -1 .. 2 around the
+  // wave's 32 pixels: the tap columns -1 and +1 move the pixel blocks one
+  // lane within each row of 16 lanes, the end lane taken from the
+  // neighbouring block (its lane 15 or 0: the reads of those blocks keep to
+  // that one column group, inside the staged row).
+  constexpr bool TR = sizeof(T) == 2 && WIDE && AL && !PAIR;
+  uint32_t trb[4];
+  if constexpr (TR) {
+    const int sa = lane & 3, se = (lane >> 2) & 3;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int a = b == 0 ? 3 : (b == 3 ? 0 : sa);
+      trb[b] = (uint32_t)(((8 * quad + se) * L::kXS) * 4 + (el0 - col16 + 16 * (b - 1) + 4 * a) * E);
+    }
+  }
   if (nstage > 0) stage(0, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -307,6 +327,22 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
     for (int c = 0; c < CH; ++c) {
       // this lane's input elements: plane 32c + 4e + quad, element el0 + 16 blk + dw
       const uint32_t* __restrict__ xq = bb + (32 * c + quad) * L::kXS;
+      u32x4 braw[4];
+      if constexpr (TR) {
+        typedef short s16x4 __attribute__((ext_vector_type(4)));
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const char* bc = reinterpret_cast<const char*>(bb) + 32 * c * L::kXS * 4;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const s16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4*)(bc + trb[b] + 4 * h * L::kXS * 4));
+            const u32x2 d2 = __builtin_bit_cast(u32x2, t);
+            braw[b][2 * h] = d2[0];
+            braw[b][2 * h + 1] = d2[1];
+          }
+      }
 #pragma unroll
       for (int kj = 0; kj < 3; ++kj) {
         const int dw = kj - 1;
@@ -322,7 +358,27 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
         for (int blk = 0; blk < 2; ++blk) {
           const int col = el0 + 16 * blk + dw;
           V bfr[P];
-          if constexpr (PAIR) {
+          if constexpr (TR) {
+            // tap column kj - 1: the block's own reads (kj = 1), or shifted
+            // one lane down (kj = 0: lane n takes lane n - 1, lane 0 the
+            // previous block's lane 15) or up (kj = 2: lane n takes n + 1,
+            // lane 15 the next block's lane 0) within each 16-lane row
+            u32x4 wv;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              const int own = (int)braw[blk + 1][d];
+              if (kj == 1) {
+                wv[d] = (uint32_t)own;
+              } else if (kj == 0) {
+                const int end = __builtin_amdgcn_update_dpp(0, (int)braw[blk][d], 0x121, 0xf, 0xf, false);
+                wv[d] = (uint32_t)__builtin_amdgcn_update_dpp(end, own, 0x111, 0xf, 0xf, false);
+              } else {
+                const int end = __builtin_amdgcn_update_dpp(0, (int)braw[blk + 2][d], 0x12f, 0xf, 0xf, false);
+                wv[d] = (uint32_t)__builtin_amdgcn_update_dpp(end, own, 0x101, 0xf, 0xf, false);
+              }
+            }
+            bfr[0] = __builtin_bit_cast(V, wv);
+          } else if constexpr (PAIR) {
             // pair planes: dword jj of the hi / lo fragment is staged plane
             // quad + 4jj / 16 + quad + 4jj (the pair 8jj + 2quad, +1), already split
             u32x4 h4, l4;
@@ -511,17 +567,23 @@ int cv_run(const void* in, const void* wt, const void* bias, void* out, void* wo
   g.x4 = (w % 8 == 0) && ((uintptr_t)in % 16 == 0);
   return cv_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
+    // aligned layout: 256-column segments on whole image rows, 16-byte rows,
+    // whole 32-plane chunks in every K split; with 2-byte types and four m
+    // blocks its B operands come from transposing reads in natural slot order
+    const bool al = g.rs == 1 && g.sw == kCvPix && w % kCvPix == 0 && g.x4 && k % 32 == 0 &&
+                    g.nc32 % g.cc_per == 0;
+    const bool nat = sizeof(T) == 2 && al && g.mb == 4;
     const int64_t units = (int64_t)g.mgroups * g.nc32 * 9 * g.mb * 64;
     const dim3 pgrid((unsigned)((units + 255) / 256));
     if (g.mb == 4)
       hipLaunchKernelGGL((conv3x3_pack_kernel<T, 4>), pgrid, dim3(256), 0, stream, (const T*)wt,
-                         (uint32_t*)workspace, g, rot, (int)pairs);
+                         (uint32_t*)workspace, g, rot, (int)pairs, (int)nat);
     else if (g.mb == 2)
       hipLaunchKernelGGL((conv3x3_pack_kernel<T, 2>), pgrid, dim3(256), 0, stream, (const T*)wt,
-                         (uint32_t*)workspace, g, rot, (int)pairs);
+                         (uint32_t*)workspace, g, rot, (int)pairs, (int)nat);
     else
       hipLaunchKernelGGL((conv3x3_pack_kernel<T, 1>), pgrid, dim3(256), 0, stream, (const T*)wt,
-                         (uint32_t*)workspace, g, rot, (int)pairs);
+                         (uint32_t*)workspace, g, rot, (int)pairs, (int)nat);
     int e = (int)hipGetLastError();
     if (e != 0) return e;
     const dim3 grid((unsigned)((int64_t)n * g.tiles_h * g.tiles_w * g.mgroups * g.ks));
@@ -559,10 +621,6 @@ int cv_run(const void* in, const void* wt, const void* bias, void* out, void* wo
       // leave no room for a second: with more workgroups, as the input
       // gradient's 1024 at 256x256, measured 37 -> 50 us; forward 41.1 ->
       // 40.2 us)
-      // aligned layout: 256-column segments on whole image rows, 16-byte rows,
-      // whole 32-plane chunks in every K split
-      const bool al = g.rs == 1 && g.sw == kCvPix && w % kCvPix == 0 && g.x4 && k % 32 == 0 &&
-                      g.nc32 % g.cc_per == 0;
       if constexpr (sizeof(T) == 2) {
         if (g.mb == 4 && g.rs == 1 && g.cc_per % 2 == 0 && g.nc32 % g.cc_per == 0 &&
             (int64_t)grid.x <= kCvFillWGs) {

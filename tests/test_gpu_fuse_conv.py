@@ -48,6 +48,16 @@ def test_fuse_conv_matches_conv2d(shape, dtype):
     _check(shape, dtype, 900)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_fuse_conv_aligned_layout(dtype):
+    """Two 256-column tiles per row, 64 rows, C=32: both directions take the
+    aligned-layout kernels with four-block m groups (2-byte types: transposing
+    operand reads, the forward with two 32-plane chunks per stage), with tap
+    columns crossing the tile seam."""
+    say(f"fuse conv aligned layout (2, 32, 64, 512) dtype={dtype}")
+    _check((2, 32, 64, 512), dtype, 915)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("hw", [256, 128])
 def test_fuse_conv_full_size(dtype, hw):
