@@ -366,16 +366,8 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
             u32x4 wv;
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-              const int own = (int)braw[blk + 1][d];
-              if (kj == 1) {
-                wv[d] = (uint32_t)own;
-              } else if (kj == 0) {
-                const int end = __builtin_amdgcn_update_dpp(0, (int)braw[blk][d], 0x121, 0xf, 0xf, false);
-                wv[d] = (uint32_t)__builtin_amdgcn_update_dpp(end, own, 0x111, 0xf, 0xf, false);
-              } else {
-                const int end = __builtin_amdgcn_update_dpp(0, (int)braw[blk + 2][d], 0x12f, 0xf, 0xf, false);
-                wv[d] = (uint32_t)__builtin_amdgcn_update_dpp(end, own, 0x101, 0xf, 0xf, false);
-              }
+              const uint32_t pv = braw[blk][d], ov = braw[blk + 1][d], nv = braw[blk + 2][d];
+              wv[d] = kj == 1 ? ov : (kj == 0 ? lane_shift<-1>(pv, ov, nv) : lane_shift<1>(pv, ov, nv));
             }
             bfr[0] = __builtin_bit_cast(V, wv);
           } else if constexpr (PAIR) {

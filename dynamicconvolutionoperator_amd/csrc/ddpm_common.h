@@ -170,6 +170,33 @@ struct Mma<f16> {
 };
 
 // ---------------------------------------------------------------------------
+// Column shift of a B fragment held as 16-column blocks (B lane l holds
+// column l & 15 of its block): the fragment of the block `own` moved by S
+// columns (|S| <= 15), each lane taking lane n + S of its 16-lane row (DPP
+// row_shl / row_shr) and the lanes past the row's end the neighbouring
+// block's (`next` for S > 0, `prev` for S < 0) by a row rotation (row_ror),
+// whose result stays in place where the shift has no source lane
+// (bound_ctrl off).  One dword of the fragment per call.
+// ---------------------------------------------------------------------------
+template <int S>
+__device__ __forceinline__ uint32_t lane_shift(uint32_t prev, uint32_t own, uint32_t next) {
+  static_assert(S >= -15 && S <= 15, "one 16-lane row at most");
+  if constexpr (S == 0) {
+    (void)prev;
+    (void)next;
+    return own;
+  } else if constexpr (S > 0) {
+    (void)prev;
+    const int end = __builtin_amdgcn_update_dpp(0, (int)next, 0x120 + (16 - S), 0xf, 0xf, false);
+    return (uint32_t)__builtin_amdgcn_update_dpp(end, (int)own, 0x100 + S, 0xf, 0xf, false);
+  } else {
+    (void)next;
+    const int end = __builtin_amdgcn_update_dpp(0, (int)prev, 0x120 - S, 0xf, 0xf, false);
+    return (uint32_t)__builtin_amdgcn_update_dpp(end, (int)own, 0x110 - S, 0xf, 0xf, false);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Vector loads/stores of VEC consecutive elements as fp32 (VEC in {1,2,4,8}).
 // Callers guarantee alignment of VEC*sizeof(T) bytes when VEC > 1.
 // ---------------------------------------------------------------------------
@@ -242,12 +269,14 @@ __device__ __forceinline__ BufRes make_buf(const void* base, uint32_t bytes) {
                                            0x00020000);
 }
 
+// `soff`: a wave-uniform part of the offset, added in the load's scalar
+// offset (no vector instruction); with off = kOob the sum stays past the end.
 template <typename T>
-__device__ __forceinline__ float buf_load1(BufRes r, uint32_t off) {
+__device__ __forceinline__ float buf_load1(BufRes r, uint32_t off, uint32_t soff = 0) {
   if constexpr (sizeof(T) == 4) {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, soff, 0));
   } else {
-    const unsigned short s = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    const unsigned short s = __builtin_amdgcn_raw_buffer_load_b16(r, off, soff, 0);
     return to_f(__builtin_bit_cast(T, s));
   }
 }

@@ -215,8 +215,20 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
   //      each chunk cc of the group at its two pixels (held for the KS
   //      stages of one (b, chunk group))
   const int px0 = 32 * wave + col16;  // pixel of block 0 within the tile; block 1 is +16
-  float gv[CH][2][8];
-  auto load_g = [&](int bg) {
+  // gv: the current (b, chunk group)'s values; gn: the next one's, loaded
+  // during the last stage of the current one (its latency hidden behind that
+  // stage's MFMAs, as the stage's copies are)
+  float gv[CH][2][8], gn[CH][2][8];
+  // aligned layout (whole 32-channel chunks): the lane's byte offset of
+  // channel quad at its pixel of each block (kOob past the last column),
+  // formed once; the channel's part goes in the loads' scalar offset
+  uint32_t glo[2];
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const int w = w0 + px0 + 16 * blk;
+    glo[blk] = w < W ? ((uint32_t)quad * (uint32_t)HW + (uint32_t)(h * W + w)) * (uint32_t)E : kOob;
+  }
+  auto load_g = [&](int bg, float (&gd)[CH][2][8]) {
     const int cg = bg % ncg, b = bg / ncg;
     const BufRes gres = make_buf(gout + ((int64_t)n * 4 * C + (int64_t)(b + 1) * C) * HW,
                                  (uint32_t)(C * HW * (int64_t)E));
@@ -227,10 +239,15 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
         const int w = w0 + px0 + 16 * blk;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const int ch = (cg * CH + c) * 32 + 4 * e + quad;
-          const uint32_t off =
-              (ch < C && w < W) ? (uint32_t)((int64_t)ch * HW + (int64_t)h * W + w) * E : kOob;
-          gv[c][blk][e] = buf_load1<T>(gres, off);
+          if constexpr (AL) {
+            const uint32_t so = (uint32_t)((cg * CH + c) * 32 + 4 * e) * (uint32_t)HW * (uint32_t)E;
+            gd[c][blk][e] = buf_load1<T>(gres, glo[blk], so);
+          } else {
+            const int ch = (cg * CH + c) * 32 + 4 * e + quad;
+            const uint32_t off =
+                (ch < C && w < W) ? (uint32_t)((int64_t)ch * HW + (int64_t)h * W + w) * E : kOob;
+            gd[c][blk][e] = buf_load1<T>(gres, off);
+          }
         }
       }
   };
@@ -242,7 +259,7 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
     for (int ib = 0; ib < MB; ++ib) acc[blk][ib] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   stage(0, 0);
-  load_g(0);
+  load_g(0, gv);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int s = 0; s < nstage; ++s) {
@@ -252,6 +269,9 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
     const int bg = s / KS;
     const int b = bg / ncg;
     const int d = dil_of(b, g.d0, g.d1, g.d2);
+    // the next (b, chunk group)'s branch-gradient values, during this stage
+    const bool gnext = ki == KS - 1 && s + 1 < nstage;
+    if (gnext) load_g(bg + 1, gn);
     const uint32_t* __restrict__ bb = ysm + buf * L::kBuf;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
@@ -288,10 +308,16 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
         }
       }
     }
-    // the next (b, chunk group) needs new branch-gradient values
-    if (ki == KS - 1 && s + 1 < nstage) load_g(bg + 1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    if (gnext) {
+#pragma unroll
+      for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) gv[c][blk][e] = gn[c][blk][e];
+    }
   }
 
   // ---- store: lane holds dY[i = ib*16 + 4*quad + e][pixel col16 of block]
