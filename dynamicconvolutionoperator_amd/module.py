@@ -33,6 +33,7 @@ import functools
 
 import torch
 from torch import nn
+from torch.nn.modules import module as _torch_module
 
 from . import _cpu
 
@@ -56,12 +57,11 @@ def _load_hip_ops():
 def _module_hooks_set(m: nn.Module) -> bool:
     """Whether calling ``m`` would run a hook: its own forward / backward
     hooks or the global module hooks."""
-    from torch.nn.modules import module as _m
-
+    g = _torch_module
     return bool(
         m._forward_hooks or m._forward_pre_hooks or m._backward_hooks or m._backward_pre_hooks
-        or _m._global_forward_hooks or _m._global_forward_pre_hooks
-        or _m._global_backward_hooks or _m._global_backward_pre_hooks
+        or g._global_forward_hooks or g._global_forward_pre_hooks
+        or g._global_backward_hooks or g._global_backward_pre_hooks
     )
 
 

@@ -20,7 +20,6 @@ kernels run asynchronously on the current stream.  Tensors must be on a ROCm
 from __future__ import annotations
 
 import contextlib
-import ctypes
 import functools
 
 import torch
@@ -42,8 +41,10 @@ def _dt(t: torch.Tensor) -> int:
         raise TypeError(f"unsupported dtype {t.dtype}; expected float32, bfloat16 or float16") from None
 
 
-def _ptr(t: torch.Tensor) -> ctypes.c_void_p:
-    return ctypes.c_void_p(t.data_ptr())
+def _ptr(t: torch.Tensor) -> int:
+    """t's device address for a ``void*`` argument (ctypes converts the int
+    through the function's argtypes; no c_void_p object per pointer)."""
+    return t.data_ptr()
 
 
 # The current device and the raw handle of its current stream straight from
@@ -54,10 +55,11 @@ _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None) or (
     lambda idx: torch.cuda.current_stream(idx).cuda_stream)
 
 
-def _stream(t: torch.Tensor) -> ctypes.c_void_p:
-    """The current stream of t's device, as the C-ABI's hipStream_t."""
+def _stream(t: torch.Tensor) -> int:
+    """The current stream of t's device, as the C-ABI's hipStream_t (an int
+    for the ``void*`` argument)."""
     idx = t.device.index
-    return ctypes.c_void_p(_raw_stream(_current_device() if idx is None else idx))
+    return _raw_stream(_current_device() if idx is None else idx)
 
 
 def _on(device: torch.device):
@@ -176,6 +178,15 @@ def fused_dynamic_cat(x, kernels, kernel_size, dilations):
 _FUSED_MAX_IMAGE_BYTES = 2**31 - 1
 
 
+@functools.lru_cache(maxsize=256)
+def _gen_query(forward_only: bool, channels: int, kernel_size: int, max_dilation: int) -> bool:
+    """The library's coverage query (a pure function of its arguments, asked
+    once per configuration: the module checks it on every call)."""
+    lib = _lib.load()
+    query = lib.ddpm_gen_fwd_supported if forward_only else lib.ddpm_gen_supported
+    return bool(query(channels, kernel_size, max_dilation))
+
+
 def generator_supported(channels: int, kernel_size: int, dilations=(1, 3, 5), shape=None,
                         dtype=None, forward_only: bool = False) -> bool:
     """Whether the fused generator kernels handle this configuration and,
@@ -183,9 +194,7 @@ def generator_supported(channels: int, kernel_size: int, dilations=(1, 3, 5), sh
     fit their 32-bit offsets.  ``forward_only``: the forward alone (inference:
     ``ddpm_gen_fwd_supported``, K in {1, 3, 5}); else forward and recompute
     backward (``ddpm_gen_supported``, K in {1, 3})."""
-    lib = _lib.load()
-    query = lib.ddpm_gen_fwd_supported if forward_only else lib.ddpm_gen_supported
-    if not query(int(channels), int(kernel_size), int(max(dilations))):
+    if not _gen_query(bool(forward_only), int(channels), int(kernel_size), int(max(dilations))):
         return False
     if shape is not None:
         esize = (dtype if dtype is not None else torch.float32).itemsize
@@ -229,9 +238,8 @@ def _launch_generator_dynamic_cat(x, y, weight, bias, k, dil):
 
 class _GeneratorDynamicCat(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, y, weight, bias, kernel_size, dilations):
-        k = _check_kernel_size(kernel_size)
-        dil = _check_dilations(dilations)
+    def forward(ctx, x, y, weight, bias, k, dil):
+        # k and dil as fused_generator_dynamic_cat checked them
         x = x.contiguous()
         y = y.contiguous()
         weight = weight.contiguous()
@@ -248,6 +256,10 @@ class _GeneratorDynamicCat(torch.autograd.Function):
         grads = _generator_backward(x, y, weight, bias, _as(grad_out, x.dtype), ctx.kernel_size,
                                     ctx.dilations, ctx.needs_input_grad[:4])
         return (*grads, None, None)
+
+
+def _align256(nbytes: int) -> int:
+    return (nbytes + 255) // 256 * 256
 
 
 def _generator_backward(x, y, weight, bias, grad_out, k, dil, needs):
@@ -269,6 +281,34 @@ def _generator_backward(x, y, weight, bias, grad_out, k, dil, needs):
                 wsy_bytes)
 
     with _on(x.device):
+        if combined:
+            # one call: dY's weight packing and dX's halo reduction run on
+            # the CUs dW leaves free; its three workspaces share one
+            # allocation (256-byte aligned parts)
+            grad_x = torch.empty_like(x)
+            grad_y = torch.empty_like(y)
+            grad_w = torch.empty_like(weight)
+            grad_b = torch.empty_like(bias)
+            wsx_bytes = _ws_bytes("ddpm_gen_bwd_x_workspace_bytes", n, c, h, w, k, *dil)
+            ws_bytes = _ws_bytes("ddpm_gen_bwd_w_workspace_bytes", n, c, h, w, k, dt)
+            wsy_bytes = _ws_bytes("ddpm_gen_bwd_y_workspace_bytes", c, k)
+            oy = _align256(wsx_bytes)
+            ow = oy + _align256(wsy_bytes)
+            wsall = torch.empty(ow + max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+            base = wsall.data_ptr()
+            _lib.check(
+                lib.ddpm_gen_bwd(_ptr(x), _ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
+                                 _ptr(grad_x), _ptr(grad_y), _ptr(grad_w), _ptr(grad_b),
+                                 base, wsx_bytes, base + oy, wsy_bytes, base + ow, ws_bytes,
+                                 n, c, h, w, k, *dil, dt, stream),
+                "ddpm_gen_bwd",
+            )
+            del wsall
+            if not needs[2]:
+                grad_w = None
+            if not needs[3]:
+                grad_b = None
+            return grad_x, grad_y, grad_w, grad_b
         if need_x:
             grad_x = torch.empty_like(x)
             wsx_bytes = _ws_bytes("ddpm_gen_bwd_x_workspace_bytes", n, c, h, w, k, *dil)
@@ -279,19 +319,7 @@ def _generator_backward(x, y, weight, bias, grad_out, k, dil, needs):
             ws_bytes = _ws_bytes("ddpm_gen_bwd_w_workspace_bytes", n, c, h, w, k, dt)
             ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
         y_pending = need_y
-        if combined:
-            grad_y, wsy, wsy_bytes = alloc_y()
-            # one call: dY's weight packing and dX's halo reduction run on
-            # the CUs dW leaves free
-            _lib.check(
-                lib.ddpm_gen_bwd(_ptr(x), _ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
-                                 _ptr(grad_x), _ptr(grad_y), _ptr(grad_w), _ptr(grad_b),
-                                 _ptr(wsx), wsx_bytes, _ptr(wsy), wsy_bytes, _ptr(ws), ws_bytes,
-                                 n, c, h, w, k, *dil, dt, stream),
-                "ddpm_gen_bwd",
-            )
-            y_pending = False
-        elif need_x and need_wb:
+        if need_x and need_wb:
             # one call: dX's halo reduction runs on the CUs dW leaves free
             _lib.check(
                 lib.ddpm_gen_bwd_xw(_ptr(x), _ptr(y), _ptr(weight), _ptr(bias), _ptr(grad_out),
@@ -520,23 +548,26 @@ def _fuse_conv_backward(cat, weight, has_bias, grad_out, needs, cat_code):
     dt = _dt(weight)
     grad_cat = grad_w = grad_b = None
     lib = _lib.load()
+    need_w = needs[1]
+    need_b = has_bias and needs[2]
+    # one workspace serves both calls (they run in order on one stream)
+    data_bytes = _ws_bytes("ddpm_fuse_conv_workspace_bytes", n, c, h, w, dt) if needs[0] else 0
+    weight_bytes = (_ws_bytes("ddpm_fuse_conv_bwd_weight_workspace_bytes", n, c, h, w, cat_code)
+                    if need_w or need_b else 0)
+    ws = torch.empty(max(data_bytes, weight_bytes, 16), dtype=torch.uint8, device=cat.device)
     if needs[0]:
         grad_cat = torch.empty((n, ci, h, w), dtype=weight.dtype, device=cat.device)
         with _on(cat.device):
-            ws, nbytes = _fuse_conv_workspace(n, c, h, w, dt, cat.device)
             code = lib.ddpm_fuse_conv_bwd_data(_ptr(grad_out), _ptr(weight), _ptr(grad_cat),
-                                               _ptr(ws), nbytes, n, c, h, w, dt, _stream(cat))
+                                               _ptr(ws), data_bytes, n, c, h, w, dt, _stream(cat))
         _lib.check(code, "ddpm_fuse_conv_bwd_data")
-    need_w = needs[1]
-    need_b = has_bias and needs[2]
     if need_w or need_b:
         gw = torch.empty_like(weight)
         gb = torch.empty((c,), dtype=weight.dtype, device=cat.device)
         with _on(cat.device):
-            nbytes = _ws_bytes("ddpm_fuse_conv_bwd_weight_workspace_bytes", n, c, h, w, cat_code)
-            ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=cat.device)
             code = lib.ddpm_fuse_conv_bwd_weight(_ptr(cat), _ptr(grad_out), _ptr(gw), _ptr(gb),
-                                                 _ptr(ws), nbytes, n, c, h, w, cat_code, _stream(cat))
+                                                 _ptr(ws), weight_bytes, n, c, h, w, cat_code,
+                                                 _stream(cat))
         if code == _lib.STATUS_UNSUPPORTED and cat_code != _PAIR_PLANES:
             _, gw, gb = torch.ops.aten.convolution_backward(
                 grad_out, cat, weight, [c] if has_bias else None, [1, 1], [1, 1], [1, 1],
