@@ -54,6 +54,7 @@ struct ConvGeom {
   int nc32;           // ceil(K / 32)
   int mb;             // 16-plane blocks of m per workgroup
   int mgroups;        // ceil(M / (mb * 16))
+  int mgl;            // m groups a workgroup runs one after another (divides mgroups)
   int ks;             // splits of the input planes (K): 1, or more for small images
   int cc_per;         // 32-plane chunks per K split
   int seg;            // staged elements per segment row (sw + 2 * kCvPad)
@@ -132,6 +133,42 @@ struct CvLds {
   static_assert(kCvPix == 256, "segments hold at most kXD dwords per plane");
 };
 
+// The sums of m group mg: lane (col16, quad) holds out[m = (mg*MB + ib)*16 +
+// 4*quad + e] at row h, columns w + 16*blk (blk = 0, 1); fp32 partials of K
+// split `ksplit` where the input planes are split, else the result in T with
+// the bias.
+template <typename T, bool BIAS, int MB>
+__device__ __forceinline__ void cv_store(const f32x4 (&acc)[2][MB], int mg, const ConvGeom& g,
+                                         const T* __restrict__ bias, T* __restrict__ out,
+                                         float* __restrict__ part, int ksplit, int n, int h, int w,
+                                         int quad) {
+  const int H = g.H, W = g.W;
+  const int64_t HW = (int64_t)H * W;
+  if (h >= H) return;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const int wb = w + 16 * blk;
+    if (wb < W) {
+      const int64_t o = ((int64_t)ksplit * g.N + n) * g.M * HW + (int64_t)h * W + wb;
+#pragma unroll
+      for (int ib = 0; ib < MB; ++ib)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int m = (mg * MB + ib) * 16 + 4 * quad + e;
+          if (m < g.M) {
+            float v = acc[blk][ib][e];
+            if (g.ks > 1) {
+              part[o + (int64_t)m * HW] = v;
+            } else {
+              if constexpr (BIAS) v += to_f(bias[m]);
+              out[o + (int64_t)m * HW] = from_f<T>(v);
+            }
+          }
+        }
+    }
+  }
+}
+
 // out: the result in T (ks = 1), or with K split (ks > 1) the fp32 partial
 // sums part[ksplit][n][M][H*W] (no bias) that conv3x3_reduce_kernel adds up.
 // CH: 32-plane chunks per stage (2 for 2-byte types when a K split's chunk
@@ -140,7 +177,10 @@ struct CvLds {
 // width is a multiple of 256, 16-byte input rows, whole 32-plane chunks: the
 // copies take their offsets from per-lane parts formed once and scalar parts
 // formed per stage, without per-copy tests.
-template <typename T, bool BIAS, int MB, bool WIDE, bool PAIR = false, int CH = 1, bool AL = false>
+// MGL: the workgroup runs g.mgl m groups one after another in one staging
+// pipeline (g.mgl = 1 otherwise).
+template <typename T, bool BIAS, int MB, bool WIDE, bool PAIR = false, int CH = 1, bool AL = false,
+          bool MGL = false>
 __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict__ in,
                                                              const uint32_t* __restrict__ pk,
                                                              const T* __restrict__ bias,
@@ -155,8 +195,10 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
   extern __shared__ __attribute__((aligned(16))) uint32_t csm[];
 
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
-  const int mg = bid % g.mgroups;
-  const int rest = bid / g.mgroups;
+  const int mgl = MGL ? g.mgl : 1;
+  const int mgw = g.mgroups / mgl;  // workgroups per (tile, K split)
+  const int mg0 = (bid % mgw) * mgl;
+  const int rest = bid / mgw;
   const int ksplit = rest % g.ks;
   const int tile = rest / g.ks;
   const int tiles_img = g.tiles_h * g.tiles_w;
@@ -174,7 +216,12 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
   // (CH divides its chunk count)
   const int cc0 = ksplit * g.cc_per;
   const int cc1 = cc0 + g.cc_per < g.nc32 ? cc0 + g.cc_per : g.nc32;
-  const int nstage = cc1 > cc0 ? 3 * ((cc1 - cc0) / CH) : 0;
+  // stages of one m group; the workgroup runs its mgl m groups' stages in
+  // one pipeline (m group mg0 + s / nst1), storing each group's sums after
+  // its last stage (one workgroup per tile instead of mgl short ones: the
+  // staging pipeline fills once)
+  const int nst1 = cc1 > cc0 ? 3 * ((cc1 - cc0) / CH) : 0;
+  const int nstage = nst1 * mgl;
   // this wave's 32 pixels: segment row wseg (wave-uniform), columns pcol0 ..
   const int wseg = (32 * wave) / g.sw;
   const int pcol0 = 32 * wave - wseg * g.sw;
@@ -209,8 +256,11 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
   const BufRes xnul = make_buf(in, 0u);
   // ---- stage s = (chunk group) * 3 + ki -> LDS buffer `buf`
   auto stage = [&](int s, int buf) {
-    const int ki = s % 3;
-    const int ccb = cc0 + (s / 3) * CH;  // first chunk of the group
+    const int gs = MGL ? s / nst1 : 0;  // m group of stage s
+    const int mg = mg0 + gs;
+    const int s1 = s - gs * nst1;
+    const int ki = s1 % 3;
+    const int ccb = cc0 + (s1 / 3) * CH;  // first chunk of the group
     uint32_t* __restrict__ dstb = csm + buf * L::kBuf;
     if constexpr (AL) {
       // one image row per stage (a row outside the image copies through a
@@ -293,6 +343,13 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
   for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
     for (int ib = 0; ib < MB; ++ib) acc[blk][ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // ---- store of m group mg: lane holds out[m = (mg*MB + ib)*16 + 4*quad +
+  //      e][pixel col16 of block]
+  auto store_mg = [&](int mg) {
+    cv_store<T, BIAS, MB>(acc, mg, g, bias, out, part, ksplit, n, h0 + wseg, w0 + pcol0 + col16,
+                          quad);
+  };
 
   // staged element of this lane's block-0 pixel at tap column 0: segment row
   // wseg, column pad + pcol0 + col16
@@ -403,35 +460,26 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
         }
       }
     }
+    // (the stage's LDS-direct copies are vector memory operations: wait for
+    // all of them, then the barrier)
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    if (MGL && (s + 1) % nst1 == 0) {
+      // the m group's last stage: its sums out (the stores complete under the
+      // next group's first stage), the accumulators cleared for that group
+      store_mg(mg0 + s / nst1);
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int ib = 0; ib < MB; ++ib) acc[blk][ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   }
 
-  // ---- store: lane holds out[m = (mg*MB + ib)*16 + 4*quad + e][pixel col16 of block]
-  const int h = h0 + wseg;
-  if (h < H) {
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      const int w = w0 + pcol0 + col16 + 16 * blk;
-      if (w < W) {
-        const int64_t o = ((int64_t)ksplit * g.N + n) * g.M * HW + (int64_t)h * W + w;
-#pragma unroll
-        for (int ib = 0; ib < MB; ++ib)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int m = (mg * MB + ib) * 16 + 4 * quad + e;
-            if (m < g.M) {
-              float v = acc[blk][ib][e];
-              if (g.ks > 1) {
-                part[o + (int64_t)m * HW] = v;
-              } else {
-                if constexpr (BIAS) v += to_f(bias[m]);
-                out[o + (int64_t)m * HW] = from_f<T>(v);
-              }
-            }
-          }
-      }
-    }
+  if (!MGL) {
+    store_mg(mg0);
+  } else if (nst1 == 0) {
+    // no input planes in this K split: its partial sums are zero
+    for (int mg = mg0; mg < mg0 + mgl; ++mg) store_mg(mg);
   }
 }
 
@@ -511,8 +559,19 @@ void cv_geom(ConvGeom& g, int64_t n, int64_t k, int64_t m, int64_t h, int64_t w,
   g.ks = (g.nc32 + g.cc_per - 1) / g.cc_per;
   while (g.mb > 1 && tiles * ((m + g.mb * 16 - 1) / (g.mb * 16)) * g.ks < kCvFillWGs) g.mb /= 2;
   g.mgroups = (int)((m + g.mb * 16 - 1) / (g.mb * 16));
+  // fp32: m groups per workgroup, the largest divisor of mgroups that leaves
+  // at least kCvFillWGs workgroups (the input gradient at 256x256: 4 groups,
+  // 256 workgroups of 4 x 6 stages instead of 1024 of 6: 76.0 -> 71.8 us).
+  // 2-byte types keep one (their 1024 short workgroups run two to a CU: 35.8
+  // -> 43.2 us with four groups each)
+  g.mgl = 1;
+  if (esz == 4)
+    for (int d = g.mgroups; d > 1; --d)
+      if (g.mgroups % d == 0 && tiles * (g.mgroups / d) * g.ks >= kCvFillWGs) {
+        g.mgl = d;
+        break;
+      }
   g.seg = sw + 2 * kCvPad;
-  (void)esz;
   g.x4 = 0;
 }
 
@@ -565,6 +624,9 @@ int cv_run(const void* in, const void* wt, const void* bias, void* out, void* wo
     const bool al = g.rs == 1 && g.sw == kCvPix && w % kCvPix == 0 && g.x4 && k % 32 == 0 &&
                     g.nc32 % g.cc_per == 0;
     const bool nat = sizeof(T) == 2 && al && g.mb == 4;
+    // several m groups per workgroup: the fp32 input gradient's aligned
+    // layout only (plain concat layout, no bias)
+    if (!(sizeof(T) == 4 && al && g.mb == 4 && !pairs && !bias)) g.mgl = 1;
     const int64_t units = (int64_t)g.mgroups * g.nc32 * 9 * g.mb * 64;
     const dim3 pgrid((unsigned)((units + 255) / 256));
     if (g.mb == 4)
@@ -578,7 +640,7 @@ int cv_run(const void* in, const void* wt, const void* bias, void* out, void* wo
                          (uint32_t*)workspace, g, rot, (int)pairs, (int)nat);
     int e = (int)hipGetLastError();
     if (e != 0) return e;
-    const dim3 grid((unsigned)((int64_t)n * g.tiles_h * g.tiles_w * g.mgroups * g.ks));
+    const dim3 grid((unsigned)((int64_t)n * g.tiles_h * g.tiles_w * (g.mgroups / g.mgl) * g.ks));
     auto launch = [&](auto kern, size_t lds) {
       const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
       if (ae != 0) return ae;
@@ -624,6 +686,11 @@ int cv_run(const void* in, const void* wt, const void* bias, void* out, void* wo
         }
       }
       if (g.mb == 4 && g.rs == 1) {
+        if constexpr (sizeof(T) == 4 && !B && !PR) {
+          if (g.mgl > 1)
+            return launch(conv3x3_kernel<T, false, 4, true, false, 1, true, true>,
+                          (size_t)2 * CvLds<T, 4, true>::kBuf * 4);
+        }
         if (al)
           return launch(conv3x3_kernel<T, B, 4, true, PR, 1, true>,
                         (size_t)2 * CvLds<T, 4, true>::kBuf * 4);
