@@ -145,8 +145,8 @@ __global__ __launch_bounds__(kFilterThreads) void filter_fwd_kernel(const TX* __
   typedef typename Vec<TK, V>::type KV;
   extern __shared__ float xs[];
   // fp32: neighbouring row tiles of a plane (which share halo rows) on one
-  // XCD -- measured 6% faster at 256x256; the 2-byte forward and the
-  // backward kernels measured faster in plain dispatch order
+  // XCD -- measured 6% faster at 256x256 (so is the fp32 dX gather); the
+  // 2-byte forward and the dK kernel measured faster in plain dispatch order
   const int bid = sizeof(TK) == 4 ? xcd_remap(blockIdx.x, gridDim.x) : (int)blockIdx.x;
   const int plane = bid / g.tiles;
   const int tile = bid - plane * g.tiles;
