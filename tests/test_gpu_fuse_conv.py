@@ -58,6 +58,15 @@ def test_fuse_conv_aligned_layout(dtype):
     _check((2, 32, 64, 512), dtype, 915)
 
 
+def test_fuse_conv_input_gradient_m_groups():
+    """fp32 input gradient whose workgroups run several 64-plane output
+    groups in one staging pipeline: 128 rows x 256 columns, C = 64 (M = 256:
+    two groups per workgroup; the 256x256 size of test_fuse_conv_full_size
+    runs four)."""
+    say("fuse conv fp32 (1, 64, 128, 256): two m groups per workgroup")
+    _check((1, 64, 128, 256), torch.float32, 920)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("hw", [256, 128])
 def test_fuse_conv_full_size(dtype, hw):
