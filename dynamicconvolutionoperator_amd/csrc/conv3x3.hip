@@ -30,7 +30,13 @@
 //     (fp32: split into bf16 hi / lo), so a fragment is one 16-byte LDS read;
 //   * MFMA slot k = 8*quad + e of a 32-plane chunk holds plane 4*e + quad (A
 //     and B alike): a lane's 8 B-operand reads are 4 planes apart and, with a
-//     row pitch of 16 (mod 64) dwords, bank-conflict free;
+//     row pitch of 16 (mod 64) dwords, bank-conflict free; the 2-byte
+//     aligned-layout instantiations instead read their B operands by
+//     transposing LDS reads in natural slot order (slot k = plane k) and form
+//     the tap columns -1 / +1 by DPP lane shifts;
+//   * where the grid would hold more than one workgroup per CU for a row
+//     segment (the fp32 input gradient at 256x256: four m groups), a
+//     workgroup runs several m groups in one staging pipeline;
 //   * v_mfma_f32_16x16x32_{bf16,f16}; fp32 operands run as three bf16
 //     products (hi*hi + hi*lo + lo*hi), accumulation in fp32.
 
