@@ -548,31 +548,63 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
   }
 }
 
-// Fixed-order sum of the split partials into grad_weight[co][ci][t] and
-// grad_bias[co]; one output element per thread (partials read with the
-// split stride, coalesced over co).
+// Fixed-order sum of the split partials [split][9][CI][C] into
+// grad_weight[co][ci][t] and grad_bias[co].  A workgroup sums a tile of
+// kCrCI ci x 9 taps x kCrCO co -- reading runs of kCrCO co of each (tap, ci)
+// row, the split stride apart -- and writes it through LDS as kCrCO runs of
+// kCrCI * 9 consecutive elements (one co's ci x taps), so reads and writes
+// are both coalesced; the workgroups after the tiles sum the bias partials.
+constexpr int kCrCI = 4;
+constexpr int kCrCO = 16;
 template <typename T>
 __global__ __launch_bounds__(256) void conv_wgrad_reduce_kernel(const float* __restrict__ pw,
                                                                 const float* __restrict__ pb,
                                                                 T* __restrict__ dw_out,
                                                                 T* __restrict__ db_out, int C,
-                                                                int CI, int splits) {
+                                                                int CI, int splits, int tiles) {
+  constexpr int RL = kCrCI * 9;  // one co's run of (ci, t) outputs
+  __shared__ float tile[kCrCO][RL + 1];
+  const int bid = (int)blockIdx.x;
+  if (bid >= tiles) {
+    const int co = (bid - tiles) * 256 + (int)threadIdx.x;
+    if (co < C) {
+      float v = 0.f;
+      for (int s = 0; s < splits; ++s) v += pb[(int64_t)s * C + co];
+      db_out[co] = from_f<T>(v);
+    }
+    return;
+  }
+  const int cib = (CI + kCrCI - 1) / kCrCI;
+  const int cob = bid / cib;
+  const int ci0 = (bid - cob * cib) * kCrCI, co0 = cob * kCrCO;
   const int64_t per = (int64_t)9 * CI * C;
-  const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (item < per) {
-    // item = (t*CI + ci)*C + co
+  for (int idx = (int)threadIdx.x; idx < RL * kCrCO; idx += 256) {
+    const int col = idx % kCrCO, r = idx / kCrCO;  // r = t * kCrCI + ci - ci0
+    const int t = r / kCrCI, cil = r - t * kCrCI;
+    const int ci = ci0 + cil, co = co0 + col;
     float v = 0.f;
+    if (ci < CI && co < C) {
+      const float* __restrict__ src = pw + ((int64_t)t * CI + ci) * C + co;
+      if (splits == kCwMaxSplits) {
+        // every load in flight before the first add
+        float a[kCwMaxSplits];
+#pragma unroll
+        for (int s = 0; s < kCwMaxSplits; ++s) a[s] = src[(int64_t)s * per];
+#pragma unroll
+        for (int s = 0; s < kCwMaxSplits; ++s) v += a[s];
+      } else {
 #pragma unroll 4
-    for (int s = 0; s < splits; ++s) v += pw[(int64_t)s * per + item];
-    const int64_t tc = item / C;
-    const int co = (int)(item - tc * C);
-    const int t = (int)(tc / CI), ci = (int)(tc - (int64_t)t * CI);
-    dw_out[((int64_t)co * CI + ci) * 9 + t] = from_f<T>(v);
-  } else if (item < per + C) {
-    const int co = (int)(item - per);
-    float v = 0.f;
-    for (int s = 0; s < splits; ++s) v += pb[(int64_t)s * C + co];
-    db_out[co] = from_f<T>(v);
+        for (int s = 0; s < splits; ++s) v += src[(int64_t)s * per];
+      }
+    }
+    tile[col][cil * 9 + t] = v;
+  }
+  __syncthreads();
+  for (int idx = (int)threadIdx.x; idx < RL * kCrCO; idx += 256) {
+    const int col = idx / RL, r = idx - col * RL;
+    const int co = co0 + col;
+    if (co < C && ci0 + r / 9 < CI)
+      dw_out[((int64_t)co * CI + ci0) * 9 + r] = from_f<T>(tile[col][r]);
   }
 }
 
@@ -729,10 +761,10 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
                          (const T*)cat, (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g);
       int e = (int)hipGetLastError();
       if (e != 0 || g.direct) return e;
-      const int64_t items = (int64_t)9 * 4 * c * c + c;
-      hipLaunchKernelGGL((conv_wgrad_reduce_kernel<T>), dim3((unsigned)((items + 255) / 256)),
+      const int tiles = (int)(((4 * c + kCrCI - 1) / kCrCI) * ((c + kCrCO - 1) / kCrCO));
+      hipLaunchKernelGGL((conv_wgrad_reduce_kernel<T>), dim3((unsigned)(tiles + (c + 255) / 256)),
                          dim3(256), 0, stream, (const float*)pw, (const float*)pb, (T*)grad_weight,
-                         (T*)grad_bias, (int)c, (int)(4 * c), g.splits);
+                         (T*)grad_bias, (int)c, (int)(4 * c), g.splits, tiles);
       return (int)hipGetLastError();
     };
     return cw_with_mb(mb, [&](auto mbc) {

@@ -40,7 +40,6 @@ constexpr int kWgSegs = 4;                   // 32-token segments per step
 constexpr int kWgTW = 32 * kWgSegs;          // columns per step
 constexpr int kWgPad = 8;                    // staged column halo (>= dilation), even
 constexpr int kWgMaxDil = kWgPad;
-constexpr int kWgMaxSplits = 16;             // fp32 partials at most (the reference's bound)
 constexpr int kWgMinSteps = 4;               // steps per split at least
 
 struct WGradGeom {
@@ -780,9 +779,7 @@ __global__ __launch_bounds__(64 * kWgSegs * WgTaps<KS>::kGroups) void gen_bwd_w_
   }
 }
 
-// Fixed-order sum of the split partials, written in Conv2d parameter layout.
-// A thread sums V consecutive input channels i of one (branch and tap,
-// channel) row over the splits in order; the bias partials follow, one per
+// Fixed-order sum of the split partials (wg_reduce_item), one item per
 // thread.  Indices are 32-bit (the host bounds 3*K*K*C*(C+1) below 2^31).
 constexpr int kWgRedThreads = 256;
 template <typename T, int V>
@@ -792,46 +789,8 @@ __global__ __launch_bounds__(kWgRedThreads) void gen_bwd_w_reduce_kernel(const f
                                                                  T* __restrict__ db_out,
                                                                  uint32_t C, uint32_t KK,
                                                                  int splits) {
-  const uint32_t per = 3u * KK * C * C, perb = 3u * KK * C;
-  const uint32_t nv = per / V;
   const uint32_t item = blockIdx.x * (uint32_t)kWgRedThreads + threadIdx.x;
-  if (item < nv) {
-    const uint32_t idx = item * V;
-    float v[V];
-#pragma unroll
-    for (int e = 0; e < V; ++e) v[e] = 0.f;
-#pragma unroll 8
-    for (int s = 0; s < splits; ++s) {
-      const float* __restrict__ src = pw + (size_t)s * per + idx;
-      if constexpr (V == 4) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(src);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] += a[e];
-      } else {
-        v[0] += src[0];
-      }
-    }
-    // idx = (bt*C + c)*C + i  ->  row o = (b*C + c)*KK + t
-    const uint32_t row = idx / C, i = idx - row * C;
-    const uint32_t bt = row / C, c = row - bt * C;
-    const uint32_t b = bt / KK, t = bt - b * KK;
-    T* __restrict__ dst = dw_out + ((size_t)(b * C + c) * KK + t) * C + i;
-    if constexpr (V == 4) {
-      typedef T T4 __attribute__((ext_vector_type(4)));
-      *reinterpret_cast<T4*>(dst) =
-          (T4){from_f<T>(v[0]), from_f<T>(v[1]), from_f<T>(v[2]), from_f<T>(v[3])};
-    } else {
-      dst[0] = from_f<T>(v[0]);
-    }
-  } else if (item < nv + perb) {
-    const uint32_t j = item - nv;
-    float v = 0.f;
-#pragma unroll 8
-    for (int s = 0; s < splits; ++s) v += pb[(size_t)s * perb + j];
-    const uint32_t bt = j / C, c = j - bt * C;
-    const uint32_t b = bt / KK, t = bt - b * KK;
-    db_out[(b * C + c) * KK + t] = from_f<T>(v);
-  }
+  wg_reduce_item<T, V>(pw, pb, dw_out, db_out, C, KK, splits, item);
 }
 
 int launch_ysplit(const float* y, uint16_t* ys, int64_t chw, int64_t total, hipStream_t stream) {
@@ -944,10 +903,14 @@ int wg_helpers(int dw_blocks) {
 
 // ddpm_gen_bwd_w's work.  check_only: validate and return before launching.
 // fin (optional): a halo reduction of the input gradient to run alongside.
+// yp (optional): the dY weight packing to run alongside.  defer (optional):
+// describe the split reduction there (items 0 with one split) instead of
+// launching it.
 int bw_run(const void* x, const void* y, const void* grad_out, void* grad_weight,
            void* grad_bias, void* workspace, int64_t workspace_bytes, int64_t n, int64_t c,
            int64_t h, int64_t w, int kernel_size, int d0, int d1, int d2, int dtype,
-           hipStream_t stream, bool check_only, const BxFinish* fin, const YPack* yp = nullptr) {
+           hipStream_t stream, bool check_only, const BxFinish* fin, const YPack* yp = nullptr,
+           WReduce* defer = nullptr) {
   if (dtype < kF32 || dtype > kF16) return kBadArgument;
   GenGeom gg;
   int st = gen_make_geom(gg, n, c, h, w, kernel_size, d0, d1, d2);
@@ -1014,6 +977,11 @@ int bw_run(const void* x, const void* y, const void* grad_out, void* grad_weight
       const bool v4 = c % 4 == 0 && reinterpret_cast<uintptr_t>(pw) % 16 == 0 &&
                       reinterpret_cast<uintptr_t>(grad_weight) % (4 * sizeof(T)) == 0;
       const int64_t items = (v4 ? total_w / 4 : total_w) + 3 * KKc * c;
+      if (defer) {
+        *defer = WReduce{pw, pb, grad_weight, grad_bias, (uint32_t)c, (uint32_t)KKc, g.splits,
+                         v4 ? 1 : 0, (int)items};
+        return 0;
+      }
       if (v4)
         hipLaunchKernelGGL((gen_bwd_w_reduce_kernel<T, 4>),
                            dim3((unsigned)((items + kWgRedThreads - 1) / kWgRedThreads)),
@@ -1098,10 +1066,12 @@ extern "C" int ddpm_gen_bwd(const void* x, const void* y, const void* weight, co
   st = bx_run(y, weight, bias, grad_out, grad_x, workspace_x, workspace_x_bytes, n, c, h, w,
               kernel_size, d0, d1, d2, dtype, stream, &fin);
   if (st != kOk || fin.part == nullptr) return st;
-  // dW and dW's split reduction; its helpers pack dY's weight and finish dX
+  // dW; its helpers pack dY's weight and finish dX; the dY kernel's
+  // workgroups then run dW's split reduction
+  WReduce red{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
   st = bw_run(x, y, grad_out, grad_weight, grad_bias, workspace_w, workspace_w_bytes, n, c, h, w,
-              kernel_size, d0, d1, d2, dtype, stream, false, &fin, &yp);
+              kernel_size, d0, d1, d2, dtype, stream, false, &fin, &yp, &red);
   if (st != kOk) return st;
   return yt_run(x, weight, grad_out, grad_y, workspace_y, workspace_y_bytes, n, c, h, w,
-                kernel_size, d0, d1, d2, dtype, stream, kYtMain, nullptr);
+                kernel_size, d0, d1, d2, dtype, stream, kYtMain, nullptr, &red);
 }

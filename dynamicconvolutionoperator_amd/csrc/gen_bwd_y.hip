@@ -88,7 +88,8 @@ template <typename T, int KS, int MB, int CH, bool AL = false>
 __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restrict__ x,
                                                                const uint32_t* __restrict__ pk,
                                                                const T* __restrict__ gout,
-                                                               T* __restrict__ gy, YGeom g) {
+                                                               T* __restrict__ gy, YGeom g,
+                                                               WReduce red) {
   typedef Mma<T> M;
   typedef typename M::V V;
   typedef YtLds<T, KS, MB, CH> L;
@@ -260,6 +261,19 @@ __global__ __launch_bounds__(kYtThreads) void gen_bwd_y_kernel(const T* __restri
 
   stage(0, 0);
   load_g(0, gv);
+  if (red.items > 0) {
+    // ddpm_gen_bwd: this workgroup's share of the weight gradient's split
+    // reduction (the partial kernel ran before this launch), its loads in
+    // flight together with the first stage's copies
+    const int per = (red.items + (int)gridDim.x - 1) / (int)gridDim.x;
+    for (int j = tid; j < per; j += kYtThreads) {
+      const uint32_t item = (uint32_t)((int)blockIdx.x * per + j);
+      if (red.v4)
+        wg_reduce_item<T, 4>(red.pw, red.pb, (T*)red.dw, (T*)red.db, red.C, red.KK, red.splits, item);
+      else
+        wg_reduce_item<T, 1>(red.pw, red.pb, (T*)red.dw, (T*)red.db, red.C, red.KK, red.splits, item);
+    }
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int s = 0; s < nstage; ++s) {
@@ -407,7 +421,7 @@ int yt_check(const void* x, const void* weight, const void* grad_out, void* grad
 // already validated by yt_check; `packed` holds yt_pack_bytes bytes).
 int yt_launch(const void* x, const void* weight, const void* grad_out, void* grad_y, void* packed,
               int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size, const GenGeom& gg,
-              int dtype, hipStream_t stream, bool pack = true);
+              int dtype, hipStream_t stream, bool pack = true, const WReduce* red = nullptr);
 
 }  // namespace
 
@@ -459,7 +473,7 @@ extern "C" int64_t ddpm_gen_bwd_y_workspace_bytes(int64_t c, int kernel_size) {
 int ddpm::yt_run(const void* x, const void* weight, const void* grad_out, void* grad_y,
                  void* workspace, int64_t workspace_bytes, int64_t n, int64_t c, int64_t h,
                  int64_t w, int kernel_size, int d0, int d1, int d2, int dtype, hipStream_t stream,
-                 int mode, YPack* pack) {
+                 int mode, YPack* pack, const WReduce* red) {
   GenGeom gg;
   bool empty;
   const int st =
@@ -478,7 +492,7 @@ int ddpm::yt_run(const void* x, const void* weight, const void* grad_out, void* 
     return kOk;
   }
   return yt_launch(x, weight, grad_out, grad_y, workspace, n, c, h, w, kernel_size, gg, dtype,
-                   stream, mode != kYtMain);
+                   stream, mode != kYtMain, red);
 }
 
 int ddpm::yt_pack(const YPack& p, int kernel_size, int dtype, hipStream_t stream) {
@@ -531,7 +545,7 @@ namespace {
 
 int yt_launch(const void* x, const void* weight, const void* grad_out, void* grad_y, void* packed,
               int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size, const GenGeom& gg,
-              int dtype, hipStream_t stream, bool pack) {
+              int dtype, hipStream_t stream, bool pack, const WReduce* red) {
   void* workspace = packed;
   YGeom g;
   g.N = (int)n;
@@ -569,8 +583,10 @@ int yt_launch(const void* x, const void* weight, const void* grad_out, void* gra
                                         : gen_bwd_y_kernel<T, KS, MB, CH>;
         const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
         if (ae != 0) return ae;
+        const WReduce nored{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
         hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(kYtThreads), lds, stream, (const T*)x,
-                           (const uint32_t*)workspace, (const T*)grad_out, (T*)grad_y, g);
+                           (const uint32_t*)workspace, (const T*)grad_out, (T*)grad_y, g,
+                           red ? *red : nored);
         return (int)hipGetLastError();
       };
       auto by_ch = [&](auto ks) {
