@@ -50,6 +50,7 @@ SIGNATURES: dict[str, tuple[list, type]] = {
     "ddpm_fuse_conv_bwd_data": ([_P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _P], _I),
     "ddpm_fuse_conv_bwd_weight_workspace_bytes": ([_L, _L, _L, _L, _I], _L),
     "ddpm_fuse_conv_bwd_weight": ([_P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _P], _I),
+    "ddpm_fuse_conv_bwd": ([_P, _P, _P, _P, _P, _P, _P, _L, _P, _L, _L, _L, _L, _L, _I, _P], _I),
     "ddpm_gen_bwd_w": ([_P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
     "ddpm_gen_bwd_xw": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _P, _L, _L, _L, _L, _L, _I, _I, _I,
                          _I, _I, _P], _I),
@@ -58,7 +59,7 @@ SIGNATURES: dict[str, tuple[list, type]] = {
 }
 
 
-ABI_VERSION = 6  # include/ddpm_hip.h
+ABI_VERSION = 7  # include/ddpm_hip.h
 
 
 class HipLibraryError(RuntimeError):

@@ -28,7 +28,7 @@ int allow_dynamic_lds(const void* fn, size_t bytes) {
 
 using namespace ddpm;
 
-extern "C" int ddpm_abi_version(void) { return 6; }
+extern "C" int ddpm_abi_version(void) { return 7; }
 
 extern "C" const char* ddpm_status_string(int code) {
   switch (code) {

@@ -40,7 +40,7 @@
 //   * v_mfma_f32_16x16x32_{bf16,f16}; fp32 operands run as three bf16
 //     products (hi*hi + hi*lo + lo*hi), accumulation in fp32.
 
-#include "gen_common.h"
+#include "conv3x3.h"
 
 #include <type_traits>
 
@@ -53,69 +53,14 @@ constexpr int kCvPad = 8;                  // staged column halo (one chunk of 2
 constexpr int kCvMaxMB = 4;                // 16-plane blocks of m per workgroup, at most
 constexpr int kCvFillWGs = 256;            // workgroups to aim for (the CU count of an MI355X)
 
-struct ConvGeom {
-  int N, K, M, H, W;  // K input planes, M output planes
-  int rs, sw;         // segment rows and columns (rs * sw = kCvPix)
-  int tiles_h, tiles_w;
-  int nc32;           // ceil(K / 32)
-  int mb;             // 16-plane blocks of m per workgroup
-  int mgroups;        // ceil(M / (mb * 16))
-  int mgl;            // m groups a workgroup runs one after another (divides mgroups)
-  int ks;             // splits of the input planes (K): 1, or more for small images
-  int cc_per;         // 32-plane chunks per K split
-  int seg;            // staged elements per segment row (sw + 2 * kCvPad)
-  int x4;             // input rows copied in 16-byte lanes (W % 8 == 0, aligned base)
-};
-
-template <typename T>
-__host__ __device__ constexpr int cv_parts() {
-  return sizeof(T) == 4 ? 2 : 1;
-}
-
-// Packed A: 16-byte units [mg][cc][ki][kj][ib][part][lane] (ib < g.mb), lane
-// (m = (mg*mb + ib)*16 + (lane & 15), q = lane >> 4) holding
-// A[m][cc*32 + 4e + q][ki][kj], e = 0..7 (`nat`: A[m][cc*32 + 8q + e][ki][kj],
-// the slot order of the transposing B reads).  `rot` selects the
-// input-gradient form (transposed, rotated).
+// The weight packing as its own kernel (cv_pack_item per thread).
 template <typename T, int MB>
 __global__ __launch_bounds__(256) void conv3x3_pack_kernel(const T* __restrict__ wt,
                                                            uint32_t* __restrict__ pk, ConvGeom g,
                                                            int rot, int pairs, int nat) {
-  constexpr int P = cv_parts<T>();
-  // 32-bit indices: the host bounds the packed units below 2^31
   const int total = g.mgroups * g.nc32 * 9 * MB * 64;
   const int idx = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-  if (idx >= total) return;
-  const int lane = idx & 63;
-  int rest = idx >> 6;
-  const int ib = rest % MB;
-  rest /= MB;
-  const int tap = rest % 9;
-  rest /= 9;
-  const int cc = rest % g.nc32;
-  const int mg = rest / g.nc32;
-  const int ki = tap / 3, kj = tap - 3 * ki;
-  const int m = (mg * MB + ib) * 16 + (lane & 15), q = lane >> 4;
-  float v[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    // pair planes (kF32Pairs input): slot 8q + e holds channel 2(q + 4(e/2)) + e%2
-    const int k = cc * 32 + (pairs ? 2 * q + 8 * (e >> 1) + (e & 1) : nat ? 8 * q + e : 4 * e + q);
-    float a = 0.f;
-    if (m < g.M && k < g.K) {
-      // forward: weight[m][k][ki][kj]; input gradient: weight[k][m][2-ki][2-kj]
-      const int64_t off = rot ? (((int64_t)k * g.M + m) * 3 + (2 - ki)) * 3 + (2 - kj)
-                              : (((int64_t)m * g.K + k) * 3 + ki) * 3 + kj;
-      a = to_f(wt[off]);
-    }
-    v[e] = a;
-  }
-  typename Mma<T>::V o[P];
-  Mma<T>::pack(v, o);
-  u32x4* __restrict__ dst = reinterpret_cast<u32x4*>(pk);
-  const int64_t unit = (((((int64_t)mg * g.nc32 + cc) * 9 + tap) * MB + ib) * P) * 64 + lane;
-#pragma unroll
-  for (int part = 0; part < P; ++part) dst[unit + part * 64] = __builtin_bit_cast(u32x4, o[part]);
+  if (idx < total) cv_pack_item<T, MB>(wt, pk, g, rot, pairs, nat, idx);
 }
 
 // One LDS staging buffer (dwords): input rows [CH * 32 planes][kXS] -- a
@@ -191,7 +136,8 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
                                                              const uint32_t* __restrict__ pk,
                                                              const T* __restrict__ bias,
                                                              T* __restrict__ out,
-                                                             float* __restrict__ part, ConvGeom g) {
+                                                             float* __restrict__ part, ConvGeom g,
+                                                             CwReduce red) {
   typedef Mma<T> M;
   typedef typename M::V V;
   typedef CvLds<T, MB, WIDE, CH> L;
@@ -380,6 +326,10 @@ __global__ __launch_bounds__(kCvThreads) void conv3x3_kernel(const T* __restrict
     }
   }
   if (nstage > 0) stage(0, 0);
+  // ddpm_fuse_conv_bwd (input gradient): this workgroup's share of the
+  // weight gradient's split reduction, its loads in flight together with the
+  // first stage's copies
+  if (red.items > 0) cw_reduce_share<T>(red, (int)blockIdx.x, (int)gridDim.x, tid, kCvThreads);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int s = 0; s < nstage; ++s) {
@@ -611,47 +561,66 @@ int64_t cv_workspace_bytes(const ConvGeom& g, int dtype) {
   return cv_align(pk) + (int64_t)g.ks * g.N * g.M * g.H * g.W * (int64_t)sizeof(float);
 }
 
+// Launch plan of one direction: the geometry, the aligned layout (256-column
+// segments on whole image rows, 16-byte rows, whole 32-plane chunks in every
+// K split) and, with 2-byte types and four m blocks, the natural slot order of
+// the transposing B reads; several m groups per workgroup only for the fp32
+// input gradient's aligned layout (plain concat layout, no bias).
+struct CvPlan {
+  ConvGeom g;
+  bool al, nat;
+};
+void cv_plan(CvPlan& p, const void* in, int64_t n, int64_t k, int64_t m, int64_t h, int64_t w,
+             int dtype, bool pairs, bool bias) {
+  const int esz = dtype == kF32 ? 4 : 2;
+  ConvGeom& g = p.g;
+  cv_geom(g, n, k, m, h, w, esz);
+  g.x4 = (w % 8 == 0) && ((uintptr_t)in % 16 == 0);
+  p.al = g.rs == 1 && g.sw == kCvPix && w % kCvPix == 0 && g.x4 && k % 32 == 0 &&
+         g.nc32 % g.cc_per == 0;
+  p.nat = esz == 2 && p.al && g.mb == 4;
+  if (!(esz == 4 && p.al && g.mb == 4 && !pairs && !bias)) g.mgl = 1;
+}
+
+// red (optional): a weight-gradient split reduction for the kernel's
+// workgroups to run.  pack false: `workspace` already holds the packed weight.
 int cv_run(const void* in, const void* wt, const void* bias, void* out, void* workspace,
            int64_t workspace_bytes, int64_t n, int64_t k, int64_t m, int64_t h, int64_t w, int rot,
-           int dtype, hipStream_t stream, bool pairs = false) {
-  const int esz = dtype == kF32 ? 4 : 2;
-  ConvGeom g;
-  cv_geom(g, n, k, m, h, w, esz);
+           int dtype, hipStream_t stream, bool pairs = false, const CwReduce* red = nullptr,
+           bool pack = true) {
+  CvPlan plan;
+  cv_plan(plan, in, n, k, m, h, w, dtype, pairs, bias != nullptr);
+  ConvGeom& g = plan.g;
   const int64_t need = cv_workspace_bytes(g, dtype);
   if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 16 != 0)
     return kWorkspaceTooSmall;
   float* part = g.ks > 1 ? (float*)((char*)workspace + cv_align(cv_pack_bytes(g, dtype))) : nullptr;
-  g.x4 = (w % 8 == 0) && ((uintptr_t)in % 16 == 0);
+  const CwReduce nored{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
+  const CwReduce& rd = red ? *red : nored;
   return cv_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
-    // aligned layout: 256-column segments on whole image rows, 16-byte rows,
-    // whole 32-plane chunks in every K split; with 2-byte types and four m
-    // blocks its B operands come from transposing reads in natural slot order
-    const bool al = g.rs == 1 && g.sw == kCvPix && w % kCvPix == 0 && g.x4 && k % 32 == 0 &&
-                    g.nc32 % g.cc_per == 0;
-    const bool nat = sizeof(T) == 2 && al && g.mb == 4;
-    // several m groups per workgroup: the fp32 input gradient's aligned
-    // layout only (plain concat layout, no bias)
-    if (!(sizeof(T) == 4 && al && g.mb == 4 && !pairs && !bias)) g.mgl = 1;
+    const bool al = plan.al, nat = plan.nat;
     const int64_t units = (int64_t)g.mgroups * g.nc32 * 9 * g.mb * 64;
     const dim3 pgrid((unsigned)((units + 255) / 256));
-    if (g.mb == 4)
-      hipLaunchKernelGGL((conv3x3_pack_kernel<T, 4>), pgrid, dim3(256), 0, stream, (const T*)wt,
-                         (uint32_t*)workspace, g, rot, (int)pairs, (int)nat);
-    else if (g.mb == 2)
-      hipLaunchKernelGGL((conv3x3_pack_kernel<T, 2>), pgrid, dim3(256), 0, stream, (const T*)wt,
-                         (uint32_t*)workspace, g, rot, (int)pairs, (int)nat);
-    else
-      hipLaunchKernelGGL((conv3x3_pack_kernel<T, 1>), pgrid, dim3(256), 0, stream, (const T*)wt,
-                         (uint32_t*)workspace, g, rot, (int)pairs, (int)nat);
-    int e = (int)hipGetLastError();
-    if (e != 0) return e;
+    if (pack) {
+      if (g.mb == 4)
+        hipLaunchKernelGGL((conv3x3_pack_kernel<T, 4>), pgrid, dim3(256), 0, stream, (const T*)wt,
+                           (uint32_t*)workspace, g, rot, (int)pairs, (int)nat);
+      else if (g.mb == 2)
+        hipLaunchKernelGGL((conv3x3_pack_kernel<T, 2>), pgrid, dim3(256), 0, stream, (const T*)wt,
+                           (uint32_t*)workspace, g, rot, (int)pairs, (int)nat);
+      else
+        hipLaunchKernelGGL((conv3x3_pack_kernel<T, 1>), pgrid, dim3(256), 0, stream, (const T*)wt,
+                           (uint32_t*)workspace, g, rot, (int)pairs, (int)nat);
+      const int e = (int)hipGetLastError();
+      if (e != 0) return e;
+    }
     const dim3 grid((unsigned)((int64_t)n * g.tiles_h * g.tiles_w * (g.mgroups / g.mgl) * g.ks));
     auto launch = [&](auto kern, size_t lds) {
       const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
       if (ae != 0) return ae;
       hipLaunchKernelGGL(kern, grid, dim3(kCvThreads), lds, stream, (const T*)in,
-                         (const uint32_t*)workspace, (const T*)bias, (T*)out, part, g);
+                         (const uint32_t*)workspace, (const T*)bias, (T*)out, part, g, rd);
       int e2 = (int)hipGetLastError();
       if (e2 != 0 || g.ks <= 1) return e2;
       // the K splits' partial sums (and the bias) in split order
@@ -762,4 +731,40 @@ extern "C" int ddpm_fuse_conv_bwd_data(const void* grad_out, const void* weight,
   if (!grad_out || !weight || !grad_cat) return kBadArgument;
   return cv_run(grad_out, weight, nullptr, grad_cat, workspace, workspace_bytes, n, c, 4 * c, h, w,
                 1, dtype, stream);
+}
+
+extern "C" int ddpm_fuse_conv_bwd(const void* cat, const void* weight, const void* grad_out,
+                                  void* grad_cat, void* grad_weight, void* grad_bias,
+                                  void* workspace_data, int64_t workspace_data_bytes,
+                                  void* workspace_weight, int64_t workspace_weight_bytes, int64_t n,
+                                  int64_t c, int64_t h, int64_t w, int dtype, hipStream_t stream) {
+  // `dtype` is the concat's code (kF32Pairs: pair planes, read by the weight
+  // gradient only); grad_out, weight and grad_cat are plain
+  const int ddt = dtype == kF32Pairs ? kF32 : dtype;
+  int st = cv_check(n, c, 4 * c, h, w, ddt);
+  if (st != kOk) return st;
+  // the weight-gradient part is validated first: nothing is launched when
+  // either part would fail
+  st = cw_run(cat, grad_out, grad_weight, grad_bias, workspace_weight, workspace_weight_bytes, n, c,
+              h, w, dtype, stream, true, nullptr, nullptr);
+  if (st != kOk) return st;
+  if (n == 0 || c == 0 || h == 0 || w == 0)  // zero weight gradients; grad_cat is empty
+    return cw_run(cat, grad_out, grad_weight, grad_bias, workspace_weight, workspace_weight_bytes,
+                  n, c, h, w, dtype, stream, false, nullptr, nullptr);
+  if (!grad_out || !weight || !grad_cat) return kBadArgument;
+  CvPlan plan;
+  cv_plan(plan, grad_out, n, c, 4 * c, h, w, ddt, false, false);
+  const int64_t need = cv_workspace_bytes(plan.g, ddt);
+  if (!workspace_data || workspace_data_bytes < need || (uintptr_t)workspace_data % 16 != 0)
+    return kWorkspaceTooSmall;
+  // the weight-gradient launch packs the input gradient's weight; the input
+  // gradient's launch sums the weight gradient's split partials
+  const CvPack pack{weight, (uint32_t*)workspace_data, plan.g, 1, 0, plan.nat ? 1 : 0,
+                    plan.g.mgroups * plan.g.nc32 * 9 * plan.g.mb * 64};
+  CwReduce red{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
+  st = cw_run(cat, grad_out, grad_weight, grad_bias, workspace_weight, workspace_weight_bytes, n, c,
+              h, w, dtype, stream, false, &pack, &red);
+  if (st != kOk) return st;
+  return cv_run(grad_out, weight, nullptr, grad_cat, workspace_data, workspace_data_bytes, n, c,
+                4 * c, h, w, 1, ddt, stream, false, &red, false);
 }

@@ -30,7 +30,7 @@
 //     16-plane block of grad_out with one more MFMA per step and part (a
 //     fragment of ones times grad_out).
 
-#include "gen_common.h"
+#include "conv3x3.h"
 
 #include <type_traits>
 
@@ -41,7 +41,6 @@ constexpr int kCwTW = 32 * kCwSegs;         // columns per step
 constexpr int kCwPad = 8;                   // staged column halo (16 bytes of 2-byte values)
 constexpr int kCwNW = 3 * kCwSegs;          // waves: segments x kernel rows
 constexpr int kCwThreads = 64 * kCwNW;
-constexpr int kCwMaxSplits = 16;
 constexpr int kCwMinSteps = 4;
 
 struct CwGeom {
@@ -125,7 +124,8 @@ struct CwPos {
 template <typename T, int MB, bool PP = false, int SJ = 1, bool AL = false>
 __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
     const T* __restrict__ cat, const T* __restrict__ gout, float* __restrict__ pw,
-    float* __restrict__ pb, T* __restrict__ dw_out, T* __restrict__ db_out, CwGeom g) {
+    float* __restrict__ pb, T* __restrict__ dw_out, T* __restrict__ db_out, CwGeom g,
+    CvPack pack) {
   typedef Mma<T> M;
   typedef typename M::V V;
   typedef typename M::E ME;
@@ -394,6 +394,9 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
     nxt.advance(g);
     ystore(0);
   }
+  // ddpm_fuse_conv_bwd: this workgroup's share of the input gradient's
+  // weight packing, before the first step's copies are waited for
+  if (pack.total > 0) cv_pack_share<T>(pack, (int)blockIdx.x, (int)gridDim.x, tid, kCwThreads);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   const int wl = 32 * sg + 8 * quad;  // this lane's first token within a 128-column subsegment
@@ -506,35 +509,22 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
   }
   if (do_bias && quad == 0) rb[sg * 16 + col16] = accb[0];  // row 0 of D: the column sums
   __syncthreads();
-  // rows (tap t, ci = cb*16 + c), columns co; partial [split][9][CI][C], or
-  // grad_weight[co][ci][t] directly
+  // rows (tap t, ci = cb*16 + c), columns co; written in grad_weight's
+  // [co][ci][t] order (runs of 16 ci x 9 taps per co): grad_weight directly,
+  // or the split's partial [split][C][CI][9]
   float* __restrict__ pwb = pw + (int64_t)split * 9 * CI * C;
-  const bool v4 = C % 4 == 0 && reinterpret_cast<uintptr_t>(pw) % 16 == 0;
-  for (int idx = tid; idx < 9 * 16 * NO / 4; idx += kCwThreads) {
-    const int q = 4 * idx;
-    const int t = q / (16 * NO);
-    const int rem2 = q - t * 16 * NO;
-    const int c = rem2 / NO, i = rem2 - c * NO;
+  for (int idx = tid; idx < NO * 16 * 9; idx += kCwThreads) {
+    const int i = idx / (16 * 9), r = idx - i * (16 * 9);
+    const int c = r / 9, t = r - c * 9;
     const int ci = cb * 16 + c;
     if (ci >= CI || co0 + i >= C) continue;
     const float* __restrict__ sp = red + (t * 16 + c) * RS + i;
-    float v[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = ((sp[e] + sp[SL + e]) + sp[2 * SL + e]) + sp[3 * SL + e];
-    if (g.direct) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (co0 + i + e < C) dw_out[((int64_t)(co0 + i + e) * CI + ci) * 9 + t] = from_f<T>(v[e]);
-    } else {
-      float* __restrict__ dst = pwb + ((int64_t)t * CI + ci) * C + co0 + i;
-      if (v4) {
-        *reinterpret_cast<f32x4*>(dst) = (f32x4){v[0], v[1], v[2], v[3]};
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (co0 + i + e < C) dst[e] = v[e];
-      }
-    }
+    const float v = ((sp[0] + sp[SL]) + sp[2 * SL]) + sp[3 * SL];
+    const int64_t o = ((int64_t)(co0 + i) * CI + ci) * 9 + t;
+    if (g.direct)
+      dw_out[o] = from_f<T>(v);
+    else
+      pwb[o] = v;
   }
   if (bias_wg && tid < 16) {
     const int co = cb * 16 + tid;
@@ -548,64 +538,16 @@ __global__ __launch_bounds__(kCwThreads) void conv_wgrad_partial_kernel(
   }
 }
 
-// Fixed-order sum of the split partials [split][9][CI][C] into
-// grad_weight[co][ci][t] and grad_bias[co].  A workgroup sums a tile of
-// kCrCI ci x 9 taps x kCrCO co -- reading runs of kCrCO co of each (tap, ci)
-// row, the split stride apart -- and writes it through LDS as kCrCO runs of
-// kCrCI * 9 consecutive elements (one co's ci x taps), so reads and writes
-// are both coalesced; the workgroups after the tiles sum the bias partials.
-constexpr int kCrCI = 4;
-constexpr int kCrCO = 16;
-template <typename T>
+// Fixed-order sum of the split partials (cw_reduce_item), one item per
+// thread.
+template <typename T, int V>
 __global__ __launch_bounds__(256) void conv_wgrad_reduce_kernel(const float* __restrict__ pw,
                                                                 const float* __restrict__ pb,
                                                                 T* __restrict__ dw_out,
-                                                                T* __restrict__ db_out, int C,
-                                                                int CI, int splits, int tiles) {
-  constexpr int RL = kCrCI * 9;  // one co's run of (ci, t) outputs
-  __shared__ float tile[kCrCO][RL + 1];
-  const int bid = (int)blockIdx.x;
-  if (bid >= tiles) {
-    const int co = (bid - tiles) * 256 + (int)threadIdx.x;
-    if (co < C) {
-      float v = 0.f;
-      for (int s = 0; s < splits; ++s) v += pb[(int64_t)s * C + co];
-      db_out[co] = from_f<T>(v);
-    }
-    return;
-  }
-  const int cib = (CI + kCrCI - 1) / kCrCI;
-  const int cob = bid / cib;
-  const int ci0 = (bid - cob * cib) * kCrCI, co0 = cob * kCrCO;
-  const int64_t per = (int64_t)9 * CI * C;
-  for (int idx = (int)threadIdx.x; idx < RL * kCrCO; idx += 256) {
-    const int col = idx % kCrCO, r = idx / kCrCO;  // r = t * kCrCI + ci - ci0
-    const int t = r / kCrCI, cil = r - t * kCrCI;
-    const int ci = ci0 + cil, co = co0 + col;
-    float v = 0.f;
-    if (ci < CI && co < C) {
-      const float* __restrict__ src = pw + ((int64_t)t * CI + ci) * C + co;
-      if (splits == kCwMaxSplits) {
-        // every load in flight before the first add
-        float a[kCwMaxSplits];
-#pragma unroll
-        for (int s = 0; s < kCwMaxSplits; ++s) a[s] = src[(int64_t)s * per];
-#pragma unroll
-        for (int s = 0; s < kCwMaxSplits; ++s) v += a[s];
-      } else {
-#pragma unroll 4
-        for (int s = 0; s < splits; ++s) v += src[(int64_t)s * per];
-      }
-    }
-    tile[col][cil * 9 + t] = v;
-  }
-  __syncthreads();
-  for (int idx = (int)threadIdx.x; idx < RL * kCrCO; idx += 256) {
-    const int col = idx / RL, r = idx - col * RL;
-    const int co = co0 + col;
-    if (co < C && ci0 + r / 9 < CI)
-      dw_out[((int64_t)co * CI + ci0) * 9 + r] = from_f<T>(tile[col][r]);
-  }
+                                                                T* __restrict__ db_out, uint32_t nw,
+                                                                uint32_t C, int splits) {
+  const uint32_t item = blockIdx.x * 256u + threadIdx.x;
+  cw_reduce_item<T, V>(pw, pb, dw_out, db_out, nw, C, splits, item);
 }
 
 // Zero fill (a kernel rather than a memset, so the call stays valid under
@@ -696,10 +638,10 @@ extern "C" int64_t ddpm_fuse_conv_bwd_weight_workspace_bytes(int64_t n, int64_t 
   return cw_partial_bytes(g);
 }
 
-extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, void* grad_weight,
-                                         void* grad_bias, void* workspace, int64_t workspace_bytes,
-                                         int64_t n, int64_t c, int64_t h, int64_t w, int dtype,
-                                         hipStream_t stream) {
+int ddpm::cw_run(const void* cat, const void* grad_out, void* grad_weight, void* grad_bias,
+                 void* workspace, int64_t workspace_bytes, int64_t n, int64_t c, int64_t h,
+                 int64_t w, int dtype, hipStream_t stream, bool check_only, const CvPack* pack,
+                 CwReduce* defer) {
   // kF32Pairs: `cat` in pair planes (whole 32-plane chunks: C % 8 == 0)
   const bool pp = dtype == kF32Pairs;
   if (pp) {
@@ -713,6 +655,7 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
   if (!grad_weight || !grad_bias) return kBadArgument;
   const int esz = dtype == kF32 ? 4 : 2;
   if (n == 0 || h == 0 || w == 0) {
+    if (check_only) return kOk;
     // an empty batch: zero gradients
     return cw_with_type(dtype, [&](auto tag) {
       using T = decltype(tag);
@@ -732,12 +675,14 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
   cw_geom(g, n, c, h, w, pp ? kCwTW : cw_step_cols(w, esz));
   const int64_t need = cw_partial_bytes(g);
   if (need > 0 && (!workspace || workspace_bytes < need)) return kWorkspaceTooSmall;
+  if (check_only) return kOk;
   g.x16 = (w % (16 / esz) == 0) && ((uintptr_t)cat % 16 == 0);
   g.g16 = (w % 8 == 0) && ((uintptr_t)grad_out % 16 == 0);
   g.y4 = (w % 4 == 0) && ((uintptr_t)grad_out % 16 == 0);
   float* pw = g.direct ? nullptr : (float*)workspace;
   float* pb = g.direct ? nullptr : pw + (int64_t)g.splits * 9 * 4 * c * c;
   const int mb = c > 64 ? 4 : (int)((c + 15) / 16);  // 16-plane blocks of co per workgroup
+  const CvPack nopack{nullptr, nullptr, ConvGeom{}, 0, 0, 0, 0};
   return cw_with_type(dtype, [&](auto tag) {
     using T = decltype(tag);
     auto launch = [&](auto mbc, auto sjc) {
@@ -758,13 +703,29 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
       const int ae = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
       if (ae != 0) return ae;
       hipLaunchKernelGGL(kern, dim3((unsigned)(g.splits * g.cblocks * g.ohalves)), dim3(kCwThreads), lds, stream,
-                         (const T*)cat, (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g);
+                         (const T*)cat, (const T*)grad_out, pw, pb, (T*)grad_weight, (T*)grad_bias, g,
+                         pack ? *pack : nopack);
       int e = (int)hipGetLastError();
       if (e != 0 || g.direct) return e;
-      const int tiles = (int)(((4 * c + kCrCI - 1) / kCrCI) * ((c + kCrCO - 1) / kCrCO));
-      hipLaunchKernelGGL((conv_wgrad_reduce_kernel<T>), dim3((unsigned)(tiles + (c + 255) / 256)),
-                         dim3(256), 0, stream, (const float*)pw, (const float*)pb, (T*)grad_weight,
-                         (T*)grad_bias, (int)c, (int)(4 * c), g.splits, tiles);
+      // four elements per item where the partials and grad_weight allow
+      // 16-byte loads and 4-element stores (36 C^2 is a multiple of 4)
+      const uint32_t nw = (uint32_t)(36 * c * c);
+      const bool v4 = (uintptr_t)pw % 16 == 0 && (uintptr_t)grad_weight % (4 * sizeof(T)) == 0;
+      const int items = (int)((v4 ? nw / 4 : nw) + c);
+      if (defer) {
+        *defer = CwReduce{pw, pb, grad_weight, grad_bias, nw, (uint32_t)c, g.splits, v4 ? 1 : 0,
+                          items};
+        return 0;
+      }
+      const dim3 rgrid((unsigned)((items + 255) / 256));
+      if (v4)
+        hipLaunchKernelGGL((conv_wgrad_reduce_kernel<T, 4>), rgrid, dim3(256), 0, stream,
+                           (const float*)pw, (const float*)pb, (T*)grad_weight, (T*)grad_bias, nw,
+                           (uint32_t)c, g.splits);
+      else
+        hipLaunchKernelGGL((conv_wgrad_reduce_kernel<T, 1>), rgrid, dim3(256), 0, stream,
+                           (const float*)pw, (const float*)pb, (T*)grad_weight, (T*)grad_bias, nw,
+                           (uint32_t)c, g.splits);
       return (int)hipGetLastError();
     };
     return cw_with_mb(mb, [&](auto mbc) {
@@ -774,4 +735,12 @@ extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, 
       return launch(mbc, std::integral_constant<int, 1>());
     });
   });
+}
+
+extern "C" int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, void* grad_weight,
+                                         void* grad_bias, void* workspace, int64_t workspace_bytes,
+                                         int64_t n, int64_t c, int64_t h, int64_t w, int dtype,
+                                         hipStream_t stream) {
+  return cw_run(cat, grad_out, grad_weight, grad_bias, workspace, workspace_bytes, n, c, h, w,
+                dtype, stream, false, nullptr, nullptr);
 }

@@ -550,10 +550,26 @@ def _fuse_conv_backward(cat, weight, has_bias, grad_out, needs, cat_code):
     lib = _lib.load()
     need_w = needs[1]
     need_b = has_bias and needs[2]
-    # one workspace serves both calls (they run in order on one stream)
     data_bytes = _ws_bytes("ddpm_fuse_conv_workspace_bytes", n, c, h, w, dt) if needs[0] else 0
     weight_bytes = (_ws_bytes("ddpm_fuse_conv_bwd_weight_workspace_bytes", n, c, h, w, cat_code)
                     if need_w or need_b else 0)
+    if needs[0] and (need_w or need_b):
+        # all gradients in one call (two launches); its two workspaces live at once
+        off = _align256(data_bytes)
+        ws = torch.empty(max(off + weight_bytes, 16), dtype=torch.uint8, device=cat.device)
+        grad_cat = torch.empty((n, ci, h, w), dtype=weight.dtype, device=cat.device)
+        gw = torch.empty_like(weight)
+        gb = torch.empty((c,), dtype=weight.dtype, device=cat.device)
+        with _on(cat.device):
+            code = lib.ddpm_fuse_conv_bwd(_ptr(cat), _ptr(weight), _ptr(grad_out), _ptr(grad_cat),
+                                          _ptr(gw), _ptr(gb), _ptr(ws), data_bytes,
+                                          _ptr(ws) + off, weight_bytes, n, c, h, w, cat_code,
+                                          _stream(cat))
+        if code != _lib.STATUS_UNSUPPORTED:
+            _lib.check(code, "ddpm_fuse_conv_bwd")
+            return grad_cat, gw if need_w else None, gb if need_b else None
+        grad_cat = None  # a part the combined call does not take: the two calls below
+    # one workspace serves both calls (they run in order on one stream)
     ws = torch.empty(max(data_bytes, weight_bytes, 16), dtype=torch.uint8, device=cat.device)
     if needs[0]:
         grad_cat = torch.empty((n, ci, h, w), dtype=weight.dtype, device=cat.device)

@@ -47,7 +47,7 @@ extern "C" {
 #define DDPM_DTYPE_F16 2
 
 /* ABI version of this header (5: dtype code 3; 6: ddpm_gen_fwd at K = 5 and
- * ddpm_gen_fwd_supported). */
+ * ddpm_gen_fwd_supported; 7: ddpm_fuse_conv_bwd). */
 int ddpm_abi_version(void);
 
 /* Text for any status code returned by this library (static storage). */
@@ -299,6 +299,25 @@ int64_t ddpm_fuse_conv_bwd_weight_workspace_bytes(int64_t n, int64_t c, int64_t 
 int ddpm_fuse_conv_bwd_weight(const void* cat, const void* grad_out, void* grad_weight,
                               void* grad_bias, void* workspace, int64_t workspace_bytes, int64_t n,
                               int64_t c, int64_t h, int64_t w, int dtype, hipStream_t stream);
+
+/* Input, weight and bias gradients of the fuse convolution in one call
+ * (ddpm_fuse_conv_bwd_weight, then ddpm_fuse_conv_bwd_data), bit-identical to
+ * the two calls in two launches instead of four: the weight-gradient launch's
+ * workgroups also pack the input gradient's weight, and the input-gradient
+ * launch's workgroups also sum the weight gradient's split partials.
+ * `dtype` is the concat's code (3: pair planes; grad_out, weight and grad_cat
+ * are then plain fp32).  workspace_data as for ddpm_fuse_conv_bwd_data
+ * (ddpm_fuse_conv_workspace_bytes), workspace_weight as for
+ * ddpm_fuse_conv_bwd_weight; both live at once.  Both parts are validated
+ * before anything is launched.
+ * Replaces the cuDNN backward-data and backward-filter convolutions of
+ * self.fuse (autograd of nn.Conv2d, triton_impl.py:294, 392) when all
+ * gradients are needed. */
+int ddpm_fuse_conv_bwd(const void* cat, const void* weight, const void* grad_out, void* grad_cat,
+                       void* grad_weight, void* grad_bias, void* workspace_data,
+                       int64_t workspace_data_bytes, void* workspace_weight,
+                       int64_t workspace_weight_bytes, int64_t n, int64_t c, int64_t h, int64_t w,
+                       int dtype, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -140,3 +140,62 @@ def test_fuse_conv_split_determinism():
     o2 = ops.fuse_conv3x3(cat, wt, b)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
+
+
+def _fuse_conv_bwd_calls(cat, wt, g, code, combined):
+    """grad_cat, grad_weight, grad_bias through the C-ABI: ddpm_fuse_conv_bwd
+    (combined) or ddpm_fuse_conv_bwd_data + _bwd_weight, outputs started as
+    NaN.  `code` is the concat's dtype code (grad_out and weight plain)."""
+    import ctypes
+
+    from dynamicconvolutionoperator_amd import _lib
+
+    lib = _lib.load()
+    n, c, h, w = g.shape
+    dt = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[wt.dtype]
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    db = int(lib.ddpm_fuse_conv_workspace_bytes(n, c, h, w, dt))
+    wb = int(lib.ddpm_fuse_conv_bwd_weight_workspace_bytes(n, c, h, w, code))
+    wsd = torch.empty(max(db, 16), dtype=torch.uint8, device=DEV)
+    wsw = torch.empty(max(wb, 16), dtype=torch.uint8, device=DEV)
+    gc = torch.full((n, 4 * c, h, w), float("nan"), dtype=wt.dtype, device=DEV)
+    gw = torch.full_like(wt, float("nan"))
+    gb = torch.full((c,), float("nan"), dtype=wt.dtype, device=DEV)
+    if combined:
+        rc = lib.ddpm_fuse_conv_bwd(p(cat), p(wt), p(g), p(gc), p(gw), p(gb), p(wsd), db, p(wsw), wb,
+                                    n, c, h, w, code, s)
+        assert rc == 0, rc
+    else:
+        rc = lib.ddpm_fuse_conv_bwd_data(p(g), p(wt), p(gc), p(wsd), db, n, c, h, w, dt, s)
+        assert rc == 0, rc
+        rc = lib.ddpm_fuse_conv_bwd_weight(p(cat), p(g), p(gw), p(gb), p(wsw), wb, n, c, h, w, code, s)
+        assert rc == 0, rc
+    torch.cuda.synchronize()
+    return gc, gw, gb
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(1, 64, 256, 256), (2, 32, 64, 512), (2, 24, 15, 17), (1, 16, 12, 40),
+                                   (1, 128, 32, 64), (0, 16, 8, 8)])
+def test_fuse_conv_bwd_combined_is_the_two_calls(shape, dtype):
+    """ddpm_fuse_conv_bwd -- the weight-gradient launch packing the input
+    gradient's weight, the input-gradient launch summing the weight
+    gradient's split partials -- bit for bit the two separate calls: 16 pixel
+    splits with the fp32 m-group loop and the 2-byte transposing reads
+    (256x256), two 256-column tiles per row, element-wise rows (15x17), a
+    single split written directly (12x40), two halves of 64 output planes
+    (C = 128) and an empty batch (zero weight gradients)."""
+    say(f"fuse conv combined backward shape={shape} dtype={dtype}")
+    n, c, h, w = shape
+    seed = 940 + c + w
+    cat = randn((n, 4 * c, h, w), seed).to(dtype).to(DEV)
+    torch.manual_seed(seed + 1)
+    wt = torch.nn.Conv2d(4 * c, c, 3, 1, 1).weight.detach().to(dtype).to(DEV)
+    g = randn((n, c, h, w), seed + 2).to(dtype).to(DEV)
+    code = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[dtype]
+    sep = _fuse_conv_bwd_calls(cat, wt, g, code, False)
+    com = _fuse_conv_bwd_calls(cat, wt, g, code, True)
+    for name, a, e in zip(("d cat", "d weight", "d bias"), com, sep):
+        assert not torch.isnan(e).any(), f"{name} {shape}"
+        assert torch.equal(a, e), f"{name} {shape} {dtype}: max|diff| {(a - e).abs().max().item():.3e}"

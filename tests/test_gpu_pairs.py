@@ -217,3 +217,24 @@ def test_fused_ddpm_partial_gradients():
         got = torch.autograd.grad(out, [leaves[i] for i in want], gout)
         for i, gr in zip(want, got):
             assert torch.equal(gr, all_grads[i]), f"leaf {i}"
+
+
+@pytest.mark.parametrize("shape", [(1, 64, 256, 256), (2, 16, 20, 36), (1, 48, 15, 17)])
+def test_fuse_conv_combined_backward_reads_pair_planes(shape):
+    """ddpm_fuse_conv_bwd with a pair-plane concat (dtype 3; grad_out and
+    weight plain fp32): bit-identical to ddpm_fuse_conv_bwd_data plus
+    ddpm_fuse_conv_bwd_weight on the plain fp32 concat."""
+    from tests.test_gpu_fuse_conv import _fuse_conv_bwd_calls
+
+    say(f"fuse conv combined backward pair planes shape={shape}")
+    n, c, h, w = shape
+    seed = 1700 + c + w
+    cat = randn((n, 4 * c, h, w), seed)
+    torch.manual_seed(seed + 1)
+    wt = torch.nn.Conv2d(4 * c, c, 3, 1, 1).weight.detach().float().to(DEV)
+    g = randn((n, c, h, w), seed + 2).to(DEV)
+    sep = _fuse_conv_bwd_calls(cat.to(DEV), wt, g, 0, False)
+    com = _fuse_conv_bwd_calls(_as_device_words(_pair_planes(cat)), wt, g, PAIRS, True)
+    for name, a, e in zip(("d cat", "d weight", "d bias"), com, sep):
+        assert not torch.isnan(e).any(), f"{name} {shape}"
+        assert torch.equal(a, e), f"{name} {shape}: max|diff| {(a - e).abs().max().item():.3e}"

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_host_only_queries():
     lib = _lib.load()
-    assert lib.ddpm_abi_version() == _lib.ABI_VERSION == 6
+    assert lib.ddpm_abi_version() == _lib.ABI_VERSION == 7
     assert b"invalid argument" in lib.ddpm_status_string(10001)
     assert lib.ddpm_gen_supported(64, 3, 5) == 1
     # up to 128 channels (four 32-channel K steps, 32-column tiles above 64)
