@@ -51,6 +51,9 @@ SIGNATURES: dict[str, tuple[list, type]] = {
     "ddpm_fuse_conv_bwd_weight_workspace_bytes": ([_L, _L, _L, _L, _I], _L),
     "ddpm_fuse_conv_bwd_weight": ([_P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _P], _I),
     "ddpm_fuse_conv_bwd": ([_P, _P, _P, _P, _P, _P, _P, _L, _P, _L, _L, _L, _L, _L, _I, _P], _I),
+    "ddpm_gen_fwd_pack": ([_P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P],
+                          _I),
+    "ddpm_fuse_conv_fwd_packed": ([_P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _P], _I),
     "ddpm_gen_bwd_w": ([_P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P], _I),
     "ddpm_gen_bwd_xw": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _P, _L, _L, _L, _L, _L, _I, _I, _I,
                          _I, _I, _P], _I),

@@ -190,4 +190,12 @@ int cw_run(const void* cat, const void* grad_out, void* grad_weight, void* grad_
            void* workspace, int64_t workspace_bytes, int64_t n, int64_t c, int64_t h, int64_t w,
            int dtype, hipStream_t stream, bool check_only, const CvPack* pack, CwReduce* defer);
 
+// The fuse convolution's forward weight packing as a descriptor for another
+// launch (defined in conv3x3.hip): validates the forward's shape (n, 4c -> c,
+// h, w; `dtype` the concat's code) and workspace (as for ddpm_fuse_conv_fwd),
+// and describes packing `weight` into the start of `workspace` in the layout
+// the forward over `cat` reads; total 0 for an empty shape.
+int cv_fwd_pack(CvPack& p, const void* cat, const void* weight, void* workspace,
+                int64_t workspace_bytes, int64_t n, int64_t c, int64_t h, int64_t w, int dtype);
+
 }  // namespace ddpm

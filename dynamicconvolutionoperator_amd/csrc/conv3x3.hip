@@ -721,6 +721,46 @@ extern "C" int ddpm_fuse_conv_fwd(const void* cat, const void* weight, const voi
                 stream, pairs);
 }
 
+int ddpm::cv_fwd_pack(CvPack& p, const void* cat, const void* weight, void* workspace,
+                      int64_t workspace_bytes, int64_t n, int64_t c, int64_t h, int64_t w,
+                      int dtype) {
+  p = CvPack{nullptr, nullptr, ConvGeom{}, 0, 0, 0, 0};
+  const bool pairs = dtype == kF32Pairs;
+  if (pairs) {
+    if (c % 8 != 0) return kUnsupported;
+    dtype = kF32;
+  }
+  int st = cv_check(n, 4 * c, c, h, w, dtype);
+  if (st != kOk) return st;
+  if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
+  if (!cat || !weight) return kBadArgument;
+  CvPlan plan;
+  cv_plan(plan, cat, n, 4 * c, c, h, w, dtype, pairs, false);
+  if (!workspace || workspace_bytes < cv_workspace_bytes(plan.g, dtype) ||
+      (uintptr_t)workspace % 16 != 0)
+    return kWorkspaceTooSmall;
+  p = CvPack{weight, (uint32_t*)workspace, plan.g, 0, pairs ? 1 : 0, plan.nat ? 1 : 0,
+             plan.g.mgroups * plan.g.nc32 * 9 * plan.g.mb * 64};
+  return kOk;
+}
+
+extern "C" int ddpm_fuse_conv_fwd_packed(const void* cat, const void* bias, void* out,
+                                         void* workspace, int64_t workspace_bytes, int64_t n,
+                                         int64_t c, int64_t h, int64_t w, int dtype,
+                                         hipStream_t stream) {
+  const bool pairs = dtype == kF32Pairs;
+  if (pairs) {
+    if (c % 8 != 0) return kUnsupported;
+    dtype = kF32;
+  }
+  int st = cv_check(n, 4 * c, c, h, w, dtype);
+  if (st != kOk) return st;
+  if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
+  if (!cat || !out) return kBadArgument;
+  return cv_run(cat, nullptr, bias, out, workspace, workspace_bytes, n, 4 * c, c, h, w, 0, dtype,
+                stream, pairs, nullptr, false);
+}
+
 extern "C" int ddpm_fuse_conv_bwd_data(const void* grad_out, const void* weight, void* grad_cat,
                                        void* workspace, int64_t workspace_bytes, int64_t n,
                                        int64_t c, int64_t h, int64_t w, int dtype,

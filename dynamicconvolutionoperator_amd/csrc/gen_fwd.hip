@@ -25,8 +25,8 @@ namespace ddpm {
 template <typename T, int KS, int NK, int CB, bool PP = false>
 __global__ __launch_bounds__(kGtThreads) __attribute__((amdgpu_waves_per_eu(gt_waves_per_eu<T, NK, CB>()))) void gen_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ wt,
-    const T* __restrict__ bias, T* __restrict__ out, TileGeom g) {
-  gen_tile_body<T, KS, NK, CB, false, PP>(x, y, wt, bias, out, nullptr, g);
+    const T* __restrict__ bias, T* __restrict__ out, TileGeom g, CvPack fpk) {
+  gen_tile_body<T, KS, NK, CB, false, PP>(x, y, wt, bias, out, nullptr, g, fpk);
 }
 
 // Two fp32 values rounded to nearest-even in T (bf16 / f16), packed low/high.
@@ -68,7 +68,7 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 template <typename T, int NK, int CB>
 __global__ __launch_bounds__(kGtThreads) __attribute__((amdgpu_waves_per_eu(gt_waves_per_eu<T, NK, CB>()))) void gen_fwd_pair_kernel(
     const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ wt,
-    const T* __restrict__ bias, T* __restrict__ out, TileGeom g) {
+    const T* __restrict__ bias, T* __restrict__ out, TileGeom g, CvPack fpk) {
   static_assert(sizeof(T) == 2, "2-byte types");
   typedef Mma<T> M;
   typedef typename M::V V;
@@ -139,6 +139,9 @@ __global__ __launch_bounds__(kGtThreads) __attribute__((amdgpu_waves_per_eu(gt_w
   V bfr[NBW][NK][1];
   gt_load_y<T, NK, CB>(y, bfr, g, n, h0, w0, wave, col16, quad);
   if (tid < NPS * 32) bs[tid] = gf_raw_to_f<T>(bv);
+  // ddpm_gen_fwd_pack: this workgroup's share of the fuse convolution's
+  // weight packing
+  if (fpk.total > 0) cv_pack_share<T>(fpk, (int)blockIdx.x, (int)gridDim.x, tid, kGtThreads);
   __builtin_amdgcn_s_waitcnt(0);  // the LDS-direct weight copies
   __syncthreads();
 
@@ -273,9 +276,14 @@ int gen_make_geom(GenGeom& g, int64_t n, int64_t c, int64_t h, int64_t w, int k,
 
 using namespace ddpm;
 
-extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, const void* bias,
-                            void* out, int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size,
-                            int d0, int d1, int d2, int dtype, hipStream_t stream) {
+namespace {
+
+// ddpm_gen_fwd's work; fpk (optional): a fuse-convolution weight packing for
+// the kernel's workgroups to run.  check_only: validate and return before
+// launching.
+int gf_run(const void* x, const void* y, const void* weight, const void* bias, void* out,
+           int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size, int d0, int d1, int d2,
+           int dtype, hipStream_t stream, const CvPack* fpk, bool check_only) {
   // kF32Pairs: fp32 inputs, the concat written as pair planes (C % 16 == 0)
   const bool pp = dtype == kF32Pairs;
   if (pp) {
@@ -288,7 +296,9 @@ extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, co
   if (st != kOk) return st;
   if (n == 0 || c == 0 || h == 0 || w == 0) return kOk;
   if (!x || !y || !weight || !bias || !out) return kBadArgument;
+  if (check_only) return kOk;
   const int esz = dtype == kF32 ? 4 : 2;
+  const CvPack pk = fpk ? *fpk : CvPack{nullptr, nullptr, ConvGeom{}, 0, 0, 0, 0};
   // 32-bit buffer offsets inside one image's [C][H][W] planes (and 16 planes
   // past a channel block's first one)
   if (c * h * w * esz > 0x7fffffffLL || 16 * h * w * esz > 0x7fffffffLL) return kUnsupported;
@@ -313,7 +323,7 @@ extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, co
           if (ae != 0) return ae;
           hipLaunchKernelGGL(kern, dim3((unsigned)((int64_t)g.N * g.tiles * g.cblocks)),
                              dim3(kGtThreads), lds_pair, stream, (const T*)x, (const T*)y,
-                             (const T*)weight, (const T*)bias, (T*)out, g);
+                             (const T*)weight, (const T*)bias, (T*)out, g, pk);
           return (int)hipGetLastError();
         };
         if (cb == 4) return nk == 1 ? launch(gen_fwd_pair_kernel<T, 1, 4>) : launch(gen_fwd_pair_kernel<T, 2, 4>);
@@ -331,7 +341,7 @@ extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, co
       if (ae != 0) return ae;
       hipLaunchKernelGGL(kern, dim3((unsigned)((int64_t)g.N * g.tiles * g.cblocks)),
                          dim3(kGtThreads), lds, stream, (const T*)x, (const T*)y,
-                         (const T*)weight, (const T*)bias, (T*)out, g);
+                         (const T*)weight, (const T*)bias, (T*)out, g, pk);
       return (int)hipGetLastError();
     };
     // 1 or 2 chunks of 32 input channels, or 4 (65..128 channels; chunks
@@ -355,4 +365,29 @@ extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, co
     };
     return pp ? by_k(std::true_type()) : by_k(std::false_type());
   });
+}
+
+}  // namespace
+
+extern "C" int ddpm_gen_fwd(const void* x, const void* y, const void* weight, const void* bias,
+                            void* out, int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size,
+                            int d0, int d1, int d2, int dtype, hipStream_t stream) {
+  return gf_run(x, y, weight, bias, out, n, c, h, w, kernel_size, d0, d1, d2, dtype, stream,
+                nullptr, false);
+}
+
+extern "C" int ddpm_gen_fwd_pack(const void* x, const void* y, const void* weight,
+                                 const void* bias, void* out, const void* fuse_weight,
+                                 void* fuse_workspace, int64_t fuse_workspace_bytes, int64_t n,
+                                 int64_t c, int64_t h, int64_t w, int kernel_size, int d0, int d1,
+                                 int d2, int dtype, hipStream_t stream) {
+  // both parts validated before anything is launched
+  int st = gf_run(x, y, weight, bias, out, n, c, h, w, kernel_size, d0, d1, d2, dtype, stream,
+                  nullptr, true);
+  if (st != kOk) return st;
+  CvPack pk;
+  st = cv_fwd_pack(pk, out, fuse_weight, fuse_workspace, fuse_workspace_bytes, n, c, h, w, dtype);
+  if (st != kOk) return st;
+  return gf_run(x, y, weight, bias, out, n, c, h, w, kernel_size, d0, d1, d2, dtype, stream, &pk,
+                false);
 }

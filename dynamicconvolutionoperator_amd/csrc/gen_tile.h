@@ -31,7 +31,7 @@
 // dropped) instead of a branch.
 #pragma once
 
-#include "gen_common.h"
+#include "conv3x3.h"
 
 namespace ddpm {
 
@@ -375,7 +375,9 @@ template <typename T, int KS, int NK, int CB, bool BX, bool PP = false>
 __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* __restrict__ y,
                                               const T* __restrict__ wt, const T* __restrict__ bias,
                                               T* __restrict__ out, float* __restrict__ part,
-                                              const TileGeom& g) {
+                                              const TileGeom& g,
+                                              CvPack fpk = CvPack{nullptr, nullptr, ConvGeom{}, 0,
+                                                                  0, 0, 0}) {
   typedef Mma<T> M;
   typedef typename M::V V;
   constexpr int P = M::P;
@@ -493,6 +495,9 @@ __device__ __forceinline__ void gen_tile_body(const T* __restrict__ a, const T* 
     bias_put();
     wput(0);
     if (NBT > 1) wload(1);
+    // ddpm_gen_fwd_pack: this workgroup's share of the fuse convolution's
+    // weight packing
+    if (fpk.total > 0) cv_pack_share<T>(fpk, (int)blockIdx.x, (int)gridDim.x, tid, kGtThreads);
   }
   __syncthreads();
 

@@ -21,10 +21,11 @@ another ``padding_mode``, a replaced module -- is honoured by calling
 ``fuse_conv_backend = "library"`` selects MIOpen through ``self.fuse`` always.
 The materialized route likewise calls ``self.generator(y)`` unless the
 generator is the constructor's unmodified 1x1 convolution
-(triton_impl.py:340-347).  For fp32 on the fused route with C % 16 == 0,
-generator, filter, concat and fuse convolution run as one pair of autograd
-ops (``ops.fused_ddpm``) whose concat is stored as bf16 pair planes, already
-split the way the fuse convolution's fp32 MFMA products need it.
+(triton_impl.py:340-347).  On the fused route with the HIP fuse
+convolution, generator, filter, concat and fuse convolution run as one pair
+of autograd ops (``ops.fused_ddpm``) whose generator launch also packs the
+fuse weight; an fp32 concat (C % 16 == 0) is stored as bf16 pair planes,
+already split the way the fuse convolution's fp32 MFMA products need it.
 """
 
 from __future__ import annotations
@@ -235,11 +236,11 @@ class DDPM(nn.Module):
         return self.fuse(cat_out)
 
     def _cuda_pairs(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor | None:
-        """fp32 on the fused route with the HIP fuse convolution: generator,
-        filter, concat and fuse convolution as one pair of ops whose concat is
-        stored as bf16 pair planes (``ops.fused_ddpm``); ``None`` where it
-        does not apply."""
-        if x.dtype != torch.float32 or not self._hip_fuse():
+        """The fused route with the HIP fuse convolution: generator, filter,
+        concat and fuse convolution as one pair of ops (``ops.fused_ddpm``:
+        the generator's launch also packs the fuse weight; an fp32 concat is
+        stored as bf16 pair planes); ``None`` where it does not apply."""
+        if not self._hip_fuse():
             return None
         ops = _load_hip_ops()
         fused_ddpm, supported = ops[5], ops[6]

@@ -632,16 +632,18 @@ def fuse_conv3x3(cat, weight, bias=None):
 # ---------------------------------------------------------------------------
 def fused_ddpm_supported(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, kernel_size,
                          dilations) -> bool:
-    """Whether :func:`fused_ddpm` takes this call: fp32 throughout, a ROCm
-    device, the fused generator kernels' coverage (:func:`generator_supported`;
-    the forward's alone when no gradient is needed),
-    C % 16 == 0 (whole 32-plane chunks of the concat), the HIP fuse
-    convolution's coverage and weight shapes of DDPM(C, K)."""
-    if x.dtype != torch.float32 or x.ndim != 4 or not x.is_cuda:
+    """Whether :func:`fused_ddpm` takes this call: one dtype (fp32, bf16 or
+    fp16) throughout, a ROCm device, the fused generator kernels' coverage
+    (:func:`generator_supported`; the forward's alone when no gradient is
+    needed), for fp32 C % 16 == 0 (whole 32-plane chunks of the pair-plane
+    concat), the HIP fuse convolution's coverage and weight shapes of
+    DDPM(C, K)."""
+    if x.dtype not in _DTYPES or x.ndim != 4 or not x.is_cuda:
         return False
     n, c, h, w = x.shape
     k = int(kernel_size)
-    if c % 16 != 0 or tuple(y.shape) != tuple(x.shape) or y.device != x.device:
+    if (x.dtype == torch.float32 and c % 16 != 0) or tuple(y.shape) != tuple(x.shape) \
+            or y.device != x.device:
         return False
     g = 3 * c * k * k
     if gen_bias is None or tuple(gen_weight.shape) != (g, c, 1, 1) or tuple(gen_bias.shape) != (g,):
@@ -651,59 +653,88 @@ def fused_ddpm_supported(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, ker
     if fuse_bias is not None and tuple(fuse_bias.shape) != (c,):
         return False
     tensors = (y, gen_weight, gen_bias, fuse_weight, fuse_bias)
-    if any(t is not None and (t.dtype != torch.float32 or t.device != x.device) for t in tensors):
+    if any(t is not None and (t.dtype != x.dtype or t.device != x.device) for t in tensors):
         return False
     needs_grad = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (x, *tensors))
     if not generator_supported(c, k, dilations, x.shape, x.dtype, forward_only=not needs_grad):
         return False
-    return 4 * c * h * w * 4 <= 2**31 - 1
+    return 4 * c * h * w * x.element_size() <= 2**31 - 1
 
 
-def _pair_concat(x, y, gen_weight, gen_bias, k, dil):
-    """ddpm_gen_fwd writing the concat as pair planes (dtype code 3)."""
+def _cat_code(dtype: torch.dtype) -> int:
+    """The concat's dtype code on the fused_ddpm route: fp32 pair planes, else
+    the plain dtype."""
+    return _PAIR_PLANES if dtype == torch.float32 else _DTYPES[dtype]
+
+
+def _concat_pack(x, y, gen_weight, gen_bias, fuse_weight, k, dil):
+    """ddpm_gen_fwd_pack: the concat (fp32 as pair planes) and, in the fuse
+    convolution's workspace, its packed weight (returned with it)."""
     n, c, h, w = x.shape
-    cat = torch.empty((n, 4 * c, h, w), dtype=torch.float32, device=x.device)
+    code = _cat_code(x.dtype)
+    cat = torch.empty((n, 4 * c, h, w), dtype=x.dtype, device=x.device)
     lib = _lib.load()
     with _on(x.device):
-        code = lib.ddpm_gen_fwd(_ptr(x), _ptr(y), _ptr(gen_weight), _ptr(gen_bias), _ptr(cat),
-                                n, c, h, w, k, *dil, _PAIR_PLANES, _stream(x))
-    _lib.check(code, "ddpm_gen_fwd")
-    return cat
+        ws, nbytes = _fuse_conv_workspace(n, c, h, w, code, x.device)
+        rc = lib.ddpm_gen_fwd_pack(_ptr(x), _ptr(y), _ptr(gen_weight), _ptr(gen_bias), _ptr(cat),
+                                   _ptr(fuse_weight), _ptr(ws), nbytes, n, c, h, w, k, *dil, code,
+                                   _stream(x))
+    _lib.check(rc, "ddpm_gen_fwd_pack")
+    return cat, ws
 
 
-class _PairConcat(torch.autograd.Function):
-    """Generator + filter + concat with the fp32 concat written as pair
-    planes.  The output is an encoding only :class:`_PairFuse` reads; the
-    gradient arriving for it is the plain fp32 gradient of the concat values,
-    so the backward is the generator op's (recompute from x, y, W, b)."""
+def _fuse_conv_forward_packed(cat, ws, fuse_bias):
+    """ddpm_fuse_conv_fwd_packed over a concat of :func:`_concat_pack` whose
+    workspace ``ws`` holds the packed weight."""
+    n, ci, h, w = cat.shape
+    c = ci // 4
+    out = torch.empty((n, c, h, w), dtype=cat.dtype, device=cat.device)
+    lib = _lib.load()
+    with _on(cat.device):
+        rc = lib.ddpm_fuse_conv_fwd_packed(_ptr(cat), _ptr(fuse_bias) if fuse_bias is not None else None,
+                                           _ptr(out), _ptr(ws), ws.numel(), n, c, h, w,
+                                           _cat_code(cat.dtype), _stream(cat))
+    _lib.check(rc, "ddpm_fuse_conv_fwd_packed")
+    return out
+
+
+class _GeneratorConcat(torch.autograd.Function):
+    """Generator + filter + concat, an fp32 concat written as pair planes
+    (an encoding only :class:`_FuseConvOfConcat` reads; the gradient arriving
+    for it is the plain fp32 gradient of the concat values), so the backward
+    is the generator op's (recompute from x, y, W, b).  The same launch packs
+    the fuse convolution's weight into the forward workspace it returns
+    beside the concat (no gradient)."""
 
     @staticmethod
-    def forward(ctx, x, y, gen_weight, gen_bias, kernel_size, dilations):
-        cat = _pair_concat(x, y, gen_weight, gen_bias, kernel_size, dilations)
+    def forward(ctx, x, y, gen_weight, gen_bias, fuse_weight, kernel_size, dilations):
+        cat, ws = _concat_pack(x, y, gen_weight, gen_bias, fuse_weight, kernel_size, dilations)
         ctx.save_for_backward(x, y, gen_weight, gen_bias)
         ctx.kernel_size = kernel_size
         ctx.dilations = dilations
-        return cat
+        ctx.mark_non_differentiable(ws)
+        return cat, ws
 
     @staticmethod
-    def backward(ctx, grad_cat):
+    def backward(ctx, grad_cat, grad_ws):
         x, y, gen_weight, gen_bias = ctx.saved_tensors
-        grads = _generator_backward(x, y, gen_weight, gen_bias, _as(grad_cat, torch.float32),
+        grads = _generator_backward(x, y, gen_weight, gen_bias, _as(grad_cat, x.dtype),
                                     ctx.kernel_size, ctx.dilations, ctx.needs_input_grad[:4])
-        return (*grads, None, None)
+        return (*grads, None, None, None)
 
 
-class _PairFuse(torch.autograd.Function):
-    """The fuse convolution of a pair-plane concat: forward and weight / bias
-    gradients read the pair planes; the input gradient is a plain fp32
-    concat gradient.  A node of its own, so autograd releases the saved
-    concat as soon as this backward has run, before the generator's
-    backward allocates its buffers."""
+class _FuseConvOfConcat(torch.autograd.Function):
+    """The fuse convolution of a :class:`_GeneratorConcat` concat (fp32:
+    forward and weight / bias gradients read the pair planes; the input
+    gradient is a plain fp32 concat gradient).  A node of its own, so
+    autograd releases the saved concat as soon as this backward has run,
+    before the generator's backward allocates its buffers."""
 
     @staticmethod
-    def forward(ctx, cat, fuse_weight, fuse_bias):
-        out = _fuse_conv_forward(cat, fuse_weight, fuse_bias, _PAIR_PLANES)
+    def forward(ctx, cat, ws, fuse_weight, fuse_bias):
+        # ws: the forward's workspace, holding the packed weight (_GeneratorConcat)
+        out = _fuse_conv_forward_packed(cat, ws, fuse_bias)
         ctx.save_for_backward(cat, fuse_weight)
         ctx.has_bias = fuse_bias is not None
         return out
@@ -711,16 +742,19 @@ class _PairFuse(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         cat, fuse_weight = ctx.saved_tensors
-        return _fuse_conv_backward(cat, fuse_weight, ctx.has_bias,
-                                   _as(grad_out, torch.float32), ctx.needs_input_grad,
-                                   _PAIR_PLANES)
+        grads = _fuse_conv_backward(cat, fuse_weight, ctx.has_bias, _as(grad_out, cat.dtype),
+                                    (ctx.needs_input_grad[0], *ctx.needs_input_grad[2:]),
+                                    _cat_code(cat.dtype))
+        return grads[0], None, grads[1], grads[2]
 
 
 def fused_ddpm(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, kernel_size, dilations):
     """``fuse_conv3x3(fused_generator_dynamic_cat(x, y, ...), fuse_weight,
-    fuse_bias)`` for fp32 shapes of :func:`fused_ddpm_supported`, with the
-    concat kept in pair planes between the two (the result differs from the
-    separate ops only by the fuse convolution's summation order)."""
+    fuse_bias)`` for shapes of :func:`fused_ddpm_supported`, the generator's
+    launch also packing the fuse convolution's weight.  fp32 keeps the concat
+    in pair planes between the two (the result differs from the separate ops
+    only by the fuse convolution's summation order); bf16 / fp16 give the
+    separate ops' results bit for bit."""
     k = _check_kernel_size(kernel_size)
     dil = _check_dilations(dilations)
     if not fused_ddpm_supported(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, k, dil):
@@ -737,10 +771,10 @@ def _fused_ddpm_checked(x, y, gen_weight, gen_bias, fuse_weight, fuse_bias, k, d
     fuse_bias = fuse_bias.contiguous() if fuse_bias is not None else None
     tensors = (x, y, gen_weight, gen_bias, fuse_weight, fuse_bias)
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
-        cat = _PairConcat.apply(x, y, gen_weight, gen_bias, k, dil)
-        return _PairFuse.apply(cat, fuse_weight, fuse_bias)
-    cat = _pair_concat(x, y, gen_weight, gen_bias, k, dil)
-    return _fuse_conv_forward(cat, fuse_weight, fuse_bias, _PAIR_PLANES)
+        cat, ws = _GeneratorConcat.apply(x, y, gen_weight, gen_bias, fuse_weight, k, dil)
+        return _FuseConvOfConcat.apply(cat, ws, fuse_weight, fuse_bias)
+    cat, ws = _concat_pack(x, y, gen_weight, gen_bias, fuse_weight, k, dil)
+    return _fuse_conv_forward_packed(cat, ws, fuse_bias)
 
 
 __all__ = [

@@ -47,7 +47,8 @@ extern "C" {
 #define DDPM_DTYPE_F16 2
 
 /* ABI version of this header (5: dtype code 3; 6: ddpm_gen_fwd at K = 5 and
- * ddpm_gen_fwd_supported; 7: ddpm_fuse_conv_bwd). */
+ * ddpm_gen_fwd_supported; 7: ddpm_fuse_conv_bwd, ddpm_gen_fwd_pack and
+ * ddpm_fuse_conv_fwd_packed). */
 int ddpm_abi_version(void);
 
 /* Text for any status code returned by this library (static storage). */
@@ -272,6 +273,27 @@ int64_t ddpm_fuse_conv_workspace_bytes(int64_t n, int64_t c, int64_t h, int64_t 
 int ddpm_fuse_conv_fwd(const void* cat, const void* weight, const void* bias, void* out,
                        void* workspace, int64_t workspace_bytes, int64_t n, int64_t c, int64_t h,
                        int64_t w, int dtype, hipStream_t stream);
+
+/* ddpm_gen_fwd writing the concat `out`, whose workgroups also pack the fuse
+ * convolution's weight (fuse_weight: [c][4c][3][3] in the concat's element
+ * type) into the start of fuse_workspace (ddpm_fuse_conv_workspace_bytes for
+ * `dtype`) in the layout ddpm_fuse_conv_fwd reads over `out`; then
+ * ddpm_fuse_conv_fwd_packed on the same concat and workspace is
+ * ddpm_fuse_conv_fwd, bit for bit, without its packing launch.  Both parts
+ * are validated before anything is launched.  No reference counterpart of
+ * its own: the generator launch of _launch_generator_dynamic_cat
+ * (_triton_kernels.py:873-908) followed by the forward of self.fuse
+ * (triton_impl.py:392), with one launch fewer. */
+int ddpm_gen_fwd_pack(const void* x, const void* y, const void* weight, const void* bias, void* out,
+                      const void* fuse_weight, void* fuse_workspace, int64_t fuse_workspace_bytes,
+                      int64_t n, int64_t c, int64_t h, int64_t w, int kernel_size, int d0, int d1,
+                      int d2, int dtype, hipStream_t stream);
+
+/* ddpm_fuse_conv_fwd whose workspace already holds the packed weight that
+ * ddpm_gen_fwd_pack wrote for this concat (same shape, dtype and buffer). */
+int ddpm_fuse_conv_fwd_packed(const void* cat, const void* bias, void* out, void* workspace,
+                              int64_t workspace_bytes, int64_t n, int64_t c, int64_t h, int64_t w,
+                              int dtype, hipStream_t stream);
 
 /* grad_cat[n][ci][h][w] = sum_{co,ki,kj} weight[co][ci][ki][kj] *
  *                         grad_out[n][co][h-ki+1][w-kj+1]  (zero outside the image).

@@ -160,18 +160,22 @@ def test_fuse_conv_reads_pair_planes(shape):
 FUSED_CASES = [((1, 64, 64, 64), 3), ((2, 16, 20, 36), 3), ((1, 48, 15, 17), 3), ((1, 32, 40, 56), 1)]
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shape,k", FUSED_CASES)
-def test_fused_ddpm_matches_the_separate_ops(shape, k):
-    say(f"fused_ddpm shape={shape} K={k}")
+def test_fused_ddpm_matches_the_separate_ops(shape, k, dtype):
+    """fp32 (pair-plane concat): the output within the fuse convolution's
+    tolerance, every gradient bit-identical; bf16 (plain concat, the same
+    kernels as the separate ops): the output too bit-identical."""
+    say(f"fused_ddpm shape={shape} K={k} dtype={dtype}")
     n, c, h, w = shape
     seed = 1700 + c + w
-    x0 = randn(shape, seed)
-    y0 = randn(shape, seed + 1)
-    gw0, gb0 = default_generator_params(c, k, seed + 2, torch.float32)
+    x0 = randn(shape, seed).to(dtype)
+    y0 = randn(shape, seed + 1).to(dtype)
+    gw0, gb0 = default_generator_params(c, k, seed + 2, dtype)
     torch.manual_seed(seed + 3)
     conv = torch.nn.Conv2d(4 * c, c, 3, 1, 1)
-    fw0, fb0 = conv.weight.detach().float(), conv.bias.detach().float()
-    gout = randn((n, c, h, w), seed + 4).to(DEV)
+    fw0, fb0 = conv.weight.detach().to(dtype), conv.bias.detach().to(dtype)
+    gout = randn((n, c, h, w), seed + 4).to(dtype).to(DEV)
     runs = []
     for fused in (False, True):
         leaves = [t.to(DEV).requires_grad_() for t in (x0, y0, gw0, gb0, fw0, fb0)]
@@ -185,8 +189,11 @@ def test_fused_ddpm_matches_the_separate_ops(shape, k):
         torch.cuda.synchronize()
         runs.append((out.detach(), grads))
     (o_sep, g_sep), (o_fused, g_fused) = runs
-    scale = o_sep.abs().max().item()
-    assert_close(o_fused, o_sep, FP32_CONV_TOL * scale, FP32_CONV_TOL, f"out {shape}")
+    if dtype == torch.float32:
+        scale = o_sep.abs().max().item()
+        assert_close(o_fused, o_sep, FP32_CONV_TOL * scale, FP32_CONV_TOL, f"out {shape}")
+    else:
+        assert torch.equal(o_fused, o_sep), f"out {shape} {dtype}"
     names = ("dx", "dy", "d gen weight", "d gen bias", "d fuse weight", "d fuse bias")
     for name, a, e in zip(names, g_fused, g_sep):
         assert torch.equal(a, e), f"{name} {shape}: max|diff| {(a - e).abs().max().item():.3e}"
@@ -238,3 +245,62 @@ def test_fuse_conv_combined_backward_reads_pair_planes(shape):
     for name, a, e in zip(("d cat", "d weight", "d bias"), com, sep):
         assert not torch.isnan(e).any(), f"{name} {shape}"
         assert torch.equal(a, e), f"{name} {shape}: max|diff| {(a - e).abs().max().item():.3e}"
+
+
+def _gen_fwd_conv(x, y, gw, gb, fw, fb, k, code, packed):
+    """The concat and the fuse convolution's output through the C-ABI:
+    ddpm_gen_fwd + ddpm_fuse_conv_fwd, or ddpm_gen_fwd_pack +
+    ddpm_fuse_conv_fwd_packed (outputs and workspace started as NaN / 0xff)."""
+    lib = _lib.load()
+    n, c, h, w = x.shape
+    cat = torch.full((n, 4 * c, h, w), float("nan"), dtype=x.dtype, device=DEV)
+    out = torch.full((n, c, h, w), float("nan"), dtype=x.dtype, device=DEV)
+    nb = int(lib.ddpm_fuse_conv_workspace_bytes(n, c, h, w, code))
+    ws = torch.full((max(nb, 16),), 255, dtype=torch.uint8, device=DEV)
+    if packed:
+        rc = lib.ddpm_gen_fwd_pack(_ptr(x), _ptr(y), _ptr(gw), _ptr(gb), _ptr(cat), _ptr(fw), _ptr(ws), nb,
+                                   n, c, h, w, k, *DIL, code, _stream())
+        assert rc == 0, rc
+        rc = lib.ddpm_fuse_conv_fwd_packed(_ptr(cat), _ptr(fb), _ptr(out), _ptr(ws), nb, n, c, h, w, code,
+                                           _stream())
+        assert rc == 0, rc
+    else:
+        rc = lib.ddpm_gen_fwd(_ptr(x), _ptr(y), _ptr(gw), _ptr(gb), _ptr(cat), n, c, h, w, k, *DIL, code,
+                              _stream())
+        assert rc == 0, rc
+        rc = lib.ddpm_fuse_conv_fwd(_ptr(cat), _ptr(fw), _ptr(fb), _ptr(out), _ptr(ws), nb, n, c, h, w, code,
+                                    _stream())
+        assert rc == 0, rc
+    torch.cuda.synchronize()
+    return cat, out
+
+
+@pytest.mark.parametrize("code", [0, 1, 2, PAIRS])
+@pytest.mark.parametrize("shape,k", [((1, 64, 256, 256), 3), ((1, 64, 128, 128), 3), ((2, 16, 20, 36), 3),
+                                     ((1, 48, 15, 17), 1), ((1, 32, 40, 56), 5), ((1, 128, 32, 64), 3)])
+def test_gen_fwd_pack_is_gen_fwd_then_fuse_conv_fwd(shape, k, code):
+    """ddpm_gen_fwd_pack (the generator's workgroups packing the fuse
+    convolution's weight) + ddpm_fuse_conv_fwd_packed: concat and output bit
+    for bit those of ddpm_gen_fwd + ddpm_fuse_conv_fwd, in every dtype code
+    (2-byte K = 3 at C <= 64: the tap-pair generator kernel), with the 128x128
+    forward's input-plane splits, element-wise rows and C = 128."""
+    n, c, h, w = shape
+    if code == PAIRS and c % 16 != 0:
+        pytest.skip("pair planes need C % 16 == 0")
+    say(f"gen_fwd_pack shape={shape} k={k} code={code}")
+    dt = {0: torch.float32, 1: torch.bfloat16, 2: torch.float16, PAIRS: torch.float32}[code]
+    x = randn(shape, 1800 + c + w)
+    y = randn(shape, 1801 + c + w)
+    gw, gb = default_generator_params(c, k, 1802 + c, torch.float32)
+    torch.manual_seed(1803 + c)
+    conv = torch.nn.Conv2d(4 * c, c, 3, 1, 1)
+    x, y, gw, gb, fw, fb = (t.detach().to(dt).to(DEV).contiguous()
+                            for t in (x, y, gw, gb, conv.weight, conv.bias))
+    a = _gen_fwd_conv(x, y, gw, gb, fw, fb, k, code, False)
+    b = _gen_fwd_conv(x, y, gw, gb, fw, fb, k, code, True)
+    for name, u, v in zip(("concat", "out"), b, a):
+        if code == PAIRS and name == "concat":
+            u, v = _words(u), _words(v)
+        else:
+            assert not torch.isnan(v).any(), f"{name} {shape}"
+        assert torch.equal(u, v), f"{name} {shape} k={k} code={code}"

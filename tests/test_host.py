@@ -143,9 +143,10 @@ def test_entry_points_validate_arguments_before_touching_the_device():
     assert lib.ddpm_filter_fwd(null, null, null, 1, 1, 4, 4, 3, 1, 3, 5, 3, 3, null) == 10001
 
 
-def test_fused_ddpm_takes_rocm_fp32_only():
-    """ops.fused_ddpm (the module's fp32 pair-plane route) is refused for CPU
-    tensors and other dtypes; the module's CPU branch never reaches it."""
+def test_fused_ddpm_takes_rocm_tensors_of_one_dtype_only():
+    """ops.fused_ddpm (the module's fused route with the HIP fuse
+    convolution) is refused for CPU tensors and mixed dtypes; the module's
+    CPU branch never reaches it."""
     from dynamicconvolutionoperator_amd import ops
 
     c, k = 16, 3
