@@ -283,6 +283,14 @@ class LaunchTimer:
         return {n: len(r) for n, r in self.records.items() if r}
 
 
+def timed_entry_points(signatures):
+    """The C-ABI entry points the step breakdown times (launching ones, not
+    the queries)."""
+    names = [n for n in signatures
+             if n.startswith(("ddpm_gen_fwd", "ddpm_gen_bwd", "ddpm_filter_", "ddpm_gen_kernels", "ddpm_fuse_conv"))]
+    return [n for n in names if not n.endswith(("_workspace_bytes", "_supported", "_scratch_bytes"))]
+
+
 def work_per_launch(name, esize):
     """Algorithmic work of one launch at the headline shape: (bytes, flops)."""
     E = B * C * H * W
@@ -302,6 +310,12 @@ def work_per_launch(name, esize):
         "ddpm_fuse_conv_fwd": ((5 * E + 36 * C * C) * esize, conv),  # cat (4E) in, out (E)
         "ddpm_fuse_conv_bwd_data": ((5 * E + 36 * C * C) * esize, conv),  # gO (E) in, d cat (4E)
         "ddpm_fuse_conv_bwd_weight": ((5 * E + 36 * C * C) * esize, conv),  # cat, gO in
+        # input, weight and bias gradients in one call: gO (E), cat (4E) in, d cat (4E) out
+        "ddpm_fuse_conv_bwd": ((9 * E + 72 * C * C) * esize, 2 * conv),
+        # the generator launch that also packs the fuse weight, and the
+        # forward that reads that packing: as the unpacked calls
+        "ddpm_gen_fwd_pack": ((6 * E + G * (C + 1) + 36 * C * C) * esize, gemm),
+        "ddpm_fuse_conv_fwd_packed": ((5 * E + 36 * C * C) * esize, conv),
         "ddpm_filter_fwd": ((3 * K * K + 5) * E * esize, 0.0),
         "ddpm_filter_bwd_x": ((3 * K * K + 5) * E * esize, 0.0),
         "ddpm_filter_bwd_k": ((3 * K * K + 4) * E * esize, 0.0),
@@ -654,29 +668,34 @@ def make_calls(lib, dt, k, hw, nsets):
     return calls, sets
 
 
-def standalone_ms(lib, names, dt, reps=20):
-    """Mean ms per launch of each named entry point launched alone at the
-    headline shape (HIP events around `reps` launches, two input sets)."""
+def standalone_ms(lib, names, dt, reps=20, rounds=5):
+    """ms per launch of each named entry point launched alone at the
+    headline shape: HIP events around `reps` launches (two input sets), the
+    median of `rounds` such rounds with the names taken in turn."""
+    import statistics
+
     import torch
 
     calls, sets = make_calls(lib, dt, K, H, 2)
-    res = {}
+    times = {name: [] for name in names}
     for name in names:
         for i in range(2):
             calls[name](sets[i])
-        torch.cuda.synchronize()
-        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0.record()
-        for i in range(reps):
-            rc = calls[name](sets[i % 2])
-            if rc:
-                raise RuntimeError(f"{name} failed with status {rc}")
-        t1.record()
-        torch.cuda.synchronize()
-        res[name] = t0.elapsed_time(t1) / reps
+    for _ in range(rounds):
+        for name in names:
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for i in range(reps):
+                rc = calls[name](sets[i % 2])
+                if rc:
+                    raise RuntimeError(f"{name} failed with status {rc}")
+            t1.record()
+            torch.cuda.synchronize()
+            times[name].append(t0.elapsed_time(t1) / reps)
     del calls, sets
     torch.cuda.empty_cache()
-    return res
+    return {name: statistics.median(v) for name, v in times.items()}
 
 
 def kernel_mode(args):
@@ -791,8 +810,7 @@ def main():
     from dynamicconvolutionoperator_amd import _lib
 
     lib = _lib.load()
-    entries = [n for n in _lib.SIGNATURES if n.startswith(("ddpm_gen_fwd", "ddpm_gen_bwd", "ddpm_filter_", "ddpm_gen_kernels", "ddpm_fuse_conv"))]
-    entries = [n for n in entries if not n.endswith(("_workspace_bytes", "_supported", "_scratch_bytes"))]
+    entries = timed_entry_points(_lib.SIGNATURES)
     extra["clock_settle_ms"] = settle_gpu_clocks()
 
     if not args.quick:
@@ -939,14 +957,17 @@ def main():
     timer.close()
     cands = {n: v["share_of_step_ms"] for n, v in kernels.items()}
     combined = {"ddpm_gen_bwd": ("ddpm_gen_bwd_x", "ddpm_gen_bwd_y", "ddpm_gen_bwd_w"),
-                "ddpm_gen_bwd_xw": ("ddpm_gen_bwd_x", "ddpm_gen_bwd_w")}
+                "ddpm_gen_bwd_xw": ("ddpm_gen_bwd_x", "ddpm_gen_bwd_w"),
+                "ddpm_fuse_conv_bwd": ("ddpm_fuse_conv_bwd_data", "ddpm_fuse_conv_bwd_weight"),
+                "ddpm_gen_fwd_pack": ("ddpm_gen_fwd",),
+                "ddpm_fuse_conv_fwd_packed": ("ddpm_fuse_conv_fwd",)}
     for name, parts in combined.items():
         if name in cands:
-            # the step runs these GEMMs as one call (small pieces of them on
-            # the CUs dW leaves free): the roofline takes its GEMM entry points
+            # the step runs these GEMMs as one call (small pieces of them in
+            # the other's launch): the roofline takes its GEMM entry points
             # timed alone at the same shape
             alone = standalone_ms(lib, parts, torch.float32)
-            extra["standalone_fp32_ms"] = alone
+            extra.setdefault("standalone_fp32_ms", {}).update(alone)
             cands.pop(name)
             cands.update(alone)
     dominant = max(cands, key=cands.get)

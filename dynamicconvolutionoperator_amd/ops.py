@@ -714,10 +714,14 @@ class _GeneratorConcat(torch.autograd.Function):
         ctx.kernel_size = kernel_size
         ctx.dilations = dilations
         ctx.mark_non_differentiable(ws)
+        # no zero-filled gradient for the workspace output (a fill kernel per step)
+        ctx.set_materialize_grads(False)
         return cat, ws
 
     @staticmethod
     def backward(ctx, grad_cat, grad_ws):
+        if grad_cat is None:
+            return (None,) * 7
         x, y, gen_weight, gen_bias = ctx.saved_tensors
         grads = _generator_backward(x, y, gen_weight, gen_bias, _as(grad_cat, x.dtype),
                                     ctx.kernel_size, ctx.dilations, ctx.needs_input_grad[:4])

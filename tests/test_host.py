@@ -328,3 +328,20 @@ def test_plain_conv_guard():
     assert not module.plain_conv(m.generator, 1)
     assert not module.plain_conv(nn.Conv2d(8, 216, 3, padding=1), 1)
     assert module.plain_conv(nn.Conv2d(8, 216, 1), 1)
+
+
+def test_bench_prices_every_step_entry_point():
+    """bench.py's roofline can pick any fused-route entry point the training
+    step calls: each has its algorithmic bytes and flops (the materialized
+    route's are priced only where bench times them alone)."""
+    import sys
+
+    sys.path.insert(0, ROOT)
+    import bench
+
+    step = [n for n in bench.timed_entry_points(_lib.SIGNATURES)
+            if not n.startswith(("ddpm_gen_kernels", "ddpm_gen_bwd_y_noalloc"))]
+    assert "ddpm_fuse_conv_bwd" in step and "ddpm_gen_fwd_pack" in step
+    for name in step:
+        nbytes, flops = bench.work_per_launch(name, 4)
+        assert nbytes > 0, name
